@@ -1,0 +1,144 @@
+/*
+ * pope_abi.h -- C ABI of libpope_hip.so, the MI355X (gfx950) PoPE attention path.
+ *
+ * This is the drop-in boundary below the reference's Python operator layer.
+ * Each entry point replaces one launch wrapper of lucidrains/PoPE-pytorch
+ * (cited per function).  The Python host layer (pope_amd/hip_pope.py and
+ * pope_amd/hip_pope_flash_attn.py) binds these with ctypes and registers them
+ * as torch.library ops with autograd.
+ *
+ * Conventions
+ *   - All tensor pointers are DEVICE pointers owned by the caller.  The library
+ *     never allocates or frees device memory: scratch space is a caller-owned
+ *     workspace whose size pope_workspace_bytes() reports.
+ *   - Every entry point returns POPE_OK (0) or a nonzero status; the message of
+ *     the last failure on the calling thread is read with pope_last_error().
+ *     No C++ exception crosses this boundary.
+ *   - Shapes/strides are validated on the host before any HIP call, so argument
+ *     errors are testable without a GPU.
+ *   - Kernels are enqueued on the caller's stream (a hipStream_t passed as
+ *     void*); nothing synchronises the host.  Calls are re-entrant.
+ *   - Strides are in ELEMENTS.  The feature (last) dimension must be contiguous.
+ */
+#ifndef POPE_ABI_H
+#define POPE_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define POPE_ABI_VERSION 1
+
+enum pope_dtype { POPE_F32 = 0, POPE_F16 = 1, POPE_BF16 = 2 };
+
+enum pope_status {
+  POPE_OK = 0,
+  POPE_ERR_INVALID = 1,     /* bad shape / stride / pointer / argument */
+  POPE_ERR_UNSUPPORTED = 2, /* valid request the kernels do not cover */
+  POPE_ERR_WORKSPACE = 3,   /* workspace missing or too small */
+  POPE_ERR_HIP = 4          /* a HIP runtime call failed */
+};
+
+enum pope_op { POPE_OP_SIM_FWD = 0, POPE_OP_SIM_BWD = 1, POPE_OP_FLASH_FWD = 2,
+               POPE_OP_FLASH_BWD = 3, POPE_OP_FLASH_DECODE = 4 };
+
+/*
+ * Problem descriptor shared by every entry point.
+ *
+ * q: (B, Hq, Nq, D)   k, v: (B, Hk, Nk, D)   o / dq / do like q, dk / dv like k,
+ * addressed as x[b*s[0] + h*s[1] + n*s[2] + d].  Query head h reads kv head
+ * h % Hk (the reference's 'b h ... -> b (g h) ...' repeat, attention.py:44-45).
+ * freqs: rows n < Nk of an (N, R) / (B, N, R) / per-head table, addressed as
+ * f[b*f_s[0] + h*f_s[1] + n*f_s[2] + r] (0 strides broadcast); the key phase is
+ * freqs[j] + bias, the query phase freqs[Nk - Nq + i] (right-aligned,
+ * pope.py:64, triton_pope_flash_attn.py:54).  R == 0 means no PoPE (plain
+ * attention / plain q k^T).  bias: (Hb, R) with Hb in {1, Hk}, row stride
+ * bias_sh (0 when Hb == 1); it must already be clamped to [-2*pi, 0]
+ * (pope.py:145).  mask: (B, Nk) bytes, nonzero = keep (attention.py:129-131).
+ */
+typedef struct pope_desc {
+  int32_t B, Hq, Hk, Nq, Nk, D, R;
+  int32_t dtype;          /* enum pope_dtype of q, k, v, o and their grads */
+  int32_t causal;         /* top-left causal: key j visible to query i iff j <= i */
+  float softmax_scale;    /* flash only; the reference default is D ** -0.5 */
+  int64_t q_s[3], k_s[3], v_s[3], o_s[3];
+  int64_t do_s[3], dq_s[3], dk_s[3], dv_s[3];
+  int64_t sim_s[3];       /* similarity output (b, h, i); column stride 1 */
+  int64_t f_s[3];         /* freqs (b, h, n) strides */
+  int64_t df_s[3];        /* dfreqs (b, h, n) strides; fp32 accumulation target */
+  int64_t bias_sh;        /* bias / dbias row stride */
+  int64_t mask_sb;        /* mask batch stride in bytes */
+} pope_desc;
+
+/* Version of this header the library was built from. */
+int pope_abi_version(void);
+
+/* Copies the last error message of the calling thread (NUL-terminated). */
+int pope_last_error(char* buf, size_t n);
+
+/* Bytes of caller-owned device workspace an operation needs (no counterpart in
+ * the reference, whose launch wrappers allocate scratch through torch:
+ * triton_pope.py:267-272,297-300; triton_pope_flash_attn.py:288,358-359). */
+int pope_workspace_bytes(int op, const pope_desc* desc, size_t* bytes);
+
+/*
+ * Fused PoPE similarity forward, fp32 MFMA:  sim[b,h,i,j] (unscaled).
+ * Replaces PoPESimilarityFunction.forward + _fwd_kernel launch
+ * (triton_pope.py:260-288; kernel :28-83).  dtype: POPE_F32 (inputs and sim).
+ */
+int pope_sim_fwd(const pope_desc* desc, const void* q, const void* k, const float* freqs,
+                 const float* bias, void* sim, void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+/*
+ * Fused PoPE similarity backward.  dsim has the sim layout (sim_s).  dq, dk are
+ * written (not accumulated).  dfreqs (fp32, df_s strides) and dbias (fp32, Hb
+ * rows, bias_sh) are ACCUMULATED into and may be NULL; the caller zeroes them.
+ * Replaces PoPESimilarityFunction.backward (triton_pope.py:291-362; kernels
+ * _bwd_kernel_dqk_df :85-194 and _bwd_kernel_dbias_optimized :196-256).
+ */
+int pope_sim_bwd(const pope_desc* desc, const void* dsim, const void* q, const void* k,
+                 const float* freqs, const float* bias, void* dq, void* dk, float* dfreqs,
+                 float* dbias, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Flash attention forward with PoPE fused (online softmax, top-left causal,
+ * key-padding mask).  Writes o (dtype) and lse (fp32, (B, Hq, Nq) contiguous,
+ * natural log, -inf for fully masked rows).  freqs/bias may be NULL when R == 0,
+ * mask may be NULL.  dtype: POPE_BF16 or POPE_F16.
+ * Replaces flash_attn_forward (triton_pope_flash_attn.py:222-271; kernel :23-117).
+ */
+int pope_flash_fwd(const pope_desc* desc, const void* q, const void* k, const void* v,
+                   const float* freqs, const float* bias, const uint8_t* mask, void* o,
+                   float* lse, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Flash attention backward with PoPE.  dq, dk, dv are written (not accumulated);
+ * dfreqs / dbias are fp32 and ACCUMULATED into (caller zeroes; NULL = not wanted).
+ * Replaces flash_attn_backward (triton_pope_flash_attn.py:273-335; kernels
+ * _bwd_preprocess :119-130 and _bwd_kernel :132-218).
+ */
+int pope_flash_bwd(const pope_desc* desc, const void* dout, const void* q, const void* k,
+                   const void* v, const void* o, const float* lse, const float* freqs,
+                   const float* bias, const uint8_t* mask, void* dq, void* dk, void* dv,
+                   float* dfreqs, float* dbias, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/*
+ * Bandwidth-bound forward for short query blocks (Nq <= 16, e.g. single-token
+ * decode against a long KV cache): split-K over the keys plus an LSE merge.
+ * Same contract as pope_flash_fwd.  Replaces flash_attn_forward at seqlen_q = 1
+ * (triton_pope_flash_attn.py:222-271 with grid (1, B*H)).
+ */
+int pope_flash_decode(const pope_desc* desc, const void* q, const void* k, const void* v,
+                      const float* freqs, const float* bias, const uint8_t* mask, void* o,
+                      float* lse, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POPE_ABI_H */

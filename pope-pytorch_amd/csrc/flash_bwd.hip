@@ -1,0 +1,5 @@
+// Flash attention backward with PoPE (placeholder until the kernels land).
+#include "pope_kernels.hpp"
+namespace pope {
+hipError_t launch_flash_bwd(const FlashBwdParams&, int, hipStream_t) { return hipErrorInvalidValue; }
+}  // namespace pope

@@ -1,0 +1,487 @@
+// C ABI of libpope_hip.so: host-side validation, workspace layout and dispatch.
+// Declarations and the reference interfaces they replace: include/pope_abi.h.
+#include "../../include/pope_abi.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "pope_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(POPE_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+// Geometry shared by the ops.
+struct Geo {
+  int Bt, Ht;   // phase-table batch / head extents (1 when freqs broadcasts)
+  size_t table; // bytes of a (Bt, Ht, Nk, R) float2 table
+};
+
+Geo geometry(const pope_desc& d, int heads) {
+  Geo g;
+  g.Bt = d.f_s[0] != 0 ? d.B : 1;
+  g.Ht = d.f_s[1] != 0 ? heads : 1;
+  g.table = d.R > 0 ? align_up((size_t)g.Bt * g.Ht * d.Nk * d.R * sizeof(float2)) : 0;
+  return g;
+}
+
+int check_strides16(const char* name, const int64_t* s) {
+  for (int i = 0; i < 3; ++i)
+    if (s[i] < 0 || (s[i] % 8) != 0)
+      return fail(POPE_ERR_INVALID, "%s stride[%d] = %lld must be a non-negative multiple of 8 elements",
+                  name, i, (long long)s[i]);
+  return POPE_OK;
+}
+
+int check_strides32(const char* name, const int64_t* s) {
+  for (int i = 0; i < 3; ++i)
+    if (s[i] < 0 || (s[i] % 4) != 0)
+      return fail(POPE_ERR_INVALID, "%s stride[%d] = %lld must be a non-negative multiple of 4 elements",
+                  name, i, (long long)s[i]);
+  return POPE_OK;
+}
+
+// Checks common to every op.
+int check_desc(const pope_desc* d) {
+  if (!d) return fail(POPE_ERR_INVALID, "descriptor is NULL");
+  if (d->B < 1 || d->Hq < 1 || d->Hk < 1 || d->Nq < 1 || d->Nk < 1)
+    return fail(POPE_ERR_INVALID, "B, Hq, Hk, Nq, Nk must be >= 1 (got %d, %d, %d, %d, %d)", d->B, d->Hq,
+                d->Hk, d->Nq, d->Nk);
+  if (d->Hq % d->Hk != 0)
+    return fail(POPE_ERR_INVALID, "query heads %d must be a multiple of kv heads %d", d->Hq, d->Hk);
+  if (d->D < 8 || d->D % 8 != 0)
+    return fail(POPE_ERR_INVALID, "head dim %d must be a positive multiple of 8", d->D);
+  if (d->R < 0 || d->R > d->D || d->R % 8 != 0)
+    return fail(POPE_ERR_INVALID, "rotate dim %d must be a multiple of 8 in [0, head dim %d]", d->R, d->D);
+  if (d->R > 0 && d->Nq > d->Nk)
+    return fail(POPE_ERR_INVALID, "query length %d exceeds key length %d (q rows are right-aligned)", d->Nq,
+                d->Nk);
+  if (d->f_s[0] < 0 || d->f_s[1] < 0 || d->f_s[2] < 0 || d->bias_sh < 0)
+    return fail(POPE_ERR_INVALID, "negative freqs/bias stride");
+  if (d->R > 0 && d->f_s[1] != 0 && d->Hq != d->Hk)
+    return fail(POPE_ERR_UNSUPPORTED, "per-head freqs need Hq == Hk");
+  return POPE_OK;
+}
+
+int check_pope_ptrs(const pope_desc* d, const float* freqs, const float* bias) {
+  if (d->R > 0 && (!freqs || !bias))
+    return fail(POPE_ERR_INVALID, "rotate dim %d > 0 needs freqs and bias", d->R);
+  return POPE_OK;
+}
+
+int check_ws(size_t need, void* ws, size_t have) {
+  if (need == 0) return POPE_OK;
+  if (!ws || have < need)
+    return fail(POPE_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? have : (size_t)0);
+  if ((reinterpret_cast<uintptr_t>(ws) % kAlign) != 0)
+    return fail(POPE_ERR_WORKSPACE, "workspace must be %zu-byte aligned", kAlign);
+  return POPE_OK;
+}
+
+// Flash workspace: [table | delta | dq accumulator]  (the last two only for the backward).
+size_t flash_ws(const pope_desc& d, int op) {
+  const Geo g = geometry(d, d.Hq);
+  size_t n = g.table;
+  if (op == POPE_OP_FLASH_BWD) {
+    const int EP = round_up(d.D + d.R, 32);
+    n += align_up((size_t)d.B * d.Hq * d.Nq * sizeof(float));
+    n += align_up((size_t)d.B * d.Hq * d.Nq * EP * sizeof(float));
+  }
+  return n;
+}
+
+// Similarity workspace: [key table with bias (Bt, Hk) | query table without bias (Bt, Hqt)
+//                        | U (B, Hq, Nq, EP) | W (B, Hk, Nk, EP)]  (the last three for the backward).
+size_t sim_table_k(const pope_desc& d) {
+  const int Bt = d.f_s[0] != 0 ? d.B : 1;
+  return d.R > 0 ? align_up((size_t)Bt * d.Hk * d.Nk * d.R * sizeof(float2)) : 0;
+}
+size_t sim_table_q(const pope_desc& d) {
+  const int Bt = d.f_s[0] != 0 ? d.B : 1;
+  const int Hqt = d.f_s[1] != 0 ? d.Hq : 1;
+  return d.R > 0 ? align_up((size_t)Bt * Hqt * d.Nk * d.R * sizeof(float2)) : 0;
+}
+size_t sim_ws(const pope_desc& d, int op) {
+  const int EP = round_up(d.D + d.R, 32);
+  size_t n = sim_table_k(d) + sim_table_q(d);
+  if (op == POPE_OP_SIM_BWD) {
+    n += align_up((size_t)d.B * d.Hq * d.Nq * EP * sizeof(float));
+    n += align_up((size_t)d.B * d.Hk * d.Nk * EP * sizeof(float));
+  }
+  return n;
+}
+
+// Decode workspace: [table | partial O (rows, splits, D) | partial (m, l) (rows, splits, 2)].
+int decode_splits(const pope_desc& d) {
+  // Enough (batch, head, split) work items to cover 256 CUs several times over,
+  // with at least 256 keys per split.
+  const int rows = d.B * d.Hq;
+  int splits = (2048 + rows - 1) / rows;
+  const int max_by_len = (d.Nk + 255) / 256;
+  if (splits > max_by_len) splits = max_by_len;
+  if (splits < 1) splits = 1;
+  if (splits > 256) splits = 256;
+  return splits;
+}
+
+size_t decode_ws(const pope_desc& d) {
+  const Geo g = geometry(d, d.Hq);
+  const int splits = decode_splits(d);
+  const size_t rows = (size_t)d.B * d.Hq * d.Nq;
+  return g.table + align_up(rows * splits * d.D * sizeof(float)) + align_up(rows * splits * 2 * sizeof(float));
+}
+
+hipError_t build_table(const pope_desc& d, const float* freqs, const float* bias, int Bt, int Ht,
+                       float2* out, hipStream_t s) {
+  pope::TableParams t;
+  t.freqs = freqs;
+  t.f_sb = d.f_s[0];
+  t.f_sh = d.f_s[1];
+  t.f_sn = d.f_s[2];
+  t.bias = bias;
+  t.bias_sh = d.bias_sh;
+  t.Bt = Bt;
+  t.Ht = Ht;
+  t.rows = d.Nk;
+  t.R = d.R;
+  t.out = out;
+  return pope::launch_phase_table(t, s);
+}
+
+void copy3(int64_t* dst, const int64_t* src) {
+  dst[0] = src[0];
+  dst[1] = src[1];
+  dst[2] = src[2];
+}
+
+int check_flash_common(const pope_desc* d, const void* q, const void* k, const void* v, const float* freqs,
+                       const float* bias, const uint8_t* mask, const void* o, const float* lse) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (d->dtype != POPE_BF16 && d->dtype != POPE_F16)
+    return fail(POPE_ERR_UNSUPPORTED, "flash kernels take bf16 or fp16 (dtype %d)", d->dtype);
+  if (d->D > 128) return fail(POPE_ERR_UNSUPPORTED, "flash kernels cover head dim <= 128 (got %d)", d->D);
+  if (!q || !k || !v || !o || !lse) return fail(POPE_ERR_INVALID, "q, k, v, o and lse must be non-NULL");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return fail(POPE_ERR_INVALID, "q, k, v, o must be 16-byte aligned");
+  if ((rc = check_strides16("q", d->q_s)) || (rc = check_strides16("k", d->k_s)) ||
+      (rc = check_strides16("v", d->v_s)) || (rc = check_strides16("o", d->o_s)))
+    return rc;
+  if ((rc = check_pope_ptrs(d, freqs, bias))) return rc;
+  if (d->mask_sb < 0) return fail(POPE_ERR_INVALID, "negative mask stride");
+  (void)mask;
+  if (d->softmax_scale != d->softmax_scale) return fail(POPE_ERR_INVALID, "softmax scale is NaN");
+  return POPE_OK;
+}
+
+
+int check_sim_common(const pope_desc* d, const void* q, const void* k, const float* freqs, const float* bias) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (d->dtype != POPE_F32) return fail(POPE_ERR_UNSUPPORTED, "similarity kernels take fp32 (dtype %d)", d->dtype);
+  if (d->D > 256) return fail(POPE_ERR_UNSUPPORTED, "similarity covers head dim <= 256 (got %d)", d->D);
+  if (!q || !k) return fail(POPE_ERR_INVALID, "q, k must be non-NULL");
+  if (!aligned16(q) || !aligned16(k)) return fail(POPE_ERR_INVALID, "q, k must be 16-byte aligned");
+  if ((rc = check_strides32("q", d->q_s)) || (rc = check_strides32("k", d->k_s))) return rc;
+  return check_pope_ptrs(d, freqs, bias);
+}
+
+// Builds the key table (with bias) and the query table (without) and fills the shared parameters.
+hipError_t sim_setup(const pope_desc& d, const void* q, const void* k, const float* freqs, const float* bias,
+                     char* ws, hipStream_t s, pope::SimParams* out) {
+  pope::SimParams& p = *out;
+  std::memset(&p, 0, sizeof p);
+  const int Bt = d.f_s[0] != 0 ? d.B : 1;
+  const int Hqt = d.f_s[1] != 0 ? d.Hq : 1;
+  float2* ktab = reinterpret_cast<float2*>(ws);
+  float2* qtab = reinterpret_cast<float2*>(ws + sim_table_k(d));
+  if (d.R > 0) {
+    hipError_t e = build_table(d, freqs, bias, Bt, d.Hk, ktab, s);
+    if (e != hipSuccess) return e;
+    e = build_table(d, freqs, nullptr, Bt, Hqt, qtab, s);  // query phases never carry the bias
+    if (e != hipSuccess) return e;
+  }
+  p.q = static_cast<const float*>(q);
+  p.k = static_cast<const float*>(k);
+  p.freqs = d.R > 0 ? freqs : nullptr;
+  p.bias = d.R > 0 ? bias : nullptr;
+  p.ktab = d.R > 0 ? ktab : nullptr;
+  p.qtab = d.R > 0 ? qtab : nullptr;
+  p.B = d.B; p.Hq = d.Hq; p.Hk = d.Hk; p.Nq = d.Nq; p.Nk = d.Nk; p.D = d.D; p.R = d.R;
+  p.E = d.D + d.R;
+  p.EP = round_up(p.E, 32);
+  copy3(p.q_s, d.q_s);
+  copy3(p.k_s, d.k_s);
+  copy3(p.sim_s, d.sim_s);
+  copy3(p.f_s, d.f_s);
+  p.bias_sh = d.bias_sh;
+  p.kt_sb = Bt > 1 ? (int64_t)d.Hk * d.Nk * d.R : 0;
+  p.kt_sh = (int64_t)d.Nk * d.R;
+  p.qt_sb = Bt > 1 ? (int64_t)Hqt * d.Nk * d.R : 0;
+  p.qt_sh = Hqt > 1 ? (int64_t)d.Nk * d.R : 0;
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pope_abi_version(void) { return POPE_ABI_VERSION; }
+
+int pope_last_error(char* buf, size_t n) {
+  if (!buf || n == 0) return POPE_ERR_INVALID;
+  std::strncpy(buf, g_err.c_str(), n - 1);
+  buf[n - 1] = '\0';
+  return POPE_OK;
+}
+
+int pope_workspace_bytes(int op, const pope_desc* desc, size_t* bytes) {
+  if (!bytes) return fail(POPE_ERR_INVALID, "bytes is NULL");
+  int rc = check_desc(desc);
+  if (rc) return rc;
+  switch (op) {
+    case POPE_OP_SIM_FWD:
+    case POPE_OP_SIM_BWD: *bytes = sim_ws(*desc, op); return POPE_OK;
+    case POPE_OP_FLASH_FWD:
+    case POPE_OP_FLASH_BWD: *bytes = flash_ws(*desc, op); return POPE_OK;
+    case POPE_OP_FLASH_DECODE: *bytes = decode_ws(*desc); return POPE_OK;
+    default: return fail(POPE_ERR_INVALID, "unknown op %d", op);
+  }
+}
+
+int pope_flash_fwd(const pope_desc* d, const void* q, const void* k, const void* v, const float* freqs,
+                   const float* bias, const uint8_t* mask, void* o, float* lse, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  int rc = check_flash_common(d, q, k, v, freqs, bias, mask, o, lse);
+  if (rc) return rc;
+  if ((rc = check_ws(flash_ws(*d, POPE_OP_FLASH_FWD), workspace, workspace_bytes))) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const Geo g = geometry(*d, d->Hq);
+  float2* table = reinterpret_cast<float2*>(workspace);
+  if (d->R > 0) {
+    hipError_t e = build_table(*d, freqs, nullptr, g.Bt, g.Ht, table, s);
+    if (e != hipSuccess) return hip_fail(e, "phase table launch");
+  }
+  pope::FlashFwdParams p;
+  std::memset(&p, 0, sizeof p);
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.freqs = d->R > 0 ? freqs : nullptr;
+  p.bias = d->R > 0 ? bias : nullptr;
+  p.mask = mask;
+  p.table = d->R > 0 ? table : nullptr;
+  p.o = static_cast<uint16_t*>(o);
+  p.lse = lse;
+  p.B = d->B; p.Hq = d->Hq; p.Hk = d->Hk; p.Nq = d->Nq; p.Nk = d->Nk; p.D = d->D; p.R = d->R;
+  p.causal = d->causal != 0;
+  p.has_mask = mask != nullptr;
+  p.nqb = (d->Nq + 127) / 128;
+  p.scale_log2 = d->softmax_scale * 1.4426950408889634f;
+  copy3(p.q_s, d->q_s); copy3(p.k_s, d->k_s); copy3(p.v_s, d->v_s);
+  copy3(p.o_s, d->o_s); copy3(p.f_s, d->f_s);
+  p.bias_sh = d->bias_sh;
+  p.mask_sb = d->mask_sb;
+  p.t_sb = g.Bt > 1 ? (int64_t)g.Ht * d->Nk * d->R : 0;
+  p.t_sh = g.Ht > 1 ? (int64_t)d->Nk * d->R : 0;
+  hipError_t e = pope::launch_flash_fwd(p, d->dtype, s);
+  if (e == hipErrorInvalidValue)
+    return fail(POPE_ERR_UNSUPPORTED, "no flash forward kernel for head dim %d, rotate dim %d", d->D, d->R);
+  if (e != hipSuccess) return hip_fail(e, "flash forward launch");
+  return POPE_OK;
+}
+
+int pope_flash_bwd(const pope_desc* d, const void* dout, const void* q, const void* k, const void* v,
+                   const void* o, const float* lse, const float* freqs, const float* bias, const uint8_t* mask,
+                   void* dq, void* dk, void* dv, float* dfreqs, float* dbias, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  int rc = check_flash_common(d, q, k, v, freqs, bias, mask, o, lse);
+  if (rc) return rc;
+  if (!dout || !dq || !dk || !dv) return fail(POPE_ERR_INVALID, "dout, dq, dk, dv must be non-NULL");
+  if (!aligned16(dout) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
+    return fail(POPE_ERR_INVALID, "dout, dq, dk, dv must be 16-byte aligned");
+  if ((rc = check_strides16("do", d->do_s)) || (rc = check_strides16("dq", d->dq_s)) ||
+      (rc = check_strides16("dk", d->dk_s)) || (rc = check_strides16("dv", d->dv_s)))
+    return rc;
+  if (d->R == 0 && (dfreqs || dbias)) return fail(POPE_ERR_INVALID, "dfreqs/dbias requested with rotate dim 0");
+  if ((rc = check_ws(flash_ws(*d, POPE_OP_FLASH_BWD), workspace, workspace_bytes))) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const Geo g = geometry(*d, d->Hq);
+  char* ws = static_cast<char*>(workspace);
+  float2* table = reinterpret_cast<float2*>(ws);
+  float* delta = reinterpret_cast<float*>(ws + g.table);
+  float* dqacc = reinterpret_cast<float*>(ws + g.table + align_up((size_t)d->B * d->Hq * d->Nq * sizeof(float)));
+  if (d->R > 0) {
+    hipError_t e = build_table(*d, freqs, nullptr, g.Bt, g.Ht, table, s);
+    if (e != hipSuccess) return hip_fail(e, "phase table launch");
+  }
+  pope::FlashBwdParams p;
+  std::memset(&p, 0, sizeof p);
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.o = static_cast<const uint16_t*>(o);
+  p.dout = static_cast<const uint16_t*>(dout);
+  p.lse = lse;
+  p.freqs = d->R > 0 ? freqs : nullptr;
+  p.bias = d->R > 0 ? bias : nullptr;
+  p.mask = mask;
+  p.table = d->R > 0 ? table : nullptr;
+  p.dq = static_cast<uint16_t*>(dq);
+  p.dk = static_cast<uint16_t*>(dk);
+  p.dv = static_cast<uint16_t*>(dv);
+  p.dfreqs = dfreqs;
+  p.dbias = dbias;
+  p.delta = delta;
+  p.dqacc = dqacc;
+  p.B = d->B; p.Hq = d->Hq; p.Hk = d->Hk; p.Nq = d->Nq; p.Nk = d->Nk; p.D = d->D; p.R = d->R;
+  p.E = d->D + d->R;
+  p.EP = round_up(p.E, 32);
+  p.causal = d->causal != 0;
+  p.has_mask = mask != nullptr;
+  p.scale = d->softmax_scale;
+  p.scale_log2 = d->softmax_scale * 1.4426950408889634f;
+  copy3(p.q_s, d->q_s); copy3(p.k_s, d->k_s); copy3(p.v_s, d->v_s);
+  copy3(p.o_s, d->o_s); copy3(p.do_s, d->do_s); copy3(p.dq_s, d->dq_s);
+  copy3(p.dk_s, d->dk_s); copy3(p.dv_s, d->dv_s); copy3(p.f_s, d->f_s);
+  copy3(p.df_s, d->df_s);
+  p.bias_sh = d->bias_sh;
+  p.mask_sb = d->mask_sb;
+  p.t_sb = g.Bt > 1 ? (int64_t)g.Ht * d->Nk * d->R : 0;
+  p.t_sh = g.Ht > 1 ? (int64_t)d->Nk * d->R : 0;
+  hipError_t e = pope::launch_flash_bwd(p, d->dtype, s);
+  if (e == hipErrorInvalidValue)
+    return fail(POPE_ERR_UNSUPPORTED, "no flash backward kernel for head dim %d, rotate dim %d", d->D, d->R);
+  if (e != hipSuccess) return hip_fail(e, "flash backward launch");
+  return POPE_OK;
+}
+
+int pope_flash_decode(const pope_desc* d, const void* q, const void* k, const void* v, const float* freqs,
+                      const float* bias, const uint8_t* mask, void* o, float* lse, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  int rc = check_flash_common(d, q, k, v, freqs, bias, mask, o, lse);
+  if (rc) return rc;
+  if (d->Nq > 16) return fail(POPE_ERR_UNSUPPORTED, "decode kernel covers up to 16 query rows (got %d)", d->Nq);
+  if ((rc = check_ws(decode_ws(*d), workspace, workspace_bytes))) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const Geo g = geometry(*d, d->Hq);
+  char* ws = static_cast<char*>(workspace);
+  const int splits = decode_splits(*d);
+  const size_t rows = (size_t)d->B * d->Hq * d->Nq;
+  float2* table = reinterpret_cast<float2*>(ws);
+  float* part_o = reinterpret_cast<float*>(ws + g.table);
+  float* part_ml = reinterpret_cast<float*>(ws + g.table + align_up(rows * splits * d->D * sizeof(float)));
+  if (d->R > 0) {
+    hipError_t e = build_table(*d, freqs, nullptr, g.Bt, g.Ht, table, s);
+    if (e != hipSuccess) return hip_fail(e, "phase table launch");
+  }
+  pope::DecodeParams p;
+  std::memset(&p, 0, sizeof p);
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.freqs = d->R > 0 ? freqs : nullptr;
+  p.bias = d->R > 0 ? bias : nullptr;
+  p.mask = mask;
+  p.table = d->R > 0 ? table : nullptr;
+  p.o = static_cast<uint16_t*>(o);
+  p.lse = lse;
+  p.part_o = part_o;
+  p.part_ml = part_ml;
+  p.B = d->B; p.Hq = d->Hq; p.Hk = d->Hk; p.Nq = d->Nq; p.Nk = d->Nk; p.D = d->D; p.R = d->R;
+  p.causal = d->causal != 0;
+  p.has_mask = mask != nullptr;
+  p.splits = splits;
+  p.keys_per_split = (d->Nk + splits - 1) / splits;
+  p.scale_log2 = d->softmax_scale * 1.4426950408889634f;
+  copy3(p.q_s, d->q_s); copy3(p.k_s, d->k_s); copy3(p.v_s, d->v_s);
+  copy3(p.o_s, d->o_s); copy3(p.f_s, d->f_s);
+  p.bias_sh = d->bias_sh;
+  p.mask_sb = d->mask_sb;
+  p.t_sb = g.Bt > 1 ? (int64_t)g.Ht * d->Nk * d->R : 0;
+  p.t_sh = g.Ht > 1 ? (int64_t)d->Nk * d->R : 0;
+  hipError_t e = pope::launch_flash_decode(p, d->dtype, s);
+  if (e == hipErrorInvalidValue)
+    return fail(POPE_ERR_UNSUPPORTED, "no decode kernel for head dim %d, rotate dim %d", d->D, d->R);
+  if (e != hipSuccess) return hip_fail(e, "flash decode launch");
+  return POPE_OK;
+}
+
+int pope_sim_fwd(const pope_desc* d, const void* q, const void* k, const float* freqs, const float* bias,
+                 void* sim, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_sim_common(d, q, k, freqs, bias);
+  if (rc) return rc;
+  if (!sim) return fail(POPE_ERR_INVALID, "sim must be non-NULL");
+  if (d->sim_s[0] < 0 || d->sim_s[1] < 0 || d->sim_s[2] < 0) return fail(POPE_ERR_INVALID, "negative sim stride");
+  if ((rc = check_ws(sim_ws(*d, POPE_OP_SIM_FWD), workspace, workspace_bytes))) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  pope::SimParams p;
+  hipError_t e = sim_setup(*d, q, k, freqs, bias, static_cast<char*>(workspace), s, &p);
+  if (e != hipSuccess) return hip_fail(e, "phase table launch");
+  p.sim = static_cast<float*>(sim);
+  e = pope::launch_sim_fwd(p, s);
+  if (e != hipSuccess) return hip_fail(e, "similarity forward launch");
+  return POPE_OK;
+}
+
+int pope_sim_bwd(const pope_desc* d, const void* dsim, const void* q, const void* k, const float* freqs,
+                 const float* bias, void* dq, void* dk, float* dfreqs, float* dbias, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  int rc = check_sim_common(d, q, k, freqs, bias);
+  if (rc) return rc;
+  if (!dsim || !dq || !dk) return fail(POPE_ERR_INVALID, "dsim, dq, dk must be non-NULL");
+  if (!aligned16(dq) || !aligned16(dk)) return fail(POPE_ERR_INVALID, "dq, dk must be 16-byte aligned");
+  if (d->sim_s[0] < 0 || d->sim_s[1] < 0 || d->sim_s[2] < 0) return fail(POPE_ERR_INVALID, "negative dsim stride");
+  if ((rc = check_strides32("dq", d->dq_s)) ||
+      (rc = check_strides32("dk", d->dk_s)))
+    return rc;
+  if (d->R == 0 && (dfreqs || dbias)) return fail(POPE_ERR_INVALID, "dfreqs/dbias requested with rotate dim 0");
+  if (d->df_s[0] < 0 || d->df_s[1] < 0 || d->df_s[2] < 0) return fail(POPE_ERR_INVALID, "negative dfreqs stride");
+  if ((rc = check_ws(sim_ws(*d, POPE_OP_SIM_BWD), workspace, workspace_bytes))) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  pope::SimParams p;
+  hipError_t e = sim_setup(*d, q, k, freqs, bias, ws, s, &p);
+  if (e != hipSuccess) return hip_fail(e, "phase table launch");
+  p.dsim = static_cast<const float*>(dsim);
+  p.g_vec = aligned16(dsim) && d->sim_s[0] % 4 == 0 && d->sim_s[1] % 4 == 0 && d->sim_s[2] % 4 == 0;
+  p.dq = static_cast<float*>(dq);
+  p.dk = static_cast<float*>(dk);
+  p.dfreqs = dfreqs;
+  p.dbias = dbias;
+  copy3(p.dq_s, d->dq_s);
+  copy3(p.dk_s, d->dk_s);
+  copy3(p.df_s, d->df_s);
+  const size_t off_u = sim_table_k(*d) + sim_table_q(*d);
+  float* U = reinterpret_cast<float*>(ws + off_u);
+  float* W = reinterpret_cast<float*>(ws + off_u + align_up((size_t)d->B * d->Hq * d->Nq * p.EP * sizeof(float)));
+  e = pope::launch_sim_bwd_ws(p, U, W, s);
+  if (e != hipSuccess) return hip_fail(e, "similarity backward launch");
+  return POPE_OK;
+}
+
+}  // extern "C"

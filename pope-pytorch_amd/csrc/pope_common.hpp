@@ -1,0 +1,112 @@
+// Shared device helpers for the PoPE kernels (gfx950 / CDNA4, wave64).
+//
+// The polar transform of PoPE (reference pope.py:30-86, triton_pope.py:18-24):
+//   magnitude  a = softplus(x)            (beta = 1, threshold 20: x > 20 -> x)
+//   phase      query: phi = F[q_off + i, d]      key: psi = F[j, d] + bias[h, d]
+//   expanded   x_hat = [a cos(phase) | a sin(phase) | raw pass-through dims]
+// Every kernel lays the expanded feature axis out as E = D + R columns:
+//   e <  R        -> cos part of rotated dim e
+//   R <= e < 2R   -> sin part of rotated dim e - R
+//   e >= 2R       -> pass-through dim e - R (raw, no softplus)
+// The column order inside a kernel is free (it only changes the order of a
+// dot product); the public materialising transform interleaves (pope.py:70).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pope {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Element-type traits for the half-precision MFMA paths.
+struct BF16 {
+  typedef __bf16 scalar;
+  typedef bf16x8 vec8;
+  static __device__ __forceinline__ float to_float(uint16_t bits) {
+    return __uint_as_float(((uint32_t)bits) << 16);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    bf16x2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mfma16(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+struct F16 {
+  typedef _Float16 scalar;
+  typedef f16x8 vec8;
+  static __device__ __forceinline__ float to_float(uint16_t bits) {
+    return (float)__builtin_bit_cast(_Float16, bits);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    f16x2 v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mfma16(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// softplus in fp32 with hardware exp2/log2: max(x,0) + ln(1 + e^-|x|), x > 20 -> x.
+__device__ __forceinline__ float softplus_f(float x) {
+  float e = __builtin_amdgcn_exp2f(-fabsf(x) * kLog2e);
+  float y = fmaxf(x, 0.f) + __builtin_amdgcn_logf(1.f + e) * kLn2;
+  return x > 20.f ? x : y;
+}
+
+// d softplus / dx = sigmoid(x).
+__device__ __forceinline__ float sigmoid_f(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
+
+// Accurate fp32 sine/cosine with full range reduction (device math library).
+__device__ __forceinline__ void sincos_acc(float x, float* s, float* c) { sincosf(x, s, c); }
+
+__device__ __forceinline__ uint32_t u16lo(uint32_t w) { return w & 0xffffu; }
+__device__ __forceinline__ uint32_t u16hi(uint32_t w) { return w >> 16; }
+
+template <typename V>
+__device__ __forceinline__ V as_vec8(u32x4 w) { return __builtin_bit_cast(V, w); }
+
+// 8 consecutive 16-bit elements -> 8 floats.
+template <typename T>
+__device__ __forceinline__ void unpack8(u32x4 w, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = T::to_float((uint16_t)u16lo(w[i]));
+    f[2 * i + 1] = T::to_float((uint16_t)u16hi(w[i]));
+  }
+}
+
+// XCD-aware workgroup remap. Consecutive hardware workgroup ids are dealt
+// round-robin to the 8 XCDs of an MI355X; each XCD has its own L2.  Return a
+// logical id such that each XCD processes a contiguous range of logical ids
+// (so the K/V of one (batch, head) stays in one L2).
+__device__ __forceinline__ int xcd_remap(int hw_id, int total) {
+  constexpr int kXcd = 8;
+  if (total % kXcd != 0) return hw_id;
+  int per = total / kXcd;
+  return (hw_id % kXcd) * per + hw_id / kXcd;
+}
+
+__device__ __forceinline__ float wave_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+}  // namespace pope

@@ -1,0 +1,74 @@
+// Kernel parameter blocks and launchers shared between the kernels and the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pope {
+
+// cos/sin of the phase table: tab[bt*t_sb + ht*t_sh + n*R + d] = (cos, sin) of
+// F[n, d] (+ bias[ht, d] when a bias is folded in), for n < rows.
+struct TableParams {
+  const float* freqs; int64_t f_sb, f_sh, f_sn;
+  const float* bias; int64_t bias_sh;  // may be null
+  int Bt, Ht, rows, R;
+  float2* out;
+};
+hipError_t launch_phase_table(const TableParams& p, hipStream_t s);
+
+struct FlashFwdParams {
+  const uint16_t* q; const uint16_t* k; const uint16_t* v;
+  const float* freqs; const float* bias; const uint8_t* mask;
+  const float2* table;       // cos/sin(F[b, h, n, d]) for n < Nk, no bias
+  uint16_t* o; float* lse;
+  int B, Hq, Hk, Nq, Nk, D, R, causal, has_mask, nqb;
+  float scale_log2;          // softmax_scale * log2(e)
+  int64_t q_s[3], k_s[3], v_s[3], o_s[3], f_s[3];
+  int64_t bias_sh, mask_sb, t_sb, t_sh;
+};
+// dtype: 1 = f16, 2 = bf16.  Returns hipErrorInvalidValue for an uncovered (E, D) shape.
+hipError_t launch_flash_fwd(const FlashFwdParams& p, int dtype, hipStream_t s);
+
+struct FlashBwdParams {
+  const uint16_t* q; const uint16_t* k; const uint16_t* v; const uint16_t* o; const uint16_t* dout;
+  const float* lse; const float* freqs; const float* bias; const uint8_t* mask;
+  const float2* table;       // cos/sin(F[b, h, n, d]) for n < Nk, no bias
+  uint16_t* dq; uint16_t* dk; uint16_t* dv;
+  float* dfreqs; float* dbias;
+  float* delta;              // (B, Hq, Nq) workspace
+  float* dqacc;              // (B, Hq, Nq, EP) fp32 workspace
+  int B, Hq, Hk, Nq, Nk, D, R, E, EP, causal, has_mask;
+  float scale, scale_log2;
+  int64_t q_s[3], k_s[3], v_s[3], o_s[3], do_s[3], dq_s[3], dk_s[3], dv_s[3], f_s[3], df_s[3];
+  int64_t bias_sh, mask_sb, t_sb, t_sh;
+};
+hipError_t launch_flash_bwd(const FlashBwdParams& p, int dtype, hipStream_t s);
+
+struct SimParams {
+  const float* q; const float* k; const float* dsim; float* sim;
+  const float* freqs; const float* bias;
+  const float2* ktab;        // cos/sin(F[j] + bias[hk]) per (bt, hk) for keys
+  const float2* qtab;        // cos/sin(F[n]) per bt, rows n < Nk (queries use n = q_off + i)
+  float* dq; float* dk; float* dfreqs; float* dbias;
+  int B, Hq, Hk, Nq, Nk, D, R, E, EP;
+  int g_vec;                 // dsim rows are 16-byte aligned: 4-wide loads allowed
+  int64_t q_s[3], k_s[3], sim_s[3], dq_s[3], dk_s[3], f_s[3], df_s[3];
+  int64_t bias_sh, kt_sb, kt_sh, qt_sb, qt_sh;
+};
+hipError_t launch_sim_fwd(const SimParams& p, hipStream_t s);
+// U: (B, Hq, Nq, EP) and W: (B, Hk, Nk, EP) fp32 workspace.
+hipError_t launch_sim_bwd_ws(const SimParams& p, float* U, float* W, hipStream_t s);
+
+struct DecodeParams {
+  const uint16_t* q; const uint16_t* k; const uint16_t* v;
+  const float* freqs; const float* bias; const uint8_t* mask;
+  const float2* table;
+  uint16_t* o; float* lse;
+  float* part_o; float* part_ml;   // split-K partials (B*Hq*Nq, splits, D) and (.., splits, 2)
+  int B, Hq, Hk, Nq, Nk, D, R, causal, has_mask, splits, keys_per_split;
+  float scale_log2;
+  int64_t q_s[3], k_s[3], v_s[3], o_s[3], f_s[3];
+  int64_t bias_sh, mask_sb, t_sb, t_sh;
+};
+hipError_t launch_flash_decode(const DecodeParams& p, int dtype, hipStream_t s);
+
+}  // namespace pope

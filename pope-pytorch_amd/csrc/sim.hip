@@ -1,0 +1,378 @@
+// Fused PoPE similarity, fp32 on MFMA (v_mfma_f32_32x32x2f32), gfx950.
+//
+// Reference: PoPESimilarityFunction (triton_pope.py:258-362) with kernels
+// _fwd_kernel :28-83, _bwd_kernel_dqk_df :85-194, _bwd_kernel_dbias_optimized
+// :196-256; PyTorch path attention.py:30-47.
+//
+//   S[b,h,i,j] = sum_e Q_hat[i,e] K_hat[j,e]     (unscaled, fp32)
+// with the expanded columns of pope_common.hpp.  The phases come from the
+// per-call tables: the key table holds cos/sin(fl(F_j + bias)) exactly as the
+// reference rounds it (pope.py:56), the query table cos/sin(F_{q_off+i}).
+//
+// Backward (G = dS):
+//   U = G K_hat (Nq x E),  W = G^T Q_hat (Nk x E)  -- two MFMA passes that read
+//   G straight from HBM into registers, writing U and W (fp32) to workspace;
+//   a finalize kernel applies the chain rule of the polar transform:
+//   dq = sigmoid(q) (cos phi U_c + sin phi U_s), dq_rest = U_rest,
+//   dphi = a (cos phi U_s - sin phi U_c)  -> dfreqs rows q_off + i,
+//   dk = sigmoid(k) (cos psi W_c + sin psi W_s), dk_rest = W_rest,
+//   dpsi = c (cos psi W_s - sin psi W_c)  -> dfreqs rows j and dbias (sum over j).
+// dbias = sum_j dpsi replaces the reference's third pass over dS
+// (_bwd_kernel_dbias_optimized): both are the derivative of S by the key phase.
+#include "pope_common.hpp"
+#include "pope_kernels.hpp"
+
+namespace pope {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kEC = 32;     // expanded columns per forward chunk
+constexpr int kLdsRow = kEC + 4;  // fp32 row stride of the forward chunk buffers
+
+// Transforms 8 consecutive expanded columns [e0, e0+8) of one row into out[8].
+// x: the row of q or k (fp32), tab: the row of the phase table (or null when R == 0).
+__device__ __forceinline__ void expand8(const float* x, const float2* tab, int e0, int R, int E, bool valid,
+                                        float* out) {
+  if (!valid || e0 >= E) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) out[s] = 0.f;
+    return;
+  }
+  const bool is_cos = e0 < R, is_sin = !is_cos && e0 < 2 * R;
+  const int d0 = is_cos ? e0 : e0 - R;
+  const float4 x0 = *reinterpret_cast<const float4*>(x + d0);
+  const float4 x1 = *reinterpret_cast<const float4*>(x + d0 + 4);
+  const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  if (is_cos || is_sin) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const float2 cs = tab[d0 + s];
+      out[s] = softplus_f(xv[s]) * (is_cos ? cs.x : cs.y);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) out[s] = xv[s];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward: one workgroup = 128 x 128 tile of S; 4 waves of 64 x 64 (2 x 2
+// MFMA blocks).  The expanded axis is swept in chunks of 32 columns, each
+// chunk transformed into LDS for both operands.
+__global__ __launch_bounds__(kThreads, 2) void sim_fwd_kernel(SimParams p, int nib, int njb) {
+  __shared__ __attribute__((aligned(16))) float qs[128 * kLdsRow];
+  __shared__ __attribute__((aligned(16))) float ks[128 * kLdsRow];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int jb = id % njb, ib = (id / njb) % nib, bh = id / (njb * nib);
+  const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
+  const int R = p.R, E = p.E, Nq = p.Nq, Nk = p.Nk, q_off = Nk - Nq;
+  const int i0 = ib * 128, j0 = jb * 128;
+  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+
+  // Transform ownership: thread -> (row, 16-column half of the chunk).
+  const int trow = tid >> 1, thalf = tid & 1;
+  const int qi = i0 + trow, kj = j0 + trow;
+  const bool qv = qi < Nq, kv = kj < Nk;
+  const float* qrow = p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + (int64_t)min(qi, Nq - 1) * p.q_s[2];
+  const float* krow = p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1] + (int64_t)min(kj, Nk - 1) * p.k_s[2];
+  const float2* qtab = R ? p.qtab + (int64_t)b * p.qt_sb + (int64_t)h * p.qt_sh + (int64_t)(q_off + min(qi, Nq - 1)) * R
+                         : nullptr;
+  const float2* ktab = R ? p.ktab + (int64_t)b * p.kt_sb + (int64_t)hk * p.kt_sh + (int64_t)min(kj, Nk - 1) * R
+                         : nullptr;
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
+
+  for (int c0 = 0; c0 < p.EP; c0 += kEC) {
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int e0 = c0 + 16 * thalf + 8 * g;
+      float o[8];
+      expand8(qrow, qtab, e0, R, E, qv, o);
+      float* dst = &qs[trow * kLdsRow + 16 * thalf + 8 * g];
+      *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
+      expand8(krow, ktab, e0, R, E, kv, o);
+      dst = &ks[trow * kLdsRow + 16 * thalf + 8 * g];
+      *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
+    }
+    __syncthreads();
+    // k-slot (t, hf) <-> chunk column 16*hf + t, read 4 at a time.
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4) {
+      float4 a[2], bb[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        a[x] = *reinterpret_cast<const float4*>(&qs[(wr + 32 * x + lr) * kLdsRow + 16 * hf + 4 * t4]);
+        bb[x] = *reinterpret_cast<const float4*>(&ks[(wc + 32 * x + lr) * kLdsRow + 16 * hf + 4 * t4]);
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int y = 0; y < 2; ++y)
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[x][s], bb[y][s], acc[x][y], 0, 0, 0);
+    }
+  }
+  // S^T layout: acc lane = key column (lr), registers = query rows.
+  // Here A = Q (rows i) and B = K (cols j): result lane <-> j, regs <-> i.
+  float* sbase = p.sim + (int64_t)b * p.sim_s[0] + (int64_t)h * p.sim_s[1];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int j = j0 + wc + 32 * y + lr;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = i0 + wr + 32 * x + 8 * (r >> 2) + 4 * hf + (r & 3);
+        if (i < Nq && j < Nk) sbase[(int64_t)i * p.sim_s[2] + j] = acc[x][y][r];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward pass A:  U[b,h,i,e] = sum_j G[b,h,i,j] K_hat[b,hk,j,e]
+// one workgroup = 128 query rows x 128 expanded columns (chunk ec); 4 waves of
+// 32 rows.  G rows go straight from HBM into A-operand registers
+// (k-slot (t, hf) <-> key j0 + 32*hf + t).
+constexpr int kBJ = 64;
+constexpr int kKtRow = 128 + 1;   // fp32 row stride of the K_hat tile (keys x 128 cols)
+
+__global__ __launch_bounds__(kThreads, 2) void sim_bwd_u_kernel(SimParams p, float* U, int nib, int nec) {
+  __shared__ float kt[kBJ * kKtRow];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int ec = id % nec, ib = (id / nec) % nib, bh = id / (nec * nib);
+  const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
+  const int R = p.R, E = p.E, Nq = p.Nq, Nk = p.Nk;
+  const int i = ib * 128 + wave * 32 + lr;
+  const int e_base = ec * 128;
+  const float* grow = p.dsim + (int64_t)b * p.sim_s[0] + (int64_t)h * p.sim_s[1] + (int64_t)min(i, Nq - 1) * p.sim_s[2];
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int y = 0; y < 4; ++y)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[y][r] = 0.f;
+
+  // K tile transform ownership: thread -> (key row, 32-column quarter)
+  const int trow = tid >> 2, tq = tid & 3;
+  const float* kb = p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1];
+  const float2* tb = R ? p.ktab + (int64_t)b * p.kt_sb + (int64_t)hk * p.kt_sh : nullptr;
+
+  for (int j0 = 0; j0 < Nk; j0 += kBJ) {
+    __syncthreads();
+    {
+      const int kj = j0 + trow;
+      const bool kv = kj < Nk;
+      const float* krow = kb + (int64_t)min(kj, Nk - 1) * p.k_s[2];
+      const float2* ktab = R ? tb + (int64_t)min(kj, Nk - 1) * R : nullptr;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float o[8];
+        expand8(krow, ktab, e_base + 32 * tq + 8 * g, R, E, kv, o);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) kt[trow * kKtRow + 32 * tq + 8 * g + s] = o[s];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t4 = 0; t4 < 8; ++t4) {
+      float4 g4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      const int jj = j0 + 32 * hf + 4 * t4;
+      if (p.g_vec && i < Nq && jj + 3 < Nk) {
+        g4 = *reinterpret_cast<const float4*>(grow + jj);
+      } else if (i < Nq) {
+        float tmp[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) tmp[s] = jj + s < Nk ? grow[jj + s] : 0.f;
+        g4 = make_float4(tmp[0], tmp[1], tmp[2], tmp[3]);
+      }
+      const float gv[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int jr = 32 * hf + 4 * t4 + s;
+#pragma unroll
+        for (int y = 0; y < 4; ++y)
+          acc[y] = __builtin_amdgcn_mfma_f32_32x32x2f32(gv[s], kt[jr * kKtRow + 32 * y + lr], acc[y], 0, 0, 0);
+      }
+    }
+  }
+  // result lane <-> column e (B operand lane), regs <-> row i
+  float* ub = U + ((int64_t)b * p.Hq + h) * Nq * p.EP;
+#pragma unroll
+  for (int y = 0; y < 4; ++y) {
+    const int e = e_base + 32 * y + lr;
+    if (e >= p.EP) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int ii = ib * 128 + wave * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+      if (ii < Nq) ub[(int64_t)ii * p.EP + e] = acc[y][r];
+    }
+  }
+}
+
+// Backward pass B:  W[b,hk,j,e] = sum_{h in group(hk)} sum_i G[b,h,i,j] Q_hat[b,h,i,e]
+// one workgroup = 128 keys x 128 expanded columns; 4 waves of 32 keys; the
+// A operand (lane <-> key j, k-slot <-> query i0 + 32*hf + t) is read from HBM
+// with coalesced 32-lane rows.
+constexpr int kBI = 64;
+
+__global__ __launch_bounds__(kThreads, 2) void sim_bwd_w_kernel(SimParams p, float* W, int njb, int nec) {
+  __shared__ float qt[kBI * kKtRow];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int ec = id % nec, jb = (id / nec) % njb, bhk = id / (nec * njb);
+  const int b = bhk / p.Hk, hk = bhk % p.Hk;
+  const int R = p.R, E = p.E, Nq = p.Nq, Nk = p.Nk, q_off = Nk - Nq;
+  const int j = jb * 128 + wave * 32 + lr;
+  const int e_base = ec * 128;
+  const int groups = p.Hq / p.Hk;
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int y = 0; y < 4; ++y)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[y][r] = 0.f;
+
+  const int trow = tid >> 2, tq = tid & 3;
+  for (int g = 0; g < groups; ++g) {
+    const int h = hk + g * p.Hk;
+    const float* gb = p.dsim + (int64_t)b * p.sim_s[0] + (int64_t)h * p.sim_s[1];
+    const float* qb = p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1];
+    const float2* tb = R ? p.qtab + (int64_t)b * p.qt_sb + (int64_t)h * p.qt_sh : nullptr;
+    for (int i0 = 0; i0 < Nq; i0 += kBI) {
+      __syncthreads();
+      {
+        const int qi = i0 + trow;
+        const bool qv = qi < Nq;
+        const float* qrow = qb + (int64_t)min(qi, Nq - 1) * p.q_s[2];
+        const float2* qtab = R ? tb + (int64_t)(q_off + min(qi, Nq - 1)) * R : nullptr;
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) {
+          float o[8];
+          expand8(qrow, qtab, e_base + 32 * tq + 8 * gg, R, E, qv, o);
+#pragma unroll
+          for (int s = 0; s < 8; ++s) qt[trow * kKtRow + 32 * tq + 8 * gg + s] = o[s];
+        }
+      }
+      __syncthreads();
+#pragma unroll 8
+      for (int t = 0; t < 32; ++t) {
+        const int ii = i0 + 32 * hf + t;
+        const float gv = (ii < Nq && j < Nk) ? gb[(int64_t)ii * p.sim_s[2] + j] : 0.f;
+        const int ir = 32 * hf + t;
+#pragma unroll
+        for (int y = 0; y < 4; ++y)
+          acc[y] = __builtin_amdgcn_mfma_f32_32x32x2f32(gv, qt[ir * kKtRow + 32 * y + lr], acc[y], 0, 0, 0);
+      }
+    }
+  }
+  float* wb = W + ((int64_t)b * p.Hk + hk) * Nk * p.EP;
+#pragma unroll
+  for (int y = 0; y < 4; ++y) {
+    const int e = e_base + 32 * y + lr;
+    if (e >= p.EP) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int jj = jb * 128 + wave * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+      if (jj < Nk) wb[(int64_t)jj * p.EP + e] = acc[y][r];
+    }
+  }
+}
+
+// Finalize: chain rule of the polar transform for one side.
+//   side 0: rows = queries of (b, h), acc = U, out = dq, phase row = q_off + i, no bias
+//   side 1: rows = keys of (b, hk), acc = W, out = dk, phase row = j, dbias accumulated
+// one workgroup = 32 rows of one (b, head); thread -> (dim lane, row group).
+__global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p, const float* acc, int side,
+                                                                     int nrb) {
+  __shared__ float red[4][256];
+  const int tid = threadIdx.x;
+  const int rb = blockIdx.x % nrb, bh = blockIdx.x / nrb;
+  const int heads = side == 0 ? p.Hq : p.Hk;
+  const int b = bh / heads, hh = bh % heads;
+  const int R = p.R, D = p.D, EP = p.EP;
+  const int rows = side == 0 ? p.Nq : p.Nk;
+  const int q_off = p.Nk - p.Nq;
+  const float* x = side == 0 ? p.q + (int64_t)b * p.q_s[0] + (int64_t)hh * p.q_s[1]
+                             : p.k + (int64_t)b * p.k_s[0] + (int64_t)hh * p.k_s[1];
+  const int64_t xs = side == 0 ? p.q_s[2] : p.k_s[2];
+  float* out = side == 0 ? p.dq + (int64_t)b * p.dq_s[0] + (int64_t)hh * p.dq_s[1]
+                         : p.dk + (int64_t)b * p.dk_s[0] + (int64_t)hh * p.dk_s[1];
+  const int64_t os = side == 0 ? p.dq_s[2] : p.dk_s[2];
+  const float2* tab = nullptr;
+  if (R) tab = side == 0 ? p.qtab + (int64_t)b * p.qt_sb + (int64_t)hh * p.qt_sh
+                         : p.ktab + (int64_t)b * p.kt_sb + (int64_t)hh * p.kt_sh;
+  const float* ab = acc + (int64_t)bh * rows * EP;
+  const int dl = tid & 63, rg = tid >> 6;
+
+  for (int d0 = 0; d0 < D; d0 += 64) {
+    const int d = d0 + dl;
+    float dpsum = 0.f;
+    for (int rr = rg; rr < 32; rr += 4) {
+      const int n = rb * 32 + rr;
+      if (n >= rows || d >= D) continue;
+      const float* arow = ab + (int64_t)n * EP;
+      if (d < R) {
+        const int prow = side == 0 ? q_off + n : n;
+        const float2 cs = tab[(int64_t)prow * R + d];
+        const float xv = x[(int64_t)n * xs + d];
+        const float uc = arow[d], us = arow[R + d];
+        out[(int64_t)n * os + d] = sigmoid_f(xv) * (cs.x * uc + cs.y * us);
+        const float dph = softplus_f(xv) * (cs.x * us - cs.y * uc);
+        if (p.dfreqs) atomicAdd(p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)hh * p.df_s[1] + (int64_t)prow * p.df_s[2] + d, dph);
+        dpsum += dph;
+      } else {
+        out[(int64_t)n * os + d] = arow[R + d];
+      }
+    }
+    if (side == 1 && p.dbias) {
+      red[rg][dl] = dpsum;
+      __syncthreads();
+      if (rg == 0 && d < R) {
+        const float s = red[0][dl] + red[1][dl] + red[2][dl] + red[3][dl];
+        atomicAdd(p.dbias + (int64_t)hh * p.bias_sh + d, s);
+      }
+      __syncthreads();
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_sim_fwd(const SimParams& p, hipStream_t s) {
+  const int nib = (p.Nq + 127) / 128, njb = (p.Nk + 127) / 128;
+  const int blocks = nib * njb * p.B * p.Hq;
+  hipLaunchKernelGGL(sim_fwd_kernel, dim3(blocks), dim3(kThreads), 0, s, p, nib, njb);
+  return hipGetLastError();
+}
+
+// Workspace for U and W follows the two tables; the ABI passes it through SimParams::dsim-adjacent
+// pointers set by the caller (see launch_sim_bwd_ws).
+hipError_t launch_sim_bwd_ws(const SimParams& p, float* U, float* W, hipStream_t s) {
+  const int nec = (p.EP + 127) / 128;
+  const int nib = (p.Nq + 127) / 128, njb = (p.Nk + 127) / 128;
+  hipLaunchKernelGGL(sim_bwd_u_kernel, dim3(nib * nec * p.B * p.Hq), dim3(kThreads), 0, s, p, U, nib, nec);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(sim_bwd_w_kernel, dim3(njb * nec * p.B * p.Hk), dim3(kThreads), 0, s, p, W, njb, nec);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const int nrq = (p.Nq + 31) / 32, nrk = (p.Nk + 31) / 32;
+  hipLaunchKernelGGL(sim_bwd_finalize_kernel, dim3(nrq * p.B * p.Hq), dim3(kThreads), 0, s, p, U, 0, nrq);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(sim_bwd_finalize_kernel, dim3(nrk * p.B * p.Hk), dim3(kThreads), 0, s, p, W, 1, nrk);
+  return hipGetLastError();
+}
+
+}  // namespace pope

@@ -1,0 +1,114 @@
+"""PoPE attention entry points: fused HIP path for GPU tensors, torch path otherwise.
+
+API mirror of the reference's ``PoPE_pytorch/attention.py``:
+``compute_attn_similarity_non_fused`` (:30-47), ``compute_attn_similarity``
+(:49-73) and ``flash_attn_with_pope`` (:75-145), with the same arguments,
+defaults, layouts (``head_dimension_at_first``), asserts and return values.
+
+Dispatch (reference :21-26, :63-71, :86): GPU tensors go to the HIP kernels of
+libpope_hip.so; if that library is missing the call raises -- there is no silent
+fallback.  The torch path (``fused=False`` or CPU tensors) is the reference's own
+non-fused computation, with the key-padding and causal masks combined into one
+explicit boolean mask so the result does not depend on the torch version's
+handling of ``attn_mask`` together with ``is_causal`` (reference :133-138).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from .pope import apply_pope_to_qk
+
+# The fused path is the HIP library; "available" means a GPU is present.  Whether
+# the library loads is checked on first use and failures raise.
+HIP_AVAILABLE = torch.cuda.is_available()
+
+
+def exists(v):
+    return v is not None
+
+
+def default(v, d):
+    return v if exists(v) else d
+
+
+def divisible_by(num, den):
+    return (num % den) == 0
+
+
+def _to_head_first(*ts):
+    return tuple(t.transpose(1, 2) for t in ts)
+
+
+def _repeat_heads(t, groups):
+    """'b h ... -> b (g h) ...': query head i reads kv head i % Hk."""
+    return t.repeat(1, groups, *([1] * (t.ndim - 2))) if groups > 1 else t
+
+
+def compute_attn_similarity_non_fused(q, k, pope, head_dimension_at_first=True):
+    if not head_dimension_at_first:
+        q, k = _to_head_first(q, k)
+    q, k = apply_pope_to_qk(pope, q, k, to_magnitude=F.softplus)
+    k = _repeat_heads(k, q.shape[1] // k.shape[1])
+    return q @ k.transpose(-1, -2)
+
+
+def compute_attn_similarity(q, k, pope, allow_tf32=True, head_dimension_at_first=True):
+    assert divisible_by(q.shape[1 if head_dimension_at_first else 2], k.shape[1 if head_dimension_at_first else 2])
+    freqs, bias = pope
+    head_dim = q.shape[-1]
+    assert head_dim in {32, 48, 64, 128, 256}, f"head_dim {head_dim} not in common sizes"
+
+    is_cuda = q.is_cuda and k.is_cuda and freqs.is_cuda and bias.is_cuda
+    if is_cuda:
+        from .hip_pope import hip_compute_qk_similarity
+        if not head_dimension_at_first:
+            q, k = _to_head_first(q, k)
+        return hip_compute_qk_similarity(q, k, freqs, bias, freqs.shape[-1], allow_tf32=allow_tf32)
+
+    return compute_attn_similarity_non_fused(q, k, pope, head_dimension_at_first=head_dimension_at_first)
+
+
+def flash_attn_with_pope(q, k, v, pos_emb=None, mask=None, causal=False, softmax_scale=None, fused=None,
+                         head_dimension_at_first=True):
+    fused = default(fused, q.is_cuda)
+    softmax_scale = default(softmax_scale, q.shape[-1] ** -0.5)
+
+    if fused:
+        from .hip_pope_flash_attn import flash_attn_head_first
+        if not head_dimension_at_first:
+            q, k, v = _to_head_first(q, k, v)
+        freqs, bias = pos_emb if exists(pos_emb) else (None, None)
+        out = flash_attn_head_first(q, k, v, freqs, bias, mask=mask, causal=causal, softmax_scale=softmax_scale)
+        if not head_dimension_at_first:
+            out = out.transpose(1, 2)
+        return out
+
+    # non-fused torch path, standardised to (batch, heads, seq, dim)
+    if not head_dimension_at_first:
+        q, k, v = _to_head_first(q, k, v)
+    if exists(pos_emb):
+        q, k = apply_pope_to_qk(pos_emb, q, k, to_magnitude=F.softplus)
+    groups = q.shape[1] // k.shape[1]
+    k, v = _repeat_heads(k, groups), _repeat_heads(v, groups)
+
+    v_dtype = v.dtype
+    if q.dtype != v.dtype:
+        v = v.to(q.dtype)
+
+    keep = None
+    if exists(mask):
+        keep = mask.bool()[:, None, None, :]
+    if causal:
+        tri = torch.ones(q.shape[-2], k.shape[-2], dtype=torch.bool, device=q.device).tril()
+        keep = tri if keep is None else keep & tri
+    out = F.scaled_dot_product_attention(q, k, v, attn_mask=keep, scale=softmax_scale)
+    if exists(keep):
+        # rows with every key masked give 0, as the fused kernels do
+        row_any = keep.any(-1, keepdim=True)
+        out = torch.where(row_any, out, torch.zeros((), dtype=out.dtype, device=out.device))
+    out = out.to(v_dtype)
+
+    if not head_dimension_at_first:
+        out = out.transpose(1, 2)
+    return out

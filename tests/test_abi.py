@@ -1,0 +1,141 @@
+"""The C ABI library on the CPU: it loads, exports every symbol include/pope_abi.h
+declares, reports workspace sizes, and rejects bad arguments on the host before
+any HIP call (so none of these tests needs or touches a GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from pope_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "pope_abi.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^int\s+(pope_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_exports():
+    assert _declared() == sorted(_lib.EXPORTS)
+
+
+def test_library_loads_and_exports_every_symbol():
+    L = _lib.lib()
+    for name in _declared():
+        assert hasattr(L, name), name
+    assert L.pope_abi_version() == _lib.ABI_VERSION
+
+
+def _desc(B=2, Hq=8, Hk=8, Nq=256, Nk=256, D=64, R=32, dtype=_lib.POPE_BF16):
+    d = _lib.PopeDesc()
+    d.B, d.Hq, d.Hk, d.Nq, d.Nk, d.D, d.R, d.dtype = B, Hq, Hk, Nq, Nk, D, R, dtype
+    d.softmax_scale = D ** -0.5
+    for f in ("q_s", "k_s", "v_s", "o_s", "do_s", "dq_s", "dk_s", "dv_s"):
+        getattr(d, f)[:] = (Hq * Nq * D, Nq * D, D)
+    d.sim_s[:] = (Hq * Nq * Nk, Nq * Nk, Nk)
+    d.f_s[:] = (0, 0, R)
+    d.bias_sh = R
+    return d
+
+
+def _ws(op, d):
+    n = ctypes.c_size_t(0)
+    st = _lib.lib().pope_workspace_bytes(op, ctypes.byref(d), ctypes.byref(n))
+    return st, n.value
+
+
+def test_workspace_sizes():
+    d = _desc()
+    st, n = _ws(_lib.OP_FLASH_FWD, d)
+    assert st == 0 and n == 256 * 32 * 8                          # cos/sin table, (Nk, R) float2
+    st, nb = _ws(_lib.OP_FLASH_BWD, d)
+    assert st == 0 and nb == n + 2 * 8 * 256 * 4 + 2 * 8 * 256 * 96 * 4  # + delta + fp32 dq accumulator
+    d3 = _desc(R=0)
+    assert _ws(_lib.OP_FLASH_FWD, d3) == (0, 0)
+    ds = _desc(dtype=_lib.POPE_F32, R=64)
+    st, n = _ws(_lib.OP_SIM_FWD, ds)
+    assert st == 0 and n == 8 * 256 * 64 * 8 + 256 * 64 * 8         # key table per kv head + query table
+
+
+def _fake(n=1 << 20):
+    # Host memory stands in for device pointers: every call below must fail in
+    # host validation, before any HIP call would dereference them.
+    return ctypes.create_string_buffer(n)
+
+
+_BUF = _fake()
+_P = ctypes.cast(_BUF, ctypes.c_void_p)
+# 256-aligned view inside the buffer
+_A = ctypes.c_void_p(((_P.value + 255) // 256) * 256)
+
+
+def _flash_fwd(d, **over):
+    args = dict(q=_A, k=_A, v=_A, freqs=_A, bias=_A, mask=None, o=_A, lse=_A, ws=_A, wsz=1 << 16)
+    args.update(over)
+    return _lib.lib().pope_flash_fwd(ctypes.byref(d), args["q"], args["k"], args["v"], args["freqs"],
+                                     args["bias"], args["mask"], args["o"], args["lse"], args["ws"],
+                                     args["wsz"], None)
+
+
+@pytest.mark.parametrize("field,value,needle", [
+    ("Hq", 6, "multiple of kv heads"),
+    ("D", 60, "multiple of 8"),
+    ("R", 72, "rotate dim"),
+    ("Nq", 512, "exceeds key length"),
+    ("B", 0, ">= 1"),
+])
+def test_flash_rejects_bad_shapes(field, value, needle):
+    d = _desc()
+    setattr(d, field, value)
+    st = _flash_fwd(d)
+    assert st != 0
+    assert needle in _lib.last_error()
+
+
+def test_flash_rejects_bad_dtype_strides_pointers_workspace():
+    d = _desc(dtype=_lib.POPE_F32)
+    assert _flash_fwd(d) == 2 and "bf16 or fp16" in _lib.last_error()
+    d = _desc(D=256, R=0)
+    assert _flash_fwd(d) == 2 and "head dim <= 128" in _lib.last_error()
+    d = _desc()
+    d.q_s[2] = 65
+    assert _flash_fwd(d) == 1 and "stride" in _lib.last_error()
+    d = _desc()
+    assert _flash_fwd(d, q=None) == 1 and "non-NULL" in _lib.last_error()
+    assert _flash_fwd(d, freqs=None) == 1 and "needs freqs and bias" in _lib.last_error()
+    assert _flash_fwd(d, k=ctypes.c_void_p(_A.value + 2)) == 1 and "aligned" in _lib.last_error()
+    assert _flash_fwd(d, ws=None) == 3 and "workspace" in _lib.last_error()
+    assert _flash_fwd(d, wsz=16) == 3 and "workspace" in _lib.last_error()
+
+
+def test_sim_and_decode_validation():
+    L = _lib.lib()
+    d = _desc(dtype=_lib.POPE_BF16)
+    st = L.pope_sim_fwd(ctypes.byref(d), _A, _A, _A, _A, _A, _A, 1 << 16, None)
+    assert st == 2 and "fp32" in _lib.last_error()
+    d = _desc(Nq=64, dtype=_lib.POPE_BF16)
+    st = L.pope_flash_decode(ctypes.byref(d), _A, _A, _A, _A, _A, None, _A, _A, _A, 1 << 16, None)
+    assert st == 2 and "16 query rows" in _lib.last_error()
+    d = _desc(dtype=_lib.POPE_F32, D=64, R=64)
+    d.bias_sh = -1
+    st = L.pope_sim_bwd(ctypes.byref(d), _A, _A, _A, _A, _A, _A, _A, None, None, _A, 1 << 16, None)
+    assert st == 1 and "negative" in _lib.last_error()
+
+
+def test_last_error_is_per_thread():
+    import threading
+    d = _desc()
+    d.D = 60
+    _flash_fwd(d)
+    seen = {}
+
+    def other():
+        seen["msg"] = _lib.last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert "multiple of 8" in _lib.last_error()
+    assert seen["msg"] == ""

@@ -1,0 +1,163 @@
+"""Flash attention with PoPE on the GPU: HIP kernels vs the CPU oracle.
+
+Tolerance (from the build's north star): max-abs error <= 2e-2 against the fp32+
+oracle run on the bf16/fp16-rounded inputs, for O, dq, dk, dv, dbias (and
+dfreqs).  The case matrix follows the reference's test_flash_attn.py:10-76
+(dtype x causal x Nq in {1, 256} x mask, B2 H4 Nk256 D64 R32, (b n h d) layout),
+plus ragged lengths, GQA, partial / full / no rotation, D = 32..128, fully
+masked rows and the reference's consistency check against the similarity path
+(test_flash_attn.py:78-110).
+"""
+import pytest
+import torch
+
+from gpu_common import make_pope_inputs, max_abs, oracle_attention
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _run(inp, causal, head_first=True, need_grads=True, scale=None):
+    import pope_amd
+    q, k, v = (inp[n].detach().clone().requires_grad_(need_grads) for n in ("q", "k", "v"))
+    freqs = inp["freqs"].detach().clone().requires_grad_(need_grads)
+    bias = inp["bias"].detach().clone().requires_grad_(need_grads)
+    R = freqs.shape[-1]
+    pos = (freqs, bias) if R > 0 else None
+    if head_first:
+        o = pope_amd.flash_attn_with_pope(q, k, v, pos_emb=pos, mask=inp["mask"], causal=causal,
+                                          softmax_scale=scale)
+    else:
+        tr = lambda t: t.transpose(1, 2).contiguous().detach().requires_grad_(need_grads)
+        qb, kb, vb = tr(q), tr(k), tr(v)
+        o = pope_amd.flash_attn_with_pope(qb, kb, vb, pos_emb=pos, mask=inp["mask"], causal=causal,
+                                          softmax_scale=scale, head_dimension_at_first=False)
+        o = o.transpose(1, 2)
+        q, k, v = qb, kb, vb
+    res = dict(o=o)
+    if need_grads:
+        do = inp["do"] if head_first else inp["do"]
+        o.backward(do)
+        g = lambda t: t.grad if head_first else t.grad.transpose(1, 2)
+        res.update(dq=g(q), dk=g(k), dv=g(v), dfreqs=freqs.grad, dbias=bias.grad)
+    return res
+
+
+def _check(res, ref, names):
+    errs = {n: max_abs(res[n], ref[n]) for n in names if res.get(n) is not None and ref.get(n) is not None}
+    print(" ".join(f"{n}={e:.2e}" for n, e in errs.items()))
+    for n, e in errs.items():
+        assert e <= TOL, f"{n} max-abs error {e:.3e} > {TOL}"
+    return errs
+
+
+# ---- the reference's case matrix: dtype x causal x Nq x mask (forward) -------------------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("seq_len_q", [1, 256])
+@pytest.mark.parametrize("has_mask", [True, False])
+def test_forward_reference_matrix(cuda, dtype, causal, seq_len_q, has_mask):
+    inp = make_pope_inputs(42, 2, 4, 4, seq_len_q, 256, 64, 32, dtype, "half" if has_mask else "none")
+    res = _run(inp, causal, head_first=False, need_grads=False)
+    ref = oracle_attention(inp, causal, grads=False)
+    _check(res, ref, ["o"])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("seq_len_q", [1, 256])
+@pytest.mark.parametrize("has_mask", [True, False])
+def test_backward_reference_matrix(cuda, dtype, causal, seq_len_q, has_mask):
+    inp = make_pope_inputs(42, 2, 4, 4, seq_len_q, 256, 64, 32, dtype, "half" if has_mask else "none")
+    res = _run(inp, causal, head_first=False)
+    ref = oracle_attention(inp, causal)
+    _check(res, ref, ["o", "dq", "dk", "dv", "dfreqs", "dbias"])
+
+
+# ---- shapes beyond the reference matrix ---------------------------------------------------------
+
+SHAPES = [
+    # B, Hq, Hk, Nq, Nk, D, R, causal, mask
+    (2, 8, 8, 384, 384, 64, 32, True, "prefix"),      # C3 pattern, small
+    (1, 4, 4, 200, 200, 64, 32, True, "random"),      # ragged tiles, random mask
+    (1, 2, 2, 77, 130, 64, 64, False, "none"),        # ragged, Nq < Nk, full rotation
+    (2, 4, 4, 256, 256, 96, 96, False, "none"),       # axial-style D = 96
+    (1, 4, 4, 128, 128, 32, 16, True, "none"),        # D = 32
+    (1, 2, 2, 192, 192, 128, 64, False, "prefix"),    # D = 128
+    (1, 8, 2, 256, 256, 64, 32, True, "prefix"),      # GQA 4:1
+    (1, 4, 4, 128, 128, 64, 0, True, "none"),         # no rotation: plain attention
+    (2, 2, 2, 64, 64, 64, 32, False, "dead_row"),     # fully masked batch row -> 0
+    (1, 2, 2, 1, 2048, 64, 64, False, "prefix"),      # single-query decode, long cache
+    (2, 2, 2, 3, 1500, 64, 32, False, "random"),      # short query block, long cache
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(str(x) for x in s))
+def test_forward_shapes(cuda, shape):
+    B, Hq, Hk, Nq, Nk, D, R, causal, mk = shape
+    inp = make_pope_inputs(7, B, Hq, Hk, Nq, Nk, D, R, torch.bfloat16, mk)
+    res = _run(inp, causal, need_grads=False)
+    ref = oracle_attention(inp, causal, grads=False)
+    _check(res, ref, ["o"])
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(str(x) for x in s))
+def test_backward_shapes(cuda, shape):
+    B, Hq, Hk, Nq, Nk, D, R, causal, mk = shape
+    inp = make_pope_inputs(11, B, Hq, Hk, Nq, Nk, D, R, torch.bfloat16, mk)
+    res = _run(inp, causal)
+    ref = oracle_attention(inp, causal)
+    _check(res, ref, ["o", "dq", "dk", "dv", "dfreqs", "dbias"])
+
+
+def test_lse_and_raw_forward(cuda):
+    from pope_amd.hip_pope_flash_attn import flash_attn_forward
+    inp = make_pope_inputs(3, 2, 4, 4, 256, 256, 64, 32, torch.bfloat16, "dead_row")
+    tr = lambda t: t.transpose(1, 2)
+    o, lse = flash_attn_forward(tr(inp["q"]), tr(inp["k"]), tr(inp["v"]), inp["freqs"], inp["bias"],
+                                inp["mask"], causal=True)
+    ref = oracle_attention(inp, True, grads=False)
+    assert max_abs(tr(o), ref["o"]) <= TOL
+    finite = torch.isfinite(ref["lse"])
+    assert torch.equal(torch.isfinite(lse.cpu()), finite)
+    assert (lse.cpu()[finite] - ref["lse"][finite]).abs().max().item() <= TOL
+
+
+def test_fp32_inputs_and_custom_scale(cuda):
+    inp = make_pope_inputs(5, 1, 4, 4, 128, 128, 64, 32, torch.float32, "prefix")
+    res = _run(inp, True, need_grads=True, scale=0.2)
+    ref = oracle_attention(inp, True, scale=0.2)
+    assert res["o"].dtype == torch.float32
+    _check(res, ref, ["o", "dq", "dk", "dv", "dbias"])
+
+
+@pytest.mark.parametrize("seq_len_q", [1, 1024])
+def test_consistent_with_similarity_path(cuda, seq_len_q):
+    """softmax(sim * scale) v from compute_attn_similarity == flash_attn_with_pope
+    (reference test_flash_attn.py:78-110, which asserts < 5e-4 with fp32 inputs)."""
+    import pope_amd
+    from pope_amd import PoPE
+    torch.manual_seed(0)
+    q = torch.randn(1, seq_len_q, 8, 64, device="cuda")
+    k = torch.randn(1, 1024, 8, 64, device="cuda")
+    v = torch.randn(1, 1024, 8, 64, device="cuda")
+    pope = PoPE(32, heads=8).cuda()(1024)
+    sim = pope_amd.compute_attn_similarity(q, k, pope, head_dimension_at_first=False)
+    attn = (sim * 64 ** -0.5).softmax(-1)
+    out_sim = torch.einsum("bhij,bhjd->bhid", attn, v.transpose(1, 2)).transpose(1, 2)
+    out = pope_amd.flash_attn_with_pope(q, k, v, pos_emb=pope, head_dimension_at_first=False)
+    # bf16 MFMA for fp32 inputs: the bound is the bf16 tolerance, not the reference's TF32 5e-4
+    assert max_abs(out, out_sim) <= TOL
+
+
+def test_readme_fused_flash_attn(cuda):
+    import pope_amd
+    pope = pope_amd.PoPE(dim=32, heads=8).cuda()
+    q = torch.randn(2, 8, 1024, 64).cuda()
+    k = torch.randn(2, 8, 1024, 64).cuda()
+    v = torch.randn(2, 8, 1024, 64).cuda()
+    mask = torch.ones((2, 1024)).bool().cuda()
+    out = pope_amd.flash_attn_with_pope(q, k, v, pos_emb=pope(1024), causal=True, mask=mask)
+    assert out.shape == (2, 8, 1024, 64)

@@ -1,0 +1,127 @@
+"""Fused PoPE similarity on the GPU: fp32 MFMA kernels vs the CPU oracle.
+
+Tolerance (from the build's north star): 1e-4 relative for fp32 similarity,
+read as ||kernel - oracle||_inf <= 1e-4 * ||oracle||_inf for S and for each
+gradient (dq, dk, dbias, dfreqs).  The oracle runs in fp32 on the same inputs
+(reproducing the reference's fl(freqs + bias) phase rounding, pope.py:56).
+Cases follow the reference's test_triton.py: multi-config incl. R = 0
+(:15-54), non-contiguous slices (:56-85), dfreqs with random freqs/bias
+(:87-109); plus GQA, ragged sizes and the README example.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import pope_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-4
+
+
+def _rel_inf(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item()
+
+
+def _case(seed, B, Hq, Hk, Nq, Nk, D, R, rand_freqs=False):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, Nq, D, generator=g)
+    k = torch.randn(B, Hk, Nk, D, generator=g)
+    if rand_freqs:
+        freqs = torch.randn(Nk, R, generator=g)
+        bias = torch.randn(Hk, R, generator=g)
+    else:
+        freqs = orc.pope_freqs(Nk, orc.inv_freqs(R)) if R else torch.empty(Nk, 0)
+        bias = torch.rand(Hk, R, generator=g) * (-2 * math.pi)
+    G = torch.randn(B, Hq, Nq, Nk, generator=g)
+    return q, k, freqs, bias, G
+
+
+def _oracle(q, k, freqs, bias, G):
+    t = [x.detach().clone().requires_grad_(True) for x in (q, k, freqs, bias)]
+    S = orc.sim_nonfused(*t)
+    (S * G).sum().backward()
+    return S.detach(), [x.grad for x in t]
+
+
+def _kernel(q, k, freqs, bias, G, slicer=None):
+    import pope_amd
+    t = [x.detach().clone().cuda().requires_grad_(True) for x in (q, k, freqs, bias)]
+    qq, kk = t[0], t[1]
+    S = pope_amd.compute_attn_similarity(qq, kk, (t[2], t[3]))
+    S.backward(G.cuda())
+    return S.detach(), [x.grad for x in t]
+
+
+def _compare(S, grads, S_ref, grads_ref, names=("dq", "dk", "dfreqs", "dbias")):
+    e = {"S": _rel_inf(S, S_ref)}
+    for n, g, r in zip(names, grads, grads_ref):
+        if r is not None and g is not None and r.numel():
+            e[n] = _rel_inf(g, r)
+    print(" ".join(f"{n}={v:.2e}" for n, v in e.items()))
+    for n, v in e.items():
+        assert v <= RTOL, f"{n}: relative error {v:.3e} > {RTOL}"
+
+
+@pytest.mark.parametrize("cfg", [
+    (1, 8, 8, 128, 128, 64, 0),      # reference test_triton.py:274-276
+    (1, 8, 8, 128, 128, 64, 32),
+    (2, 4, 4, 256, 256, 128, 64),
+    (2, 8, 8, 256, 256, 64, 64),     # C2 pattern, small
+    (1, 4, 2, 100, 300, 64, 32),     # GQA, ragged, Nq < Nk
+    (1, 2, 2, 64, 64, 256, 128),     # E = 384: several expanded-column chunks
+    (1, 2, 2, 33, 33, 48, 16),       # D = 48
+], ids=lambda c: "x".join(map(str, c)))
+def test_similarity_multi_config(cuda, cfg):
+    q, k, freqs, bias, G = _case(100, *cfg)
+    S_ref, g_ref = _oracle(q, k, freqs, bias, G)
+    S, g = _kernel(q, k, freqs, bias, G)
+    _compare(S, g, S_ref, g_ref)
+
+
+def test_similarity_non_contiguous(cuda):
+    import pope_amd
+    g = torch.Generator().manual_seed(5)
+    qf = torch.randn(1, 8, 256, 64, generator=g)
+    kf = torch.randn(1, 8, 256, 64, generator=g)
+    freqs = orc.pope_freqs(256, orc.inv_freqs(32))[:128]
+    bias = torch.rand(8, 32, generator=g) * (-2 * math.pi)
+    Gd = torch.randn(1, 8, 128, 128, generator=g)
+    q_nc, k_nc = qf[:, :, :128, :], kf[:, :, :128, :]
+    S_ref, g_ref = _oracle(q_nc, k_nc, freqs, bias, Gd)
+    qc = qf.cuda()[:, :, :128, :].detach().requires_grad_(True)
+    kc = kf.cuda()[:, :, :128, :].detach().requires_grad_(True)
+    assert not qc.is_contiguous()
+    fb = [freqs.cuda().requires_grad_(True), bias.cuda().requires_grad_(True)]
+    S = pope_amd.compute_attn_similarity(qc, kc, tuple(fb))
+    S.backward(Gd.cuda())
+    _compare(S, [qc.grad, kc.grad, fb[0].grad, fb[1].grad], S_ref, g_ref)
+
+
+def test_similarity_dfreqs_random_tables(cuda):
+    # reference test_triton.py:87-109: B1 H2 N64 D32 R16, random freqs and bias
+    q, k, freqs, bias, G = _case(9, 1, 2, 2, 64, 64, 32, 16, rand_freqs=True)
+    S_ref, g_ref = _oracle(q, k, freqs, bias, G)
+    S, g = _kernel(q, k, freqs, bias, G)
+    _compare(S, g, S_ref, g_ref)
+
+
+def test_similarity_head_dim_assert(cuda):
+    import pope_amd
+    q = torch.randn(1, 2, 8, 40, device="cuda")
+    with pytest.raises(AssertionError):
+        pope_amd.compute_attn_similarity(q, q, (torch.zeros(8, 8, device="cuda"), torch.zeros(2, 8, device="cuda")))
+
+
+def test_readme_fused_similarity(cuda):
+    import pope_amd
+    pope = pope_amd.PoPE(dim=64, heads=8).cuda()
+    pos_emb = pope(1024)
+    q = torch.randn(1, 8, 1024, 64).cuda()
+    k = torch.randn(1, 8, 1024, 64).cuda()
+    sim = pope_amd.compute_attn_similarity(q, k, pos_emb)
+    assert sim.shape == (1, 8, 1024, 1024)
+    ref = orc.sim_nonfused(q.cpu(), k.cpu(), pos_emb.freqs.cpu(), pos_emb.bias.detach().cpu())
+    assert _rel_inf(sim, ref) <= RTOL
