@@ -137,6 +137,19 @@ int pope_flash_decode(const pope_desc* desc, const void* q, const void* k, const
                       const float* freqs, const float* bias, const uint8_t* mask, void* o,
                       float* lse, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Per-kernel timing.  No counterpart in the reference (its tests print only
+ * parity diffs, tests/test_flash_attn.py:61,109).  While enabled, every kernel
+ * launch of the library is bracketed by a pair of hipEvents recorded on the
+ * stream the kernel runs on.  pope_profile_read waits for the recorded events
+ * and writes one line per kernel name, "name count total_ms min_ms max_ms",
+ * cumulative since the last pope_profile_reset.  Used by bench.py to time the
+ * dominant kernel on its own stream.
+ */
+int pope_profile_enable(int on);
+int pope_profile_read(char* buf, size_t n);
+int pope_profile_reset(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -283,8 +283,7 @@ __global__ __launch_bounds__(kFwdThreads, 2) void flash_fwd_kernel(FlashFwdParam
 template <typename T, int EP, int DV>
 hipError_t launch_t(const FlashFwdParams& p, hipStream_t s) {
   const int blocks = p.nqb * p.B * p.Hq;
-  hipLaunchKernelGGL((flash_fwd_kernel<T, EP, DV>), dim3(blocks), dim3(kFwdThreads), 0, s, p);
-  return hipGetLastError();
+  return launch_named("flash_fwd", flash_fwd_kernel<T, EP, DV>, dim3(blocks), dim3(kFwdThreads), s, p);
 }
 
 template <typename T>

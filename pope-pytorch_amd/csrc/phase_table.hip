@@ -33,8 +33,7 @@ hipError_t launch_phase_table(const TableParams& p, hipStream_t s) {
   if (total == 0) return hipSuccess;
   int64_t blocks = (total + 255) / 256;
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(phase_table_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
-  return hipGetLastError();
+  return launch_named("phase_table", phase_table_kernel, dim3((unsigned)blocks), dim3(256), s, p);
 }
 
 }  // namespace pope

@@ -102,16 +102,36 @@ int check_ws(size_t need, void* ws, size_t have) {
   return POPE_OK;
 }
 
-// Flash workspace: [table | delta | dq accumulator]  (the last two only for the backward).
+// Flash backward workspace pieces, in order after the phase table (each 256-byte aligned):
+//   Q_hat (B, Hq, NqP, EP), Q_hat^T (B, Hq, EP, NqP), dO^T (B, Hq, DV, NqP),
+//   K_hat (B, Hk, NkP, EP), K_hat^T (B, Hk, EP, NkP)   -- 16-bit elements
+//   delta (B, Hq, NqP)                                  -- fp32
+// with EP = round_up(D + R, 32), DV = round_up(D, 32), NqP / NkP = round_up(N, 128).
+struct BwdLayout {
+  int EP, DV, NqP, NkP;
+  size_t qh, qht, dot, kh, kht, delta, total;
+};
+
+BwdLayout bwd_layout(const pope_desc& d) {
+  BwdLayout L;
+  L.EP = round_up(d.D + d.R, 32);
+  L.DV = round_up(d.D, 32);
+  L.NqP = round_up(d.Nq, 128);
+  L.NkP = round_up(d.Nk, 128);
+  size_t off = geometry(d, d.Hq).table;
+  L.qh = off;    off += align_up((size_t)d.B * d.Hq * L.NqP * L.EP * 2);
+  L.qht = off;   off += align_up((size_t)d.B * d.Hq * L.NqP * L.EP * 2);
+  L.dot = off;   off += align_up((size_t)d.B * d.Hq * L.NqP * L.DV * 2);
+  L.kh = off;    off += align_up((size_t)d.B * d.Hk * L.NkP * L.EP * 2);
+  L.kht = off;   off += align_up((size_t)d.B * d.Hk * L.NkP * L.EP * 2);
+  L.delta = off; off += align_up((size_t)d.B * d.Hq * L.NqP * sizeof(float));
+  L.total = off;
+  return L;
+}
+
 size_t flash_ws(const pope_desc& d, int op) {
-  const Geo g = geometry(d, d.Hq);
-  size_t n = g.table;
-  if (op == POPE_OP_FLASH_BWD) {
-    const int EP = round_up(d.D + d.R, 32);
-    n += align_up((size_t)d.B * d.Hq * d.Nq * sizeof(float));
-    n += align_up((size_t)d.B * d.Hq * d.Nq * EP * sizeof(float));
-  }
-  return n;
+  if (op == POPE_OP_FLASH_BWD) return bwd_layout(d).total;
+  return geometry(d, d.Hq).table;
 }
 
 // Similarity workspace: [key table with bias (Bt, Hk) | query table without bias (Bt, Hqt)
@@ -252,6 +272,24 @@ extern "C" {
 
 int pope_abi_version(void) { return POPE_ABI_VERSION; }
 
+int pope_profile_enable(int on) {
+  pope::prof_enable(on);
+  return POPE_OK;
+}
+
+int pope_profile_read(char* buf, size_t n) {
+  if (!buf || n == 0) return fail(POPE_ERR_INVALID, "profile buffer is NULL");
+  const int rc = pope::prof_read(buf, n);
+  if (rc == 1) return fail(POPE_ERR_HIP, "waiting for profiling events failed");
+  if (rc == 2) return fail(POPE_ERR_INVALID, "profile buffer of %zu bytes too small", n);
+  return POPE_OK;
+}
+
+int pope_profile_reset(void) {
+  pope::prof_reset();
+  return POPE_OK;
+}
+
 int pope_last_error(char* buf, size_t n) {
   if (!buf || n == 0) return POPE_ERR_INVALID;
   std::strncpy(buf, g_err.c_str(), n - 1);
@@ -331,10 +369,9 @@ int pope_flash_bwd(const pope_desc* d, const void* dout, const void* q, const vo
   if ((rc = check_ws(flash_ws(*d, POPE_OP_FLASH_BWD), workspace, workspace_bytes))) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const Geo g = geometry(*d, d->Hq);
+  const BwdLayout L = bwd_layout(*d);
   char* ws = static_cast<char*>(workspace);
   float2* table = reinterpret_cast<float2*>(ws);
-  float* delta = reinterpret_cast<float*>(ws + g.table);
-  float* dqacc = reinterpret_cast<float*>(ws + g.table + align_up((size_t)d->B * d->Hq * d->Nq * sizeof(float)));
   if (d->R > 0) {
     hipError_t e = build_table(*d, freqs, nullptr, g.Bt, g.Ht, table, s);
     if (e != hipSuccess) return hip_fail(e, "phase table launch");
@@ -356,11 +393,18 @@ int pope_flash_bwd(const pope_desc* d, const void* dout, const void* q, const vo
   p.dv = static_cast<uint16_t*>(dv);
   p.dfreqs = dfreqs;
   p.dbias = dbias;
-  p.delta = delta;
-  p.dqacc = dqacc;
+  p.qh = reinterpret_cast<uint16_t*>(ws + L.qh);
+  p.qht = reinterpret_cast<uint16_t*>(ws + L.qht);
+  p.dot = reinterpret_cast<uint16_t*>(ws + L.dot);
+  p.kh = reinterpret_cast<uint16_t*>(ws + L.kh);
+  p.kht = reinterpret_cast<uint16_t*>(ws + L.kht);
+  p.delta = reinterpret_cast<float*>(ws + L.delta);
   p.B = d->B; p.Hq = d->Hq; p.Hk = d->Hk; p.Nq = d->Nq; p.Nk = d->Nk; p.D = d->D; p.R = d->R;
   p.E = d->D + d->R;
-  p.EP = round_up(p.E, 32);
+  p.EP = L.EP;
+  p.DV = L.DV;
+  p.NqP = L.NqP;
+  p.NkP = L.NkP;
   p.causal = d->causal != 0;
   p.has_mask = mask != nullptr;
   p.scale = d->softmax_scale;

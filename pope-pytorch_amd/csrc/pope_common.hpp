@@ -39,6 +39,7 @@ struct BF16 {
     bf16x2 v = {(__bf16)a, (__bf16)b};
     return __builtin_bit_cast(uint32_t, v);
   }
+  static __device__ __forceinline__ uint16_t bits(float a) { return __builtin_bit_cast(uint16_t, (__bf16)a); }
   static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
@@ -57,6 +58,7 @@ struct F16 {
     f16x2 v = {(_Float16)a, (_Float16)b};
     return __builtin_bit_cast(uint32_t, v);
   }
+  static __device__ __forceinline__ uint16_t bits(float a) { return __builtin_bit_cast(uint16_t, (_Float16)a); }
   static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }

@@ -5,6 +5,24 @@
 
 namespace pope {
 
+// Per-kernel timing (profile.cpp).  prof_begin returns -1 when profiling is off.
+int prof_begin(const char* name, hipStream_t s);
+void prof_end(int token, hipStream_t s);
+void prof_enable(int on);
+int prof_read(char* buf, size_t n);
+void prof_reset();
+
+// Launches `kernel`, bracketed by profiling events when profiling is on.
+template <typename... KArgs, typename... Args>
+hipError_t launch_named(const char* name, void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t s,
+                        Args... args) {
+  const int t = prof_begin(name, s);
+  hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
+  const hipError_t e = hipGetLastError();
+  prof_end(t, s);
+  return e;
+}
+
 // cos/sin of the phase table: tab[bt*t_sb + ht*t_sh + n*R + d] = (cos, sin) of
 // F[n, d] (+ bias[ht, d] when a bias is folded in), for n < rows.
 struct TableParams {
@@ -34,9 +52,14 @@ struct FlashBwdParams {
   const float2* table;       // cos/sin(F[b, h, n, d]) for n < Nk, no bias
   uint16_t* dq; uint16_t* dk; uint16_t* dv;
   float* dfreqs; float* dbias;
-  float* delta;              // (B, Hq, Nq) workspace
-  float* dqacc;              // (B, Hq, Nq, EP) fp32 workspace
-  int B, Hq, Hk, Nq, Nk, D, R, E, EP, causal, has_mask;
+  // workspace, written by the prep kernels (rows past Nq / Nk and columns past E are zero)
+  uint16_t* qh;              // (B, Hq, NqP, EP)  expanded queries Q_hat
+  uint16_t* qht;             // (B, Hq, EP, NqP)  Q_hat transposed
+  uint16_t* dot;             // (B, Hq, DV, NqP)  dO transposed
+  uint16_t* kh;              // (B, Hk, NkP, EP)  expanded keys K_hat
+  uint16_t* kht;             // (B, Hk, EP, NkP)  K_hat transposed
+  float* delta;              // (B, Hq, NqP)      rowsum(O * dO)
+  int B, Hq, Hk, Nq, Nk, D, R, E, EP, DV, NqP, NkP, causal, has_mask;
   float scale, scale_log2;
   int64_t q_s[3], k_s[3], v_s[3], o_s[3], do_s[3], dq_s[3], dk_s[3], dv_s[3], f_s[3], df_s[3];
   int64_t bias_sh, mask_sb, t_sb, t_sh;

@@ -354,8 +354,7 @@ __global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p,
 hipError_t launch_sim_fwd(const SimParams& p, hipStream_t s) {
   const int nib = (p.Nq + 127) / 128, njb = (p.Nk + 127) / 128;
   const int blocks = nib * njb * p.B * p.Hq;
-  hipLaunchKernelGGL(sim_fwd_kernel, dim3(blocks), dim3(kThreads), 0, s, p, nib, njb);
-  return hipGetLastError();
+  return launch_named("sim_fwd", sim_fwd_kernel, dim3(blocks), dim3(kThreads), s, p, nib, njb);
 }
 
 // Workspace for U and W follows the two tables; the ABI passes it through SimParams::dsim-adjacent
@@ -363,16 +362,17 @@ hipError_t launch_sim_fwd(const SimParams& p, hipStream_t s) {
 hipError_t launch_sim_bwd_ws(const SimParams& p, float* U, float* W, hipStream_t s) {
   const int nec = (p.EP + 127) / 128;
   const int nib = (p.Nq + 127) / 128, njb = (p.Nk + 127) / 128;
-  hipLaunchKernelGGL(sim_bwd_u_kernel, dim3(nib * nec * p.B * p.Hq), dim3(kThreads), 0, s, p, U, nib, nec);
-  hipError_t e = hipGetLastError();
+  hipError_t e = launch_named("sim_bwd_u", sim_bwd_u_kernel, dim3(nib * nec * p.B * p.Hq), dim3(kThreads), s, p, U,
+                              nib, nec);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(sim_bwd_w_kernel, dim3(njb * nec * p.B * p.Hk), dim3(kThreads), 0, s, p, W, njb, nec);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  e = launch_named("sim_bwd_w", sim_bwd_w_kernel, dim3(njb * nec * p.B * p.Hk), dim3(kThreads), s, p, W, njb, nec);
+  if (e != hipSuccess) return e;
   const int nrq = (p.Nq + 31) / 32, nrk = (p.Nk + 31) / 32;
-  hipLaunchKernelGGL(sim_bwd_finalize_kernel, dim3(nrq * p.B * p.Hq), dim3(kThreads), 0, s, p, U, 0, nrq);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(sim_bwd_finalize_kernel, dim3(nrk * p.B * p.Hk), dim3(kThreads), 0, s, p, W, 1, nrk);
-  return hipGetLastError();
+  e = launch_named("sim_bwd_finalize_q", sim_bwd_finalize_kernel, dim3(nrq * p.B * p.Hq), dim3(kThreads), s, p,
+                   (const float*)U, 0, nrq);
+  if (e != hipSuccess) return e;
+  return launch_named("sim_bwd_finalize_k", sim_bwd_finalize_kernel, dim3(nrk * p.B * p.Hk), dim3(kThreads), s, p,
+                      (const float*)W, 1, nrk);
 }
 
 }  // namespace pope

@@ -40,7 +40,8 @@ class PopeDesc(ctypes.Structure):
 
 EXPORTS = (
     "pope_abi_version", "pope_last_error", "pope_workspace_bytes", "pope_sim_fwd", "pope_sim_bwd",
-    "pope_flash_fwd", "pope_flash_bwd", "pope_flash_decode",
+    "pope_flash_fwd", "pope_flash_bwd", "pope_flash_decode", "pope_profile_enable", "pope_profile_read",
+    "pope_profile_reset",
 )
 
 _lib = None
@@ -66,6 +67,12 @@ def _declare(lib):
     lib.pope_flash_bwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     lib.pope_flash_decode.restype = i32
     lib.pope_flash_decode.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
+    lib.pope_profile_enable.restype = i32
+    lib.pope_profile_enable.argtypes = [i32]
+    lib.pope_profile_read.restype = i32
+    lib.pope_profile_read.argtypes = [ctypes.c_char_p, sz]
+    lib.pope_profile_reset.restype = i32
+    lib.pope_profile_reset.argtypes = []
 
 
 def lib():
@@ -128,6 +135,27 @@ def workspace(op: int, desc: PopeDesc, device) -> torch.Tensor | None:
         return None
     # torch's caching allocator returns 512-byte aligned blocks
     return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def profile_enable(on: bool = True) -> None:
+    """Bracket every kernel launch of the library with hipEvents on its stream."""
+    check(lib().pope_profile_enable(1 if on else 0), "profile enable")
+
+
+def profile_reset() -> None:
+    check(lib().pope_profile_reset(), "profile reset")
+
+
+def profile_read() -> dict:
+    """Per-kernel totals since the last reset: {name: (count, total_ms, min_ms, max_ms)}.
+    Waits for the recorded events."""
+    buf = ctypes.create_string_buffer(1 << 16)
+    check(lib().pope_profile_read(buf, len(buf)), "profile read")
+    out = {}
+    for line in buf.value.decode().splitlines():
+        name, cnt, tot, mn, mx = line.split()
+        out[name] = (int(cnt), float(tot), float(mn), float(mx))
+    return out
 
 
 def dtype_code(dtype: torch.dtype) -> int:

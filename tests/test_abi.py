@@ -51,7 +51,8 @@ def test_workspace_sizes():
     st, n = _ws(_lib.OP_FLASH_FWD, d)
     assert st == 0 and n == 256 * 32 * 8                          # cos/sin table, (Nk, R) float2
     st, nb = _ws(_lib.OP_FLASH_BWD, d)
-    assert st == 0 and nb == n + 2 * 8 * 256 * 4 + 2 * 8 * 256 * 96 * 4  # + delta + fp32 dq accumulator
+    # + Q_hat, Q_hat^T, K_hat, K_hat^T (E = 96 columns), dO^T (64 rows), delta
+    assert st == 0 and nb == n + 4 * (2 * 8 * 256 * 96 * 2) + 2 * 8 * 256 * 64 * 2 + 2 * 8 * 256 * 4
     d3 = _desc(R=0)
     assert _ws(_lib.OP_FLASH_FWD, d3) == (0, 0)
     ds = _desc(dtype=_lib.POPE_F32, R=64)
