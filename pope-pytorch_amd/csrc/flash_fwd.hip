@@ -3,27 +3,40 @@
 // Reference semantics: triton_pope_flash_attn.py:23-117 (kernel) and :222-271
 // (launcher); PyTorch path attention.py:106-145.
 //
-// Work decomposition
-//   one workgroup = 4 waves = 128 query rows of one (batch, query head);
-//   each wave owns 32 query rows; the key axis is swept in tiles of BN = 64.
-// Per key tile
-//   K is loaded, put through the polar transform and written to LDS as
-//   K_hat[key][e] (E = D + R expanded columns, see pope_common.hpp);
-//   V is written to LDS transposed, Vt[d][key].
-//   S^T = K_hat Q_hat^T runs on v_mfma_f32_32x32x16 with K_hat as the A operand
-//   (lane = key) and the wave's Q_hat, held in registers for the whole sweep,
-//   as the B operand (lane = query).  The result puts one query per lane and
-//   keys in registers, so the softmax row reductions stay in-lane (plus one
-//   swap between the two lane halves).
-//   O^T += Vt P^T reuses the probabilities straight from the S registers as
-//   the B operand (a key permutation inside each 16-key group that the Vt
-//   reads follow).
+// Two launches:
+//   fwd_prep_k : K_hat = the polar transform of the keys, written once per call
+//                as (B, Hk, NkP, EP) 16-bit rows (zero past Nk and past E);
+//   flash_fwd  : the attention sweep.
+//
+// flash_fwd work decomposition
+//   one workgroup = 8 waves = 128 query rows of one (batch, query head).  Waves
+//   0-3 (group 0) and 4-7 (group 1) own the same 128 rows, 32 per wave, and
+//   split the key axis: per iteration the workgroup stages a pair of 64-key
+//   tiles in LDS, group g takes tile 2 t + g.  Each group keeps its own online
+//   softmax state; group 1 hands (m, l, O) to group 0 through LDS at the end.
+//   The next pair of tiles is fetched into registers while the current pair is
+//   computed (LDS double-buffered when it fits the 160 KB of a CU).
+// Per tile and wave
+//   S^T = K_hat Q_hat^T on v_mfma_f32_32x32x16: A = K_hat tile rows (lane =
+//   key), B = the wave's Q_hat held in registers (lane = query).  The result
+//   has one query per lane and keys in registers, so the softmax row
+//   reductions stay in-lane (plus one swap between the two lane halves).
+//   O^T += Vt P^T reuses the probabilities straight from the S registers as the
+//   B operand (a key permutation inside each 16-key group that the Vt reads
+//   follow); V is transposed into LDS as key pairs packed per 32-bit word.
+// Scheduling
+//   blockIdx -> (query block, batch*head) with the heaviest causal blocks first
+//   and batch*head fastest, so consecutive workgroups land on different XCDs
+//   while every workgroup of one (batch, head) lands on the same XCD (the
+//   dispatcher deals workgroup ids round-robin over the 8 XCDs): its K_hat / V
+//   stay in one L2.  One workgroup per CU; twice as many workgroups as CUs keep
+//   the causal triangle balanced.
 // Phases
 //   The learned bias is moved to the query side: cos(phi - (F_j + b)) =
 //   cos((phi - b) - F_j), so Q_hat = a * (cos, sin)(F[q_off+i] - b) is computed
-//   once per workgroup with accurate sincos and K_hat = c * (cos, sin)(F_j)
-//   reads the per-call table of cos/sin(F).  Differences to the reference's
-//   fl(F_j + b) rounding are below bf16 resolution.
+//   with accurate sincos and K_hat = c * (cos, sin)(F_j) uses the per-call table
+//   of cos/sin(F).  Differences to the reference's fl(F_j + b) rounding are
+//   below bf16 resolution.
 // Masking
 //   top-left causal (key j visible to query i iff j <= i, the SDPA convention
 //   the reference uses, triton_pope_flash_attn.py:64,86-87), key padding mask
@@ -37,52 +50,94 @@ namespace pope {
 
 namespace {
 
-constexpr int kFwdBM = 128;
-constexpr int kFwdBN = 64;
-constexpr int kFwdThreads = 256;
+constexpr int kBM = 128;        // query rows per workgroup
+constexpr int kBN = 64;         // keys per tile (one tile per wave group per iteration)
+constexpr int kThreads = 512;   // 8 waves
+constexpr int kLdsMax = 160 * 1024;
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(uint16_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// ---------------------------------------------------------------------------
+// fwd_prep_k: one thread per (batch * kv head, padded key row, 8-column chunk).
+template <typename T>
+__global__ __launch_bounds__(256) void fwd_prep_k_kernel(FlashFwdParams p) {
+  const int nch = p.EP / 8;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)p.B * p.Hk * p.NkP * nch) return;
+  const int c = (int)(idx % nch);
+  const int64_t row = idx / nch;
+  const int j = (int)(row % p.NkP);
+  const int bhk = (int)(row / p.NkP);
+  const int b = bhk / p.Hk, hk = bhk % p.Hk;
+  const int R = p.R, E = p.D + p.R, e0 = 8 * c;
+  u32x4 w = {0u, 0u, 0u, 0u};
+  if (j < p.Nk && e0 < E) {
+    const bool is_cos = e0 < R, is_sin = !is_cos && e0 < 2 * R;
+    const int d0 = is_cos ? e0 : e0 - R;
+    const u32x4 raw = ld16(p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1] + (int64_t)j * p.k_s[2] + d0);
+    if (is_cos || is_sin) {
+      float x[8];
+      unpack8<T>(raw, x);
+      const float2* t = p.table + (int64_t)b * p.t_sb + (int64_t)hk * p.t_sh + (int64_t)j * R + d0;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float2 t0 = t[2 * s], t1 = t[2 * s + 1];
+        const float a0 = softplus_f(x[2 * s]), a1 = softplus_f(x[2 * s + 1]);
+        w[s] = is_cos ? T::pack2(a0 * t0.x, a1 * t1.x) : T::pack2(a0 * t0.y, a1 * t1.y);
+      }
+    } else {
+      w = raw;
+    }
+  }
+  st16(p.kh + ((int64_t)bhk * p.NkP + j) * p.EP + e0, w);
+}
+
+// ---------------------------------------------------------------------------
+template <typename T, int EP, int DV>
+struct FwdCfg {
+  static constexpr int KH = EP + 8;            // K_hat row stride (elements)
+  static constexpr int VT = 2 * kBN + 8;       // Vt row stride (elements): both tiles of a pair
+  static constexpr int BUF = (2 * kBN * KH + DV * VT) * 2;   // bytes of one staged pair
+  static constexpr int NBUF = 2 * BUF + 64 * 4 <= kLdsMax ? 2 : 1;
+  static constexpr int MERGE = 4 * 64 * (2 + 16 * (DV / 32)) * 4;   // group 1's (m, l, O) hand-off
+  static constexpr int LDS = NBUF * BUF > MERGE ? NBUF * BUF : MERGE;
+  static constexpr int KCH = 2 * kBN * (EP / 8);               // 16-byte K_hat chunks per pair
+  static constexpr int KLD = (KCH + kThreads - 1) / kThreads;  // per thread
+  static constexpr int VCH = kBN * (DV / 8);                   // key-pair x 8-dim chunks per pair
+  static constexpr int VLD = (VCH + kThreads - 1) / kThreads;
+};
 
 template <typename T, int EP, int DV>
-__global__ __launch_bounds__(kFwdThreads, 2) void flash_fwd_kernel(FlashFwdParams p) {
-  constexpr int BN = kFwdBN;
-  constexpr int KSTEPS = EP / 16;
-  constexpr int KH = EP + 8;   // K_hat row stride (elements); +8 spreads rows over LDS banks
-  constexpr int VT = BN + 4;   // Vt row stride (elements)
-  constexpr int NDB = DV / 32;
+__global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p) {
+  typedef FwdCfg<T, EP, DV> C;
+  constexpr int KS = EP / 16, NDB = DV / 32, KH = C::KH, VT = C::VT;
   typedef typename T::vec8 vec8;
 
-  __shared__ __attribute__((aligned(16))) uint16_t kh[BN * KH];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[DV * VT];
-  __shared__ uint32_t mskw[BN / 4];
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS];
+  __shared__ uint32_t mskw[2][2 * kBN / 4];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = id / p.nqb;
-  const int qb = p.nqb - 1 - (id % p.nqb);
+  const int grp = wave >> 2, wq = wave & 3;
+  const int BH = p.B * p.Hq;
+  const int bh = blockIdx.x % BH;
+  const int qb = p.nqb - 1 - (int)(blockIdx.x / BH);
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const int D = p.D, R = p.R, E = D + R, Nk = p.Nk, Nq = p.Nq;
   const int q_off = Nk - Nq;
-  const int qi = qb * kFwdBM + wave * 32 + lr;
+  const int qi = qb * kBM + wq * 32 + lr;
   const bool qvalid = qi < Nq;
 
-  // Zero the padding that the tile loops never write.
-  for (int i = tid; i < BN * (EP - E); i += kFwdThreads) {
-    int j = i / (EP - E), c = i % (EP - E);
-    kh[j * KH + E + c] = 0;
-  }
-  for (int i = tid; i < (DV - D) * VT; i += kFwdThreads) vt[D * VT + i] = 0;
-
   // ---- Q_hat for this lane's query row, in MFMA B-operand order ----------
-  vec8 qreg[KSTEPS];
+  vec8 qreg[KS];
   {
-    const uint16_t* qrow = p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + (int64_t)qi * p.q_s[2];
-    const float* frow = p.freqs ? p.freqs + (int64_t)b * p.f_s[0] + (int64_t)h * p.f_s[1] +
-                                      (int64_t)(q_off + qi) * p.f_s[2]
-                                : nullptr;
-    const float* brow = p.bias ? p.bias + (int64_t)hk * p.bias_sh : nullptr;
+    const uint16_t* qrow = p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + (int64_t)min(qi, Nq - 1) * p.q_s[2];
+    const float* frow = R ? p.freqs + (int64_t)b * p.f_s[0] + (int64_t)h * p.f_s[1] +
+                                (int64_t)(q_off + min(qi, Nq - 1)) * p.f_s[2]
+                          : nullptr;
+    const float* brow = R ? p.bias + (int64_t)hk * p.bias_sh : nullptr;
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
+    for (int kk = 0; kk < KS; ++kk) {
       const int e0 = 16 * kk + 8 * hf;
       float out[8];
       if (!qvalid || e0 >= E) {
@@ -119,145 +174,206 @@ __global__ __launch_bounds__(kFwdThreads, 2) void flash_fwd_kernel(FlashFwdParam
     for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  int kt_end = (Nk + BN - 1) / BN;
+  int nt = (Nk + kBN - 1) / kBN;
   if (p.causal) {
-    const int last_q = min(qb * kFwdBM + kFwdBM, Nq) - 1;
-    kt_end = min(kt_end, last_q / BN + 1);
+    const int last_q = min(qb * kBM + kBM, Nq) - 1;
+    nt = min(nt, last_q / kBN + 1);
   }
+  const int npair = (nt + 1) / 2;
   const int nch = D / 8;
-  const uint16_t* kbase = p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1];
-  const uint16_t* vbase = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
-  const float2* tbase = p.table ? p.table + (int64_t)b * p.t_sb + (int64_t)h * p.t_sh : nullptr;
+  const uint16_t* khg = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;
+  const uint16_t* vg = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
+  const uint8_t* mrow = p.has_mask ? p.mask + (int64_t)b * p.mask_sb : nullptr;
 
-  for (int kt = 0; kt < kt_end; ++kt) {
-    const int j0 = kt * BN;
-    __syncthreads();
-    // ---- K tile -> K_hat in LDS ------------------------------------------
-    for (int it = tid; it < BN * nch; it += kFwdThreads) {
-      const int j = it / nch, c = it - j * nch, key = j0 + j, d0 = c * 8;
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (key < Nk) raw = ld16(kbase + (int64_t)key * p.k_s[2] + d0);
-      if (d0 < R) {
-        float x[8];
-        unpack8<T>(raw, x);
-        const float4* tp = reinterpret_cast<const float4*>(tbase + (int64_t)min(key, Nk - 1) * R + d0);
-        u32x4 wc, ws;
+  // ---- staging of a pair of tiles: global -> registers -> LDS ----------------
+  u32x4 kpf[C::KLD], vpf0[C::VLD], vpf1[C::VLD];
+  uint32_t mpf = 0;
+  auto fetch = [&](int pr) {
+    const int j0 = pr * 2 * kBN;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          float4 t = tp[s];  // (cos, sin) of dims d0+2s, d0+2s+1
-          float a0 = softplus_f(x[2 * s]), a1 = softplus_f(x[2 * s + 1]);
-          wc[s] = T::pack2(a0 * t.x, a1 * t.z);
-          ws[s] = T::pack2(a0 * t.y, a1 * t.w);
-        }
-        *reinterpret_cast<u32x4*>(&kh[j * KH + d0]) = wc;
-        *reinterpret_cast<u32x4*>(&kh[j * KH + R + d0]) = ws;
-      } else {
-        *reinterpret_cast<u32x4*>(&kh[j * KH + R + d0]) = raw;
+    for (int m = 0; m < C::KLD; ++m) {
+      const int c = tid + m * kThreads;
+      if (c < C::KCH) {
+        const int row = c / (EP / 8), c8 = c % (EP / 8);
+        kpf[m] = ld16(khg + (int64_t)(j0 + row) * EP + 8 * c8);
       }
     }
-    // ---- V tile -> Vt in LDS (key pairs packed per 32-bit word) ------------
-    for (int it = tid; it < (BN / 2) * nch; it += kFwdThreads) {
-      const int pr = it / nch, c = it - pr * nch, key = j0 + 2 * pr, d0 = c * 8;
-      u32x4 r0 = {0u, 0u, 0u, 0u}, r1 = {0u, 0u, 0u, 0u};
-      if (key < Nk) r0 = ld16(vbase + (int64_t)key * p.v_s[2] + d0);
-      if (key + 1 < Nk) r1 = ld16(vbase + (int64_t)(key + 1) * p.v_s[2] + d0);
+#pragma unroll
+    for (int m = 0; m < C::VLD; ++m) {
+      const int c = tid + m * kThreads;
+      vpf0[m] = u32x4{0u, 0u, 0u, 0u};
+      vpf1[m] = u32x4{0u, 0u, 0u, 0u};
+      if (c < C::VCH) {
+        const int kp = c / (DV / 8), c8 = c % (DV / 8), key = j0 + 2 * kp;
+        if (c8 < nch) {
+          if (key < Nk) vpf0[m] = ld16(vg + (int64_t)key * p.v_s[2] + 8 * c8);
+          if (key + 1 < Nk) vpf1[m] = ld16(vg + (int64_t)(key + 1) * p.v_s[2] + 8 * c8);
+        }
+      }
+    }
+    if (tid < 2 * kBN / 4) {
+      uint32_t w = 0;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        *reinterpret_cast<uint32_t*>(&vt[(d0 + 2 * s) * VT + 2 * pr]) = u16lo(r0[s]) | (u16lo(r1[s]) << 16);
-        *reinterpret_cast<uint32_t*>(&vt[(d0 + 2 * s + 1) * VT + 2 * pr]) = u16hi(r0[s]) | (u16hi(r1[s]) << 16);
+        const int key = j0 + 4 * tid + s;
+        const bool ok = key < Nk && (!p.has_mask || mrow[key] != 0);
+        w |= ok ? (1u << (8 * s)) : 0u;
+      }
+      mpf = w;
+    }
+  };
+  auto stage = [&](int buf) {
+    uint16_t* kh = reinterpret_cast<uint16_t*>(smem + buf * C::BUF);
+    uint16_t* vt = kh + 2 * kBN * KH;
+#pragma unroll
+    for (int m = 0; m < C::KLD; ++m) {
+      const int c = tid + m * kThreads;
+      if (c < C::KCH) {
+        const int row = c / (EP / 8), c8 = c % (EP / 8);
+        st16(kh + row * KH + 8 * c8, kpf[m]);
       }
     }
-    if (tid < BN / 4) {
-      uint32_t w = 0;
-      if (p.has_mask) {
-        const uint8_t* mrow = p.mask + (int64_t)b * p.mask_sb;
+#pragma unroll
+    for (int m = 0; m < C::VLD; ++m) {
+      const int c = tid + m * kThreads;
+      if (c < C::VCH) {
+        const int kp = c / (DV / 8), c8 = c % (DV / 8), d0 = 8 * c8;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const int key = j0 + 4 * tid + s;
-          w |= (key < Nk && mrow[key]) ? (1u << (8 * s)) : 0u;
+          *reinterpret_cast<uint32_t*>(vt + (d0 + 2 * s) * VT + 2 * kp) = u16lo(vpf0[m][s]) | (u16lo(vpf1[m][s]) << 16);
+          *reinterpret_cast<uint32_t*>(vt + (d0 + 2 * s + 1) * VT + 2 * kp) =
+              u16hi(vpf0[m][s]) | (u16hi(vpf1[m][s]) << 16);
         }
-      } else {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) w |= (j0 + 4 * tid + s < Nk) ? (1u << (8 * s)) : 0u;
       }
-      mskw[tid] = w;
+    }
+    if (tid < 2 * kBN / 4) mskw[buf & (C::NBUF - 1)][tid] = mpf;
+  };
+
+  if (npair > 0) {
+    fetch(0);
+    stage(0);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < npair; ++t) {
+    const int buf = C::NBUF == 2 ? (t & 1) : 0;
+    if (t + 1 < npair) fetch(t + 1);
+
+    const int tile = 2 * t + grp;
+    if (tile < nt) {
+      const uint16_t* kh = reinterpret_cast<const uint16_t*>(smem + buf * C::BUF) + grp * kBN * KH;
+      const uint16_t* vt = reinterpret_cast<const uint16_t*>(smem + buf * C::BUF) + 2 * kBN * KH + grp * kBN;
+      const uint32_t* mw_s = &mskw[buf][grp * kBN / 4];
+      const int j0 = tile * kBN;
+
+      // ---- S^T = K_hat Q_hat^T ---------------------------------------------
+      f32x16 sacc[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+          const vec8 a = as_vec8<vec8>(ld16(kh + (32 * kb + lr) * KH + 16 * kk + 8 * hf));
+          sacc[kb] = T::mfma32(a, qreg[kk], sacc[kb]);
+        }
+      }
+      // ---- scale + masks + running max --------------------------------------
+      float mt = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t mw = mw_s[8 * kb + 2 * g + hf];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 4 * g + i;
+            const int key = j0 + 32 * kb + 8 * g + 4 * hf + i;
+            const bool ok = ((mw >> (8 * i)) & 0xffu) && (!p.causal || key <= qi);
+            const float s = ok ? sacc[kb][r] * p.scale_log2 : -INFINITY;
+            sacc[kb][r] = s;
+            mt = fmaxf(mt, s);
+          }
+        }
+      }
+      mt = fmaxf(mt, wave_shfl_xor(mt, 32));
+      if (__any(mt > -INFINITY)) {
+        const float m_new = fmaxf(m_run, mt);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        float psum = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float pr = __builtin_amdgcn_exp2f(sacc[kb][r] - m_use);
+            sacc[kb][r] = pr;
+            psum += pr;
+          }
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+
+        // ---- O^T += Vt P^T -------------------------------------------------
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int g = 0; g < 2; ++g) {
+            u32x4 pw;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) pw[s] = T::pack2(sacc[kb][8 * g + 2 * s], sacc[kb][8 * g + 2 * s + 1]);
+            const vec8 pb = as_vec8<vec8>(pw);
+            const int kc = 32 * kb + 16 * g + 4 * hf;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+              const uint16_t* vr = vt + (32 * db + lr) * VT + kc;
+              const u32x2 lo = *reinterpret_cast<const u32x2*>(vr);
+              const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 8);
+              const u32x4 aw = {lo[0], lo[1], hi[0], hi[1]};
+              oacc[db] = T::mfma32(as_vec8<vec8>(aw), pb, oacc[db]);
+            }
+          }
+        }
+      }
+    }
+
+    if (t + 1 < npair) {
+      if (C::NBUF == 1) __syncthreads();   // every wave is done with the single buffer
+      stage(C::NBUF == 2 ? buf ^ 1 : 0);
     }
     __syncthreads();
+  }
 
-    // ---- S^T = K_hat Q_hat^T ---------------------------------------------
-    f32x16 sacc[2];
+  // ---- merge group 1 into group 0, epilogue ------------------------------------
+  float* mg = reinterpret_cast<float*>(smem);
+  constexpr int MS = 2 + 16 * NDB;   // floats per lane in the hand-off
+  if (grp == 1) {
+    float* dst = mg + (wq * 64 + lane) * MS;
+    dst[0] = m_run;
+    dst[1] = l_run;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk) {
-        vec8 a = as_vec8<vec8>(*reinterpret_cast<const u32x4*>(&kh[(32 * kb + lr) * KH + 16 * kk + 8 * hf]));
-        sacc[kb] = T::mfma32(a, qreg[kk], sacc[kb]);
-      }
-    }
-    // ---- scale + masks + running max --------------------------------------
-    float mt = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const uint32_t mw = mskw[8 * kb + 2 * g + hf];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 4 * g + i;
-          const int key = j0 + 32 * kb + 8 * g + 4 * hf + i;
-          const bool ok = ((mw >> (8 * i)) & 0xffu) && (!p.causal || key <= qi);
-          const float s = ok ? sacc[kb][r] * p.scale_log2 : -INFINITY;
-          sacc[kb][r] = s;
-          mt = fmaxf(mt, s);
-        }
-      }
-    }
-    mt = fmaxf(mt, wave_shfl_xor(mt, 32));
-    if (!__any(mt > -INFINITY)) continue;  // every row of this wave masked for this tile
-    const float m_new = fmaxf(m_run, mt);
+      for (int r = 0; r < 16; ++r) dst[2 + 16 * db + r] = oacc[db][r];
+  }
+  __syncthreads();
+  if (grp == 1) return;
+  {
+    const float* src = mg + (wq * 64 + lane) * MS;
+    const float m1 = src[0], l1 = src[1];
+    const float m_new = fmaxf(m_run, m1);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    float psum = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pr = __builtin_amdgcn_exp2f(sacc[kb][r] - m_use);
-        sacc[kb][r] = pr;
-        psum += pr;
-      }
-    l_run = l_run * alpha + psum;
+    const float a0 = __builtin_amdgcn_exp2f(m_run - m_use), a1 = __builtin_amdgcn_exp2f(m1 - m_use);
+    l_run = l_run * a0 + l1 * a1;
     m_run = m_new;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-
-    // ---- O^T += Vt P^T ---------------------------------------------------
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        u32x4 pw;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) pw[s] = T::pack2(sacc[kb][8 * g + 2 * s], sacc[kb][8 * g + 2 * s + 1]);
-        const vec8 pb = as_vec8<vec8>(pw);
-        const int kc = 32 * kb + 16 * g + 4 * hf;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const uint16_t* vr = &vt[(32 * db + lr) * VT + kc];
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vr);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 8);
-          const u32x4 aw = {lo[0], lo[1], hi[0], hi[1]};
-          oacc[db] = T::mfma32(as_vec8<vec8>(aw), pb, oacc[db]);
-        }
-      }
-    }
+      for (int r = 0; r < 16; ++r) oacc[db][r] = oacc[db][r] * a0 + src[2 + 16 * db + r] * a1;
   }
-
-  // ---- epilogue -------------------------------------------------------------
   const float l = l_run + wave_shfl_xor(l_run, 32);
   const float inv = l > 0.f ? 1.f / l : 0.f;
   if (qvalid) {
@@ -282,16 +398,18 @@ __global__ __launch_bounds__(kFwdThreads, 2) void flash_fwd_kernel(FlashFwdParam
 
 template <typename T, int EP, int DV>
 hipError_t launch_t(const FlashFwdParams& p, hipStream_t s) {
+  const int64_t nprep = (int64_t)p.B * p.Hk * p.NkP * (EP / 8);
+  hipError_t e = launch_named("flash_fwd_prep_k", fwd_prep_k_kernel<T>, dim3((unsigned)((nprep + 255) / 256)),
+                              dim3(256), s, p);
+  if (e != hipSuccess) return e;
   const int blocks = p.nqb * p.B * p.Hq;
-  return launch_named("flash_fwd", flash_fwd_kernel<T, EP, DV>, dim3(blocks), dim3(kFwdThreads), s, p);
+  return launch_named("flash_fwd", flash_fwd_kernel<T, EP, DV>, dim3(blocks), dim3(kThreads), s, p);
 }
 
 template <typename T>
 hipError_t dispatch(const FlashFwdParams& p, hipStream_t s) {
-  const int DV = (p.D + 31) / 32 * 32;
-  const int EP = (p.D + p.R + 31) / 32 * 32;
 #define POPE_FWD_CASE(ep, dv) \
-  if (EP == ep && DV == dv) return launch_t<T, ep, dv>(p, s);
+  if (p.EP == ep && p.DV == dv) return launch_t<T, ep, dv>(p, s);
   POPE_FWD_CASE(32, 32) POPE_FWD_CASE(64, 32)
   POPE_FWD_CASE(64, 64) POPE_FWD_CASE(96, 64) POPE_FWD_CASE(128, 64)
   POPE_FWD_CASE(96, 96) POPE_FWD_CASE(128, 96) POPE_FWD_CASE(160, 96) POPE_FWD_CASE(192, 96)

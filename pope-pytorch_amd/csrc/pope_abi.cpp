@@ -129,9 +129,14 @@ BwdLayout bwd_layout(const pope_desc& d) {
   return L;
 }
 
+// Flash forward workspace: [phase table | K_hat (B, Hk, NkP, EP) 16-bit].
+size_t fwd_kh_bytes(const pope_desc& d) {
+  return align_up((size_t)d.B * d.Hk * round_up(d.Nk, 128) * round_up(d.D + d.R, 32) * 2);
+}
+
 size_t flash_ws(const pope_desc& d, int op) {
   if (op == POPE_OP_FLASH_BWD) return bwd_layout(d).total;
-  return geometry(d, d.Hq).table;
+  return geometry(d, d.Hq).table + fwd_kh_bytes(d);
 }
 
 // Similarity workspace: [key table with bias (Bt, Hk) | query table without bias (Bt, Hqt)
@@ -333,9 +338,13 @@ int pope_flash_fwd(const pope_desc* d, const void* q, const void* k, const void*
   p.bias = d->R > 0 ? bias : nullptr;
   p.mask = mask;
   p.table = d->R > 0 ? table : nullptr;
+  p.kh = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + g.table);
   p.o = static_cast<uint16_t*>(o);
   p.lse = lse;
   p.B = d->B; p.Hq = d->Hq; p.Hk = d->Hk; p.Nq = d->Nq; p.Nk = d->Nk; p.D = d->D; p.R = d->R;
+  p.EP = round_up(d->D + d->R, 32);
+  p.DV = round_up(d->D, 32);
+  p.NkP = round_up(d->Nk, 128);
   p.causal = d->causal != 0;
   p.has_mask = mask != nullptr;
   p.nqb = (d->Nq + 127) / 128;

@@ -37,8 +37,9 @@ struct FlashFwdParams {
   const uint16_t* q; const uint16_t* k; const uint16_t* v;
   const float* freqs; const float* bias; const uint8_t* mask;
   const float2* table;       // cos/sin(F[b, h, n, d]) for n < Nk, no bias
+  uint16_t* kh;              // (B, Hk, NkP, EP) workspace: K_hat rows, written by fwd_prep_k
   uint16_t* o; float* lse;
-  int B, Hq, Hk, Nq, Nk, D, R, causal, has_mask, nqb;
+  int B, Hq, Hk, Nq, Nk, D, R, EP, DV, NkP, causal, has_mask, nqb;
   float scale_log2;          // softmax_scale * log2(e)
   int64_t q_s[3], k_s[3], v_s[3], o_s[3], f_s[3];
   int64_t bias_sh, mask_sb, t_sb, t_sh;

@@ -48,13 +48,14 @@ def _ws(op, d):
 
 def test_workspace_sizes():
     d = _desc()
+    table = 256 * 32 * 8                                           # cos/sin table, (Nk, R) float2
     st, n = _ws(_lib.OP_FLASH_FWD, d)
-    assert st == 0 and n == 256 * 32 * 8                          # cos/sin table, (Nk, R) float2
+    assert st == 0 and n == table + 2 * 8 * 256 * 96 * 2            # + K_hat (E = 96 columns)
     st, nb = _ws(_lib.OP_FLASH_BWD, d)
     # + Q_hat, Q_hat^T, K_hat, K_hat^T (E = 96 columns), dO^T (64 rows), delta
-    assert st == 0 and nb == n + 4 * (2 * 8 * 256 * 96 * 2) + 2 * 8 * 256 * 64 * 2 + 2 * 8 * 256 * 4
-    d3 = _desc(R=0)
-    assert _ws(_lib.OP_FLASH_FWD, d3) == (0, 0)
+    assert st == 0 and nb == table + 4 * (2 * 8 * 256 * 96 * 2) + 2 * 8 * 256 * 64 * 2 + 2 * 8 * 256 * 4
+    d3 = _desc(R=0, Nk=200)                                         # no table; K_hat rows padded to 256
+    assert _ws(_lib.OP_FLASH_FWD, d3) == (0, 2 * 8 * 256 * 64 * 2)
     ds = _desc(dtype=_lib.POPE_F32, R=64)
     st, n = _ws(_lib.OP_SIM_FWD, ds)
     assert st == 0 and n == 8 * 256 * 64 * 8 + 256 * 64 * 8         # key table per kv head + query table
