@@ -41,10 +41,11 @@ MAX_PAD = 512
 def fa_flops(kind: str) -> float:
     """Algorithmic flops of one launch (FA accounting, causal = half the N^2 pairs, head dim D).
 
-    flash_fwd: 2 GEMMs (QK^T, PV); flash_bwd_dkdv: 4 (QK^T, dO V^T, P^T dO, dS^T Q);
-    flash_bwd_dq: 1 (dS K).  Together 7 * 2 * B * H * N^2 * D / 2 = 3.5 * 4 * B*H*N^2*D / 2."""
+    flash_fwd: 2 GEMMs (QK^T, PV); flash_bwd: 5 (dK/dV jobs: QK^T, dO V^T, P^T dO, dS^T Q; dQ jobs:
+    dS K -- their recomputation of QK^T and dO V^T is not counted).  Together
+    7 * 2 * B * H * N^2 * D / 2 = 3.5 * 4 * B * H * N^2 * D / 2."""
     pairs = B * H * N * N / 2
-    gemms = {"flash_fwd": 2, "flash_bwd_dkdv": 4, "flash_bwd_dq": 1}[kind]
+    gemms = {"flash_fwd": 2, "flash_bwd": 5}[kind]
     return gemms * 2 * pairs * D
 
 
@@ -164,7 +165,7 @@ def main():
     value = STEP_FLOPS / (ms * 1e-3) / 1e12
 
     # dominant kernel: largest total time among the kernels with an algorithmic flop count
-    cand = {n: kernels[n] for n in ("flash_fwd", "flash_bwd_dkdv", "flash_bwd_dq") if n in kernels}
+    cand = {n: kernels[n] for n in ("flash_fwd", "flash_bwd") if n in kernels}
     dom = max(cand, key=lambda n: cand[n][1])
     cnt, tot, _, _ = cand[dom]
     avg_s = tot / cnt * 1e-3

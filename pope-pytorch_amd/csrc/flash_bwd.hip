@@ -18,18 +18,30 @@
 // bias equals the summed key-phase derivative (the reference adds the same
 // quantity, tl.sum(dfk, 0), triton_pope_flash_attn.py:210).
 //
-// Kernels (all on the caller's stream, no atomics except dfreqs / dbias):
-//   prep_q : Q_hat rows and Q_hat^T, dO^T, delta = rowsum(O * dO) in fp32
-//   prep_k : K_hat rows and K_hat^T
-//   dkdv   : one workgroup = 128 keys (32 per wave) of one (batch, kv head);
-//            loops over the query heads of its group and the query tiles that
-//            can see its keys (causal tiles before the diagonal are skipped);
-//            epilogue applies the key-side chain rule and sums dbias.
-//   dq     : one workgroup = 128 queries (32 per wave); loops over the key
-//            tiles up to the causal diagonal; epilogue applies the query-side
-//            chain rule.  dQ needs no atomics, so the result is deterministic
-//            (the reference accumulates dq with atomics in the input dtype,
-//            triton_pope_flash_attn.py:215).
+// Launches (all on the caller's stream, no atomics except dfreqs / dbias):
+//   prep_khat  : K_hat rows (flash_fwd.hip, shared with the forward)
+//   prep_q     : Q_hat rows and delta = rowsum(O * dO) in fp32
+//   bwd_main   : one launch holding two kinds of jobs, one per workgroup of 4 waves
+//     dK/dV job: 128 keys (32 per wave) of one (batch, kv head); loops over the
+//                query heads of its group and the query tiles that can see its
+//                keys (tiles before the causal diagonal are skipped); the
+//                epilogue applies the key-side chain rule and sums dbias.
+//     dQ job   : 128 queries (32 per wave); loops over the key tiles up to the
+//                causal diagonal; the epilogue applies the query-side chain
+//                rule.  dQ needs no atomics, so dq is deterministic (the
+//                reference accumulates it with atomics in the input dtype,
+//                triton_pope_flash_attn.py:215).
+//   Causal dK/dV job r and dQ job (blocks - 1 - r) cost the same; the launch
+//   orders the pairs heaviest first, so the triangle's work balances over the
+//   CUs.  Streamed tiles are double-buffered in LDS, the next one fetched into
+//   registers while the current one is computed.
+//
+// MFMA layouts (v_mfma_f32_32x32x16, result lane = column, registers = rows
+// 8 (r / 4) + 4 half + r % 4): a result read back as an operand has, per 16-wide
+// k group, the rows [4 half, 4 half + 4) and [8 + 4 half, 12 + 4 half).  The
+// other operand of such a product is read from a row-major LDS tile with
+// ds_read_b64_tr_b16 in the same row order (lds_operand_tr), so no transposed
+// copy of any tile is ever stored.
 #include "pope_common.hpp"
 #include "pope_kernels.hpp"
 
@@ -43,23 +55,6 @@ __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_c
 __device__ __forceinline__ void st16(uint16_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
 
-// B/A operand of 8 elements gathered as two runs of 4: [p, p+4) and [p+8, p+12).
-// This is the k-slot order of a 16-wide group of a 32x32 MFMA result read back
-// as an operand (result rows 8*(r/4) + 4*half + r%4).
-__device__ __forceinline__ u32x4 ld_split8(const uint16_t* p) {
-  const u32x2 lo = *reinterpret_cast<const u32x2*>(p);
-  const u32x2 hi = *reinterpret_cast<const u32x2*>(p + 8);
-  return u32x4{lo[0], lo[1], hi[0], hi[1]};
-}
-
-template <typename T>
-__device__ __forceinline__ u32x4 pack8(const float* x) {
-  u32x4 w;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) w[s] = T::pack2(x[2 * s], x[2 * s + 1]);
-  return w;
-}
-
 // Registers [8 g, 8 g + 8) of an MFMA result, packed as an 8-element operand.
 template <typename T>
 __device__ __forceinline__ u32x4 pack8(const f32x16& x, int g) {
@@ -70,166 +65,117 @@ __device__ __forceinline__ u32x4 pack8(const f32x16& x, int g) {
 }
 
 // ---------------------------------------------------------------------------
-// prep_q: one thread per (batch, query head, padded query row).
+// prep_q: one thread per (batch * query head, padded query row, work item);
+// items [0, R/8) are rotated 8-dim chunks (one sincos per dim feeds both the
+// cos and the sin column), [R/8, D/8) pass-through chunks, then the zero
+// padding chunks up to EP, and a last item computes delta.
 template <typename T>
-__global__ __launch_bounds__(kThreads) void bwd_prep_q_kernel(FlashBwdParams p) {
-  const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (idx >= (int64_t)p.B * p.Hq * p.NqP) return;
-  const int i = (int)(idx % p.NqP);
-  const int bh = (int)(idx / p.NqP);
-  const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
+__global__ __launch_bounds__(256) void bwd_prep_q_kernel(FlashBwdParams p) {
   const int D = p.D, R = p.R, E = p.E, EP = p.EP, NqP = p.NqP;
+  const int nitem = D / 8 + (EP - E) / 8 + 1;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)p.B * p.Hq * NqP * nitem) return;
+  const int c = (int)(idx % nitem);
+  const int64_t row = idx / nitem;
+  const int i = (int)(row % NqP);
+  const int bh = (int)(row / NqP);
+  const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const bool valid = i < p.Nq;
   const int q_off = p.Nk - p.Nq;
-
-  const uint16_t* qrow = p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + (int64_t)i * p.q_s[2];
-  const float* frow = R ? p.freqs + (int64_t)b * p.f_s[0] + (int64_t)h * p.f_s[1] + (int64_t)(q_off + i) * p.f_s[2]
-                        : nullptr;
-  const float* brow = R ? p.bias + (int64_t)hk * p.bias_sh : nullptr;
   uint16_t* qh_row = p.qh + ((int64_t)bh * NqP + i) * EP;
-  uint16_t* qht_col = p.qht + (int64_t)bh * EP * NqP + i;
-  for (int e0 = 0; e0 < EP; e0 += 8) {
-    float out[8];
-    if (!valid || e0 >= E) {
+
+  if (c == nitem - 1) {   // delta = rowsum(O * dO)
+    float dl = 0.f;
+    if (valid) {
+      const uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1] + (int64_t)i * p.o_s[2];
+      const uint16_t* drow = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1] + (int64_t)i * p.do_s[2];
+      for (int d0 = 0; d0 < D; d0 += 8) {
+        float xo[8], xd[8];
+        unpack8<T>(ld16(orow + d0), xo);
+        unpack8<T>(ld16(drow + d0), xd);
 #pragma unroll
-      for (int s = 0; s < 8; ++s) out[s] = 0.f;
-    } else {
-      const bool is_cos = e0 < R, is_sin = !is_cos && e0 < 2 * R;
-      const int d0 = is_cos ? e0 : e0 - R;
-      float x[8];
-      unpack8<T>(ld16(qrow + d0), x);
-      if (is_cos || is_sin) {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          float sn, cs;
-          sincos_acc(frow[d0 + s] - brow[d0 + s], &sn, &cs);
-          out[s] = softplus_f(x[s]) * (is_cos ? cs : sn);
-        }
-      } else {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) out[s] = x[s];
+        for (int s = 0; s < 8; ++s) dl += xo[s] * xd[s];
       }
     }
-    const u32x4 w = pack8<T>(out);
-    st16(qh_row + e0, w);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      qht_col[(int64_t)(e0 + 2 * s) * NqP] = (uint16_t)u16lo(w[s]);
-      qht_col[(int64_t)(e0 + 2 * s + 1) * NqP] = (uint16_t)u16hi(w[s]);
-    }
+    p.delta[(int64_t)bh * NqP + i] = dl;
+    return;
   }
-
-  const uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1] + (int64_t)i * p.o_s[2];
-  const uint16_t* drow = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1] + (int64_t)i * p.do_s[2];
-  uint16_t* dot_col = p.dot + (int64_t)bh * p.DV * NqP + i;
-  float dl = 0.f;
-  for (int d0 = 0; d0 < p.DV; d0 += 8) {
-    u32x4 wd = zero4();
-    if (valid && d0 < D) {
-      wd = ld16(drow + d0);
-      float xo[8], xd[8];
-      unpack8<T>(ld16(orow + d0), xo);
-      unpack8<T>(wd, xd);
-#pragma unroll
-      for (int s = 0; s < 8; ++s) dl += xo[s] * xd[s];
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      dot_col[(int64_t)(d0 + 2 * s) * NqP] = (uint16_t)u16lo(wd[s]);
-      dot_col[(int64_t)(d0 + 2 * s + 1) * NqP] = (uint16_t)u16hi(wd[s]);
-    }
+  if (c >= D / 8) {   // zero padding columns [E, EP)
+    st16(qh_row + E + 8 * (c - D / 8), zero4());
+    return;
   }
-  p.delta[(int64_t)bh * NqP + i] = dl;
-}
-
-// prep_k: one thread per (batch, kv head, padded key row).
-template <typename T>
-__global__ __launch_bounds__(kThreads) void bwd_prep_k_kernel(FlashBwdParams p) {
-  const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (idx >= (int64_t)p.B * p.Hk * p.NkP) return;
-  const int j = (int)(idx % p.NkP);
-  const int bhk = (int)(idx / p.NkP);
-  const int b = bhk / p.Hk, hk = bhk % p.Hk;
-  const int R = p.R, E = p.E, EP = p.EP, NkP = p.NkP;
-  const bool valid = j < p.Nk;
-  const uint16_t* krow = p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1] + (int64_t)j * p.k_s[2];
-  const float2* trow = R ? p.table + (int64_t)b * p.t_sb + (int64_t)hk * p.t_sh + (int64_t)j * R : nullptr;
-  uint16_t* kh_row = p.kh + ((int64_t)bhk * NkP + j) * EP;
-  uint16_t* kht_col = p.kht + (int64_t)bhk * EP * NkP + j;
-  for (int e0 = 0; e0 < EP; e0 += 8) {
-    float out[8];
-    if (!valid || e0 >= E) {
-#pragma unroll
-      for (int s = 0; s < 8; ++s) out[s] = 0.f;
-    } else {
-      const bool is_cos = e0 < R, is_sin = !is_cos && e0 < 2 * R;
-      const int d0 = is_cos ? e0 : e0 - R;
-      float x[8];
-      unpack8<T>(ld16(krow + d0), x);
-      if (is_cos || is_sin) {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const float2 t = trow[d0 + s];
-          out[s] = softplus_f(x[s]) * (is_cos ? t.x : t.y);
-        }
-      } else {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) out[s] = x[s];
-      }
-    }
-    const u32x4 w = pack8<T>(out);
-    st16(kh_row + e0, w);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      kht_col[(int64_t)(e0 + 2 * s) * NkP] = (uint16_t)u16lo(w[s]);
-      kht_col[(int64_t)(e0 + 2 * s + 1) * NkP] = (uint16_t)u16hi(w[s]);
-    }
+  const int d0 = 8 * c;
+  u32x4 raw = zero4();
+  if (valid) raw = ld16(p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + (int64_t)i * p.q_s[2] + d0);
+  if (d0 >= R) {
+    st16(qh_row + R + d0, raw);
+    return;
   }
+  float x[8], oc[8], os[8];
+  unpack8<T>(raw, x);
+  const float* frow = p.freqs + (int64_t)b * p.f_s[0] + (int64_t)h * p.f_s[1] + (int64_t)(q_off + i) * p.f_s[2];
+  const float* brow = p.bias + (int64_t)hk * p.bias_sh;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    float sn = 0.f, cs = 0.f;
+    if (valid) sincos_acc(frow[d0 + s] - brow[d0 + s], &sn, &cs);
+    const float a = valid ? softplus_f(x[s]) : 0.f;
+    oc[s] = a * cs;
+    os[s] = a * sn;
+  }
+  u32x4 wc, ws;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    wc[s] = T::pack2(oc[2 * s], oc[2 * s + 1]);
+    ws[s] = T::pack2(os[2 * s], os[2 * s + 1]);
+  }
+  st16(qh_row + d0, wc);
+  st16(qh_row + R + d0, ws);
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV.  Lane roles: lane lr of wave w owns key j0 + 32 w + lr.
+template <int EP, int DV>
+struct BwdCfg {
+  static constexpr bool kBig = EP + DV > 160;
+  static constexpr int BMK = kBig ? 32 : 64;   // query tile of a dK/dV job
+  static constexpr int BNQ = kBig ? 32 : 64;   // key tile of a dQ job
+  static constexpr int MINB = kBig ? 1 : 2;
+  static constexpr int QH = EP + 8, DO = DV + 8;
+  // dK/dV stage: Q_hat tile, dO tile, lse and delta
+  static constexpr int KV_STAGE = (BMK * QH + BMK * DO) * 2 + 2 * BMK * 4;
+  // dQ stage: K_hat tile, V tile
+  static constexpr int Q_STAGE = (BNQ * QH + BNQ * DO) * 2;
+  static constexpr int STAGE = KV_STAGE > Q_STAGE ? KV_STAGE : Q_STAGE;
+  static constexpr int EPI = 32 * (EP + 1) * 4;
+  static constexpr int LDS = 2 * STAGE > EPI ? 2 * STAGE : EPI;
+};
+
+// dK / dV job.  Lane lr of wave w owns key j0 + 32 w + lr.
 //   S  = Q_hat K_hat^T : A = Q_hat tile rows (LDS), B = the lane's K_hat row (regs)
 //   dP = dO V^T        : A = dO tile rows (LDS),    B = the lane's V row (regs)
-// Both results have lane = key, registers = queries, so P and dS feed the next
-// products directly as A operands (lane = key row, k-slots = queries):
-//   dV     += P^T dO      B = dO^T  tile (LDS, [d][query])
-//   dK_hat += dS^T Q_hat  B = Q_hat^T tile (LDS, [e][query])
-template <typename T, int EP, int DV, int BM, int MINB>
-__global__ __launch_bounds__(kThreads, MINB) void bwd_dkdv_kernel(FlashBwdParams p) {
-  constexpr int BN = 128;
-  constexpr int KS = EP / 16, DS = DV / 16, EB = EP / 32, DB = DV / 32, QB = BM / 32;
-  constexpr int QH = EP + 8, QT = BM + 8, DO = DV + 8;
-  constexpr int MAIN = (BM * QH + EP * QT + BM * DO + DV * QT) * 2 + 2 * BM * 4;
-  constexpr int BS = EP + 1;
-  constexpr int EPI = 32 * BS * 4;
-  constexpr int LDS = MAIN > EPI ? MAIN : EPI;
+// Both results have lane = key, registers = queries, so P and dS are A operands
+// (lane = key row, k = queries) of
+//   dV     += P^T dO      B = dO tile read transposed
+//   dK_hat += dS^T Q_hat  B = Q_hat tile read transposed
+template <typename T, int EP, int DV>
+__device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, float* dbias_s, int kb, int bhk) {
+  typedef BwdCfg<EP, DV> C;
+  constexpr int BM = C::BMK, KS = EP / 16, DS = DV / 16, EB = EP / 32, DB = DV / 32, QB = BM / 32;
+  constexpr int QH = C::QH, DO = C::DO;
+  constexpr int QCH = BM * (EP / 8), DCH = BM * (DV / 8);
+  constexpr int QLD = (QCH + kThreads - 1) / kThreads, DLD = (DCH + kThreads - 1) / kThreads;
   typedef typename T::vec8 vec8;
 
-  __shared__ __attribute__((aligned(16))) char smem[LDS];
-  __shared__ float dbias_s[EP];
-  uint16_t* qh_s = reinterpret_cast<uint16_t*>(smem);
-  uint16_t* qht_s = qh_s + BM * QH;
-  uint16_t* do_s = qht_s + EP * QT;
-  uint16_t* dot_s = do_s + BM * DO;
-  float* lse_s = reinterpret_cast<float*>(dot_s + DV * QT);
-  float* dl_s = lse_s + BM;
-
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
-  const int nkb = p.NkP / BN;
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int kb = id % nkb, bhk = id / nkb;
   const int b = bhk / p.Hk, hk = bhk % p.Hk;
   const int D = p.D, R = p.R, Nq = p.Nq, Nk = p.Nk, NqP = p.NqP;
-  const int j0 = kb * BN;
+  const int j0 = kb * 128;
   const int kj = j0 + 32 * wave + lr;
 
   const uint8_t* mrow = p.has_mask ? p.mask + (int64_t)b * p.mask_sb : nullptr;
   const bool kvis = kj < Nk && (!p.has_mask || mrow[kj] != 0);
-
   for (int e = tid; e < EP; e += kThreads) dbias_s[e] = 0.f;
 
-  // This lane's K_hat and V rows as B operands (k-slots 16 kk + 8 hf ...).
   vec8 kreg[KS], vreg[DS];
   {
     const uint16_t* khr = p.kh + ((int64_t)bhk * p.NkP + kj) * EP;
@@ -255,87 +201,110 @@ __global__ __launch_bounds__(kThreads, MINB) void bwd_dkdv_kernel(FlashBwdParams
 
   const int any_key = __syncthreads_or(kvis ? 1 : 0);
   const int nqt = (Nq + BM - 1) / BM;
-  const int qt0 = p.causal ? j0 / BM : 0;
+  const int qt0 = p.causal ? min(j0 / BM, nqt) : 0;
   const int groups = p.Hq / p.Hk;
+  const int per_head = nqt - qt0;
+  const int nsteps = any_key ? groups * per_head : 0;
 
-  if (any_key) {
-    for (int g = 0; g < groups; ++g) {
-      const int h = hk + g * p.Hk;
-      const int bh = b * p.Hq + h;
-      const uint16_t* qh_g = p.qh + (int64_t)bh * NqP * EP;
-      const uint16_t* qht_g = p.qht + (int64_t)bh * EP * NqP;
-      const uint16_t* dot_g = p.dot + (int64_t)bh * DV * NqP;
-      const uint16_t* do_g = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1];
-      for (int qt = qt0; qt < nqt; ++qt) {
-        const int i0 = qt * BM;
-        __syncthreads();
-        for (int c = tid; c < BM * (EP / 8); c += kThreads) {
-          const int row = c / (EP / 8), c8 = c % (EP / 8);
-          st16(qh_s + row * QH + 8 * c8, ld16(qh_g + (int64_t)(i0 + row) * EP + 8 * c8));
-        }
-        for (int c = tid; c < EP * (BM / 8); c += kThreads) {
-          const int e = c / (BM / 8), c8 = c % (BM / 8);
-          st16(qht_s + e * QT + 8 * c8, ld16(qht_g + (int64_t)e * NqP + i0 + 8 * c8));
-        }
-        for (int c = tid; c < BM * (DV / 8); c += kThreads) {
-          const int row = c / (DV / 8), c8 = c % (DV / 8);
-          u32x4 w = zero4();
-          if (i0 + row < Nq && 8 * c8 < D) w = ld16(do_g + (int64_t)(i0 + row) * p.do_s[2] + 8 * c8);
-          st16(do_s + row * DO + 8 * c8, w);
-        }
-        for (int c = tid; c < DV * (BM / 8); c += kThreads) {
-          const int d = c / (BM / 8), c8 = c % (BM / 8);
-          st16(dot_s + d * QT + 8 * c8, ld16(dot_g + (int64_t)d * NqP + i0 + 8 * c8));
-        }
-        if (tid < BM) {
-          const int i = i0 + tid;
-          const float l = i < Nq ? p.lse[(int64_t)bh * Nq + i] : -INFINITY;
-          lse_s[tid] = l == -INFINITY ? INFINITY : l * kLog2e;
-          dl_s[tid] = p.delta[(int64_t)bh * NqP + i];
-        }
-        __syncthreads();
-
+  // staging of one query tile: global -> registers -> LDS
+  u32x4 qpf[QLD], dpf[DLD];
+  float lpf = 0.f, dlpf = 0.f;
+  auto fetch = [&](int st) {
+    const int g = st / per_head, qt = qt0 + st % per_head;
+    const int h = hk + g * p.Hk, bh = b * p.Hq + h, i0 = qt * BM;
+    const uint16_t* qh_g = p.qh + ((int64_t)bh * NqP + i0) * EP;
+    const uint16_t* do_g = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1];
 #pragma unroll
-        for (int qs = 0; qs < QB; ++qs) {
-          f32x16 s, dp;
+    for (int m = 0; m < QLD; ++m) {
+      const int c = tid + m * kThreads;
+      if (c < QCH) qpf[m] = ld16(qh_g + (int64_t)(c / (EP / 8)) * EP + 8 * (c % (EP / 8)));
+    }
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            s[r] = 0.f;
-            dp[r] = 0.f;
-          }
-#pragma unroll
-          for (int kk = 0; kk < KS; ++kk) {
-            const vec8 a = as_vec8<vec8>(ld16(qh_s + (32 * qs + lr) * QH + 16 * kk + 8 * hf));
-            s = T::mfma32(a, kreg[kk], s);
-          }
-#pragma unroll
-          for (int kk = 0; kk < DS; ++kk) {
-            const vec8 a = as_vec8<vec8>(ld16(do_s + (32 * qs + lr) * DO + 16 * kk + 8 * hf));
-            dp = T::mfma32(a, vreg[kk], dp);
-          }
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int qr = 32 * qs + 8 * (r >> 2) + 4 * hf + (r & 3);
-            const bool vis = kvis && (!p.causal || kj <= i0 + qr);
-            const float pv = vis ? __builtin_amdgcn_exp2f(fmaf(s[r], p.scale_log2, -lse_s[qr])) : 0.f;
-            s[r] = pv;
-            dp[r] = pv * (dp[r] - dl_s[qr]);
-          }
-#pragma unroll
-          for (int g2 = 0; g2 < 2; ++g2) {
-            const vec8 ap = as_vec8<vec8>(pack8<T>(s, g2));
-            const vec8 ads = as_vec8<vec8>(pack8<T>(dp, g2));
-            const int col = 32 * qs + 16 * g2 + 4 * hf;
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-              dva[db] = T::mfma32(ap, as_vec8<vec8>(ld_split8(dot_s + (32 * db + lr) * QT + col)), dva[db]);
-#pragma unroll
-            for (int eb = 0; eb < EB; ++eb)
-              dka[eb] = T::mfma32(ads, as_vec8<vec8>(ld_split8(qht_s + (32 * eb + lr) * QT + col)), dka[eb]);
-          }
-        }
+    for (int m = 0; m < DLD; ++m) {
+      const int c = tid + m * kThreads;
+      dpf[m] = zero4();
+      if (c < DCH) {
+        const int row = c / (DV / 8), c8 = c % (DV / 8);
+        if (i0 + row < Nq && 8 * c8 < D) dpf[m] = ld16(do_g + (int64_t)(i0 + row) * p.do_s[2] + 8 * c8);
       }
     }
+    if (tid < BM) {
+      const int i = i0 + tid;
+      const float l = i < Nq ? p.lse[(int64_t)bh * Nq + i] : -INFINITY;
+      lpf = l == -INFINITY ? INFINITY : l * kLog2e;
+      dlpf = p.delta[(int64_t)bh * NqP + i];
+    }
+  };
+  auto stage = [&](int buf) {
+    uint16_t* qh_s = reinterpret_cast<uint16_t*>(smem + buf * C::STAGE);
+    uint16_t* do_s = qh_s + BM * QH;
+    float* lse_s = reinterpret_cast<float*>(do_s + BM * DO);
+#pragma unroll
+    for (int m = 0; m < QLD; ++m) {
+      const int c = tid + m * kThreads;
+      if (c < QCH) st16(qh_s + (c / (EP / 8)) * QH + 8 * (c % (EP / 8)), qpf[m]);
+    }
+#pragma unroll
+    for (int m = 0; m < DLD; ++m) {
+      const int c = tid + m * kThreads;
+      if (c < DCH) st16(do_s + (c / (DV / 8)) * DO + 8 * (c % (DV / 8)), dpf[m]);
+    }
+    if (tid < BM) {
+      lse_s[tid] = lpf;
+      lse_s[BM + tid] = dlpf;
+    }
+  };
+
+  if (nsteps > 0) {
+    fetch(0);
+    stage(0);
+  }
+  __syncthreads();
+  for (int st = 0; st < nsteps; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nsteps) fetch(st + 1);
+    const int i0 = (qt0 + st % per_head) * BM;
+    const uint16_t* qh_s = reinterpret_cast<const uint16_t*>(smem + buf * C::STAGE);
+    const uint16_t* do_s = qh_s + BM * QH;
+    const float* lse_s = reinterpret_cast<const float*>(do_s + BM * DO);
+    const float* dl_s = lse_s + BM;
+#pragma unroll
+    for (int qs = 0; qs < QB; ++qs) {
+      f32x16 s, dp;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] = 0.f;
+        dp[r] = 0.f;
+      }
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk)
+        s = T::mfma32(as_vec8<vec8>(ld16(qh_s + (32 * qs + lr) * QH + 16 * kk + 8 * hf)), kreg[kk], s);
+#pragma unroll
+      for (int kk = 0; kk < DS; ++kk)
+        dp = T::mfma32(as_vec8<vec8>(ld16(do_s + (32 * qs + lr) * DO + 16 * kk + 8 * hf)), vreg[kk], dp);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qr = 32 * qs + 8 * (r >> 2) + 4 * hf + (r & 3);
+        const bool vis = kvis && (!p.causal || kj <= i0 + qr);
+        const float pv = vis ? __builtin_amdgcn_exp2f(fmaf(s[r], p.scale_log2, -lse_s[qr])) : 0.f;
+        s[r] = pv;
+        dp[r] = pv * (dp[r] - dl_s[qr]);
+      }
+#pragma unroll
+      for (int g2 = 0; g2 < 2; ++g2) {
+        const vec8 ap = as_vec8<vec8>(pack8<T>(s, g2));
+        const vec8 ads = as_vec8<vec8>(pack8<T>(dp, g2));
+        const int ra = 32 * qs + 16 * g2 + 4 * hf;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          dva[db] = T::mfma32(ap, as_vec8<vec8>(lds_operand_tr(do_s, DO, ra, ra + 8, 32 * db, lane)), dva[db]);
+#pragma unroll
+        for (int eb = 0; eb < EB; ++eb)
+          dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_operand_tr(qh_s, QH, ra, ra + 8, 32 * eb, lane)), dka[eb]);
+      }
+    }
+    if (st + 1 < nsteps) stage(buf ^ 1);
+    __syncthreads();
   }
 
   // ---- dV: lane = d column, registers = the wave's keys -----------------------
@@ -353,7 +322,8 @@ __global__ __launch_bounds__(kThreads, MINB) void bwd_dkdv_kernel(FlashBwdParams
   }
 
   // ---- dK: key-side chain rule, one wave's 32 keys at a time through LDS -------
-  float* buf = reinterpret_cast<float*>(smem);
+  constexpr int BS = EP + 1;
+  float* ebuf = reinterpret_cast<float*>(smem);
   const uint16_t* kb_ptr = p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1];
   uint16_t* dkb = p.dk + (int64_t)b * p.dk_s[0] + (int64_t)hk * p.dk_s[1];
   const float2* tb = R ? p.table + (int64_t)b * p.t_sb + (int64_t)hk * p.t_sh : nullptr;
@@ -364,14 +334,14 @@ __global__ __launch_bounds__(kThreads, MINB) void bwd_dkdv_kernel(FlashBwdParams
 #pragma unroll
       for (int eb = 0; eb < EB; ++eb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) buf[(8 * (r >> 2) + 4 * hf + (r & 3)) * BS + 32 * eb + lr] = dka[eb][r];
+        for (int r = 0; r < 16; ++r) ebuf[(8 * (r >> 2) + 4 * hf + (r & 3)) * BS + 32 * eb + lr] = dka[eb][r];
     }
     __syncthreads();
     for (int it = tid; it < 32 * D; it += kThreads) {
       const int kr = it / D, d = it - kr * D;
       const int key = j0 + 32 * w + kr;
       if (key >= Nk) continue;
-      const float* row = buf + kr * BS;
+      const float* row = ebuf + kr * BS;
       float g;
       if (d < R) {
         const float x = T::to_float(kb_ptr[(int64_t)key * p.k_s[2] + d]);
@@ -393,38 +363,27 @@ __global__ __launch_bounds__(kThreads, MINB) void bwd_dkdv_kernel(FlashBwdParams
   }
 }
 
-// ---------------------------------------------------------------------------
-// dQ.  Lane roles: lane lr of wave w owns query i0 + 32 w + lr.
+// dQ job.  Lane lr of wave w owns query i0 + 32 w + lr.
 //   S^T  = K_hat Q_hat^T : A = K_hat tile rows (LDS), B = the lane's Q_hat row (regs)
 //   dP^T = V dO^T        : A = V tile rows (LDS),     B = the lane's dO row (regs)
-// Results: lane = query, registers = keys; dS^T feeds dQ_hat^T = K_hat^T dS^T
-// as the B operand, with A = K_hat^T tile (LDS, [e][key]).
-template <typename T, int EP, int DV, int BN, int MINB>
-__global__ __launch_bounds__(kThreads, MINB) void bwd_dq_kernel(FlashBwdParams p) {
-  constexpr int BM = 128;
-  constexpr int KS = EP / 16, DS = DV / 16, EB = EP / 32, NB = BN / 32;
-  constexpr int KH = EP + 8, KT = BN + 8, VR = DV + 8;
-  constexpr int MAIN = (BN * KH + EP * KT + BN * VR) * 2;
-  constexpr int BS = EP + 1;
-  constexpr int EPI = 32 * BS * 4;
-  constexpr int LDS = MAIN > EPI ? MAIN : EPI;
+// Results: lane = query, registers = keys; dS^T is the B operand of
+//   dQ_hat^T += K_hat^T dS^T   A = K_hat tile read transposed.
+template <typename T, int EP, int DV>
+__device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint8_t (*msk_s)[64], int qb,
+                                       int bh) {
+  typedef BwdCfg<EP, DV> C;
+  constexpr int BN = C::BNQ, KS = EP / 16, DS = DV / 16, EB = EP / 32, NB = BN / 32;
+  constexpr int KH = C::QH, VR = C::DO;
+  constexpr int KCH = BN * (EP / 8), VCH = BN * (DV / 8);
+  constexpr int KLD = (KCH + kThreads - 1) / kThreads, VLD = (VCH + kThreads - 1) / kThreads;
   typedef typename T::vec8 vec8;
 
-  __shared__ __attribute__((aligned(16))) char smem[LDS];
-  __shared__ uint8_t msk_s[BN];
-  uint16_t* kh_s = reinterpret_cast<uint16_t*>(smem);
-  uint16_t* kht_s = kh_s + BN * KH;
-  uint16_t* v_s = kht_s + EP * KT;
-
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
-  const int nqb = p.NqP / BM;
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int qb = nqb - 1 - (id % nqb), bh = id / nqb;
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const int bhk = b * p.Hk + hk;
   const int D = p.D, R = p.R, Nq = p.Nq, Nk = p.Nk, NkP = p.NkP;
   const int q_off = Nk - Nq;
-  const int qi = qb * BM + 32 * wave + lr;
+  const int qi = qb * 128 + 32 * wave + lr;
   const bool qvalid = qi < Nq;
 
   vec8 qreg[KS], doreg[DS];
@@ -453,41 +412,66 @@ __global__ __launch_bounds__(kThreads, MINB) void bwd_dq_kernel(FlashBwdParams p
 #pragma unroll
     for (int r = 0; r < 16; ++r) dqa[x][r] = 0.f;
 
-  int kt_end = (Nk + BN - 1) / BN;
+  int nt = (Nk + BN - 1) / BN;
   if (p.causal) {
-    const int last_q = min(qb * BM + BM, Nq) - 1;
-    kt_end = last_q < 0 ? 0 : min(kt_end, last_q / BN + 1);
+    const int last_q = min(qb * 128 + 128, Nq) - 1;
+    nt = last_q < 0 ? 0 : min(nt, last_q / BN + 1);
   }
   const uint16_t* kh_g = p.kh + (int64_t)bhk * NkP * EP;
-  const uint16_t* kht_g = p.kht + (int64_t)bhk * EP * NkP;
   const uint16_t* v_g = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
   const uint8_t* mrow = p.has_mask ? p.mask + (int64_t)b * p.mask_sb : nullptr;
 
-  for (int kt = 0; kt < kt_end; ++kt) {
+  u32x4 kpf[KLD], vpf[VLD];
+  uint8_t mpf = 0;
+  auto fetch = [&](int kt) {
     const int j0 = kt * BN;
-    __syncthreads();
-    for (int c = tid; c < BN * (EP / 8); c += kThreads) {
-      const int row = c / (EP / 8), c8 = c % (EP / 8);
-      st16(kh_s + row * KH + 8 * c8, ld16(kh_g + (int64_t)(j0 + row) * EP + 8 * c8));
+#pragma unroll
+    for (int m = 0; m < KLD; ++m) {
+      const int c = tid + m * kThreads;
+      if (c < KCH) kpf[m] = ld16(kh_g + (int64_t)(j0 + c / (EP / 8)) * EP + 8 * (c % (EP / 8)));
     }
-    for (int c = tid; c < EP * (BN / 8); c += kThreads) {
-      const int e = c / (BN / 8), c8 = c % (BN / 8);
-      st16(kht_s + e * KT + 8 * c8, ld16(kht_g + (int64_t)e * NkP + j0 + 8 * c8));
+#pragma unroll
+    for (int m = 0; m < VLD; ++m) {
+      const int c = tid + m * kThreads;
+      vpf[m] = zero4();
+      if (c < VCH) {
+        const int row = c / (DV / 8), c8 = c % (DV / 8);
+        if (j0 + row < Nk && 8 * c8 < D) vpf[m] = ld16(v_g + (int64_t)(j0 + row) * p.v_s[2] + 8 * c8);
+      }
     }
-    for (int c = tid; c < BN * (DV / 8); c += kThreads) {
-      const int row = c / (DV / 8), c8 = c % (DV / 8);
-      u32x4 w = zero4();
-      if (j0 + row < Nk && 8 * c8 < D) w = ld16(v_g + (int64_t)(j0 + row) * p.v_s[2] + 8 * c8);
-      st16(v_s + row * VR + 8 * c8, w);
-    }
-    int vis = 0;
     if (tid < BN) {
       const int key = j0 + tid;
-      vis = key < Nk && (!p.has_mask || mrow[key] != 0);
-      msk_s[tid] = (uint8_t)vis;
+      mpf = (key < Nk && (!p.has_mask || mrow[key] != 0)) ? 1 : 0;
     }
-    if (!__syncthreads_or(vis)) continue;   // every key of this tile masked
+  };
+  auto stage = [&](int buf) {
+    uint16_t* kh_s = reinterpret_cast<uint16_t*>(smem + buf * C::STAGE);
+    uint16_t* v_s = kh_s + BN * KH;
+#pragma unroll
+    for (int m = 0; m < KLD; ++m) {
+      const int c = tid + m * kThreads;
+      if (c < KCH) st16(kh_s + (c / (EP / 8)) * KH + 8 * (c % (EP / 8)), kpf[m]);
+    }
+#pragma unroll
+    for (int m = 0; m < VLD; ++m) {
+      const int c = tid + m * kThreads;
+      if (c < VCH) st16(v_s + (c / (DV / 8)) * VR + 8 * (c % (DV / 8)), vpf[m]);
+    }
+    if (tid < BN) msk_s[buf][tid] = mpf;
+  };
 
+  if (nt > 0) {
+    fetch(0);
+    stage(0);
+  }
+  __syncthreads();
+  for (int kt = 0; kt < nt; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nt) fetch(kt + 1);
+    const int j0 = kt * BN;
+    const uint16_t* kh_s = reinterpret_cast<const uint16_t*>(smem + buf * C::STAGE);
+    const uint16_t* v_s = kh_s + BN * KH;
+    const uint8_t* mk = msk_s[buf];
 #pragma unroll
     for (int ks = 0; ks < NB; ++ks) {
       f32x16 s, dp;
@@ -497,35 +481,34 @@ __global__ __launch_bounds__(kThreads, MINB) void bwd_dq_kernel(FlashBwdParams p
         dp[r] = 0.f;
       }
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        const vec8 a = as_vec8<vec8>(ld16(kh_s + (32 * ks + lr) * KH + 16 * kk + 8 * hf));
-        s = T::mfma32(a, qreg[kk], s);
-      }
+      for (int kk = 0; kk < KS; ++kk)
+        s = T::mfma32(as_vec8<vec8>(ld16(kh_s + (32 * ks + lr) * KH + 16 * kk + 8 * hf)), qreg[kk], s);
 #pragma unroll
-      for (int kk = 0; kk < DS; ++kk) {
-        const vec8 a = as_vec8<vec8>(ld16(v_s + (32 * ks + lr) * VR + 16 * kk + 8 * hf));
-        dp = T::mfma32(a, doreg[kk], dp);
-      }
+      for (int kk = 0; kk < DS; ++kk)
+        dp = T::mfma32(as_vec8<vec8>(ld16(v_s + (32 * ks + lr) * VR + 16 * kk + 8 * hf)), doreg[kk], dp);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int kr = 32 * ks + 8 * (r >> 2) + 4 * hf + (r & 3);
-        const bool ok = msk_s[kr] && (!p.causal || j0 + kr <= qi);
+        const bool ok = mk[kr] && (!p.causal || j0 + kr <= qi);
         const float pv = ok ? __builtin_amdgcn_exp2f(fmaf(s[r], p.scale_log2, -lse2)) : 0.f;
         dp[r] = pv * (dp[r] - dl);
       }
 #pragma unroll
       for (int g2 = 0; g2 < 2; ++g2) {
         const vec8 bds = as_vec8<vec8>(pack8<T>(dp, g2));
-        const int col = 32 * ks + 16 * g2 + 4 * hf;
+        const int ra = 32 * ks + 16 * g2 + 4 * hf;
 #pragma unroll
         for (int eb = 0; eb < EB; ++eb)
-          dqa[eb] = T::mfma32(as_vec8<vec8>(ld_split8(kht_s + (32 * eb + lr) * KT + col)), bds, dqa[eb]);
+          dqa[eb] = T::mfma32(as_vec8<vec8>(lds_operand_tr(kh_s, KH, ra, ra + 8, 32 * eb, lane)), bds, dqa[eb]);
       }
     }
+    if (kt + 1 < nt) stage(buf ^ 1);
+    __syncthreads();
   }
 
   // ---- dQ: query-side chain rule, one wave's 32 queries at a time through LDS ----
-  float* buf = reinterpret_cast<float*>(smem);
+  constexpr int BS = EP + 1;
+  float* ebuf = reinterpret_cast<float*>(smem);
   const uint16_t* qb_ptr = p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1];
   uint16_t* dqb = p.dq + (int64_t)b * p.dq_s[0] + (int64_t)h * p.dq_s[1];
   const float* fb = R ? p.freqs + (int64_t)b * p.f_s[0] + (int64_t)h * p.f_s[1] : nullptr;
@@ -537,14 +520,14 @@ __global__ __launch_bounds__(kThreads, MINB) void bwd_dq_kernel(FlashBwdParams p
 #pragma unroll
       for (int eb = 0; eb < EB; ++eb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) buf[lr * BS + 32 * eb + 8 * (r >> 2) + 4 * hf + (r & 3)] = dqa[eb][r];
+        for (int r = 0; r < 16; ++r) ebuf[lr * BS + 32 * eb + 8 * (r >> 2) + 4 * hf + (r & 3)] = dqa[eb][r];
     }
     __syncthreads();
     for (int it = tid; it < 32 * D; it += kThreads) {
       const int qr = it / D, d = it - qr * D;
-      const int i = qb * BM + 32 * w + qr;
+      const int i = qb * 128 + 32 * w + qr;
       if (i >= Nq) continue;
-      const float* row = buf + qr * BS;
+      const float* row = ebuf + qr * BS;
       float g;
       if (d < R) {
         const float x = T::to_float(qb_ptr[(int64_t)i * p.q_s[2] + d]);
@@ -562,23 +545,61 @@ __global__ __launch_bounds__(kThreads, MINB) void bwd_dq_kernel(FlashBwdParams p
 }
 
 template <typename T, int EP, int DV>
-hipError_t launch_t(const FlashBwdParams& p, hipStream_t s) {
-  constexpr bool kBig = EP + DV > 160;
-  constexpr int BMK = kBig ? 32 : 64;   // query tile of the dK/dV kernel
-  constexpr int BNQ = kBig ? 32 : 64;   // key tile of the dQ kernel
-  constexpr int MINB = kBig ? 1 : 2;
-  const int64_t nq = (int64_t)p.B * p.Hq * p.NqP, nk = (int64_t)p.B * p.Hk * p.NkP;
-  hipError_t e = launch_named("flash_bwd_prep_q", bwd_prep_q_kernel<T>,
-                              dim3((unsigned)((nq + kThreads - 1) / kThreads)), dim3(kThreads), s, p);
+__global__ __launch_bounds__(kThreads, (BwdCfg<EP, DV>::MINB)) void bwd_main_kernel(FlashBwdParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[BwdCfg<EP, DV>::LDS];
+  __shared__ float dbias_s[EP];
+  __shared__ uint8_t msk_s[2][64];
+  const int nqb = p.NqP / 128;
+  const int id = blockIdx.x;
+  int kind, blk, head;   // kind 0 = dK/dV job (head = b * Hk + hk), 1 = dQ job (head = b * Hq + h)
+  if (p.interleave) {
+    // pairs of equal cost, heaviest first: dK/dV block r with dQ block nqb - 1 - r; the
+    // batch * head index is fastest so that one head's jobs share an XCD (workgroup ids are
+    // dealt round-robin over the 8 XCDs)
+    const int BH = p.B * p.Hq;
+    const int r = id / (2 * BH), rem = id % (2 * BH);
+    kind = rem / BH;
+    head = rem % BH;
+    blk = kind == 0 ? r : nqb - 1 - r;
+  } else if (id < p.n_kv_jobs) {
+    const int BHk = p.B * p.Hk;
+    kind = 0;
+    blk = id / BHk;
+    head = id % BHk;
+  } else {
+    const int BH = p.B * p.Hq, j = id - p.n_kv_jobs;
+    kind = 1;
+    blk = p.causal ? nqb - 1 - j / BH : j / BH;
+    head = j % BH;
+  }
+  if (kind == 0)
+    dkdv_job<T, EP, DV>(p, smem, dbias_s, blk, head);
+  else
+    dq_job<T, EP, DV>(p, smem, msk_s, blk, head);
+}
+
+template <typename T, int EP, int DV>
+hipError_t launch_t(const FlashBwdParams& p0, hipStream_t s) {
+  FlashBwdParams p = p0;
+  KhatParams kp;
+  kp.k = p.k;
+  kp.k_s[0] = p.k_s[0]; kp.k_s[1] = p.k_s[1]; kp.k_s[2] = p.k_s[2];
+  kp.table = p.table;
+  kp.t_sb = p.t_sb;
+  kp.t_sh = p.t_sh;
+  kp.kh = p.kh;
+  kp.B = p.B; kp.Hk = p.Hk; kp.Nk = p.Nk; kp.NkP = p.NkP; kp.D = p.D; kp.R = p.R; kp.EP = EP;
+  hipError_t e = launch_prep_khat(kp, T::kCode, s);
   if (e != hipSuccess) return e;
-  e = launch_named("flash_bwd_prep_k", bwd_prep_k_kernel<T>, dim3((unsigned)((nk + kThreads - 1) / kThreads)),
-                   dim3(kThreads), s, p);
+  const int nitem = p.D / 8 + (EP - p.E) / 8 + 1;
+  const int64_t nq = (int64_t)p.B * p.Hq * p.NqP * nitem;
+  e = launch_named("flash_bwd_prep_q", bwd_prep_q_kernel<T>, dim3((unsigned)((nq + 255) / 256)), dim3(256), s, p);
   if (e != hipSuccess) return e;
-  e = launch_named("flash_bwd_dkdv", bwd_dkdv_kernel<T, EP, DV, BMK, MINB>, dim3((p.NkP / 128) * p.B * p.Hk),
-                   dim3(kThreads), s, p);
-  if (e != hipSuccess) return e;
-  return launch_named("flash_bwd_dq", bwd_dq_kernel<T, EP, DV, BNQ, MINB>, dim3((p.NqP / 128) * p.B * p.Hq),
-                      dim3(kThreads), s, p);
+  const int nkb = p.NkP / 128, nqb = p.NqP / 128;
+  p.n_kv_jobs = nkb * p.B * p.Hk;
+  p.interleave = p.causal && p.Hq == p.Hk && nkb == nqb && p.Nq == p.Nk;
+  const int jobs = p.n_kv_jobs + nqb * p.B * p.Hq;
+  return launch_named("flash_bwd", bwd_main_kernel<T, EP, DV>, dim3(jobs), dim3(kThreads), s, p);
 }
 
 template <typename T>

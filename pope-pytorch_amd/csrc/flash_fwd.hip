@@ -59,9 +59,9 @@ __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_c
 __device__ __forceinline__ void st16(uint16_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
 // ---------------------------------------------------------------------------
-// fwd_prep_k: one thread per (batch * kv head, padded key row, 8-column chunk).
+// prep_khat: one thread per (batch * kv head, padded key row, 8-column chunk).
 template <typename T>
-__global__ __launch_bounds__(256) void fwd_prep_k_kernel(FlashFwdParams p) {
+__global__ __launch_bounds__(256) void prep_khat_kernel(KhatParams p) {
   const int nch = p.EP / 8;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)p.B * p.Hk * p.NkP * nch) return;
@@ -398,9 +398,15 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
 
 template <typename T, int EP, int DV>
 hipError_t launch_t(const FlashFwdParams& p, hipStream_t s) {
-  const int64_t nprep = (int64_t)p.B * p.Hk * p.NkP * (EP / 8);
-  hipError_t e = launch_named("flash_fwd_prep_k", fwd_prep_k_kernel<T>, dim3((unsigned)((nprep + 255) / 256)),
-                              dim3(256), s, p);
+  KhatParams kp;
+  kp.k = p.k;
+  kp.k_s[0] = p.k_s[0]; kp.k_s[1] = p.k_s[1]; kp.k_s[2] = p.k_s[2];
+  kp.table = p.table;
+  kp.t_sb = p.t_sb;
+  kp.t_sh = p.t_sh;
+  kp.kh = p.kh;
+  kp.B = p.B; kp.Hk = p.Hk; kp.Nk = p.Nk; kp.NkP = p.NkP; kp.D = p.D; kp.R = p.R; kp.EP = EP;
+  hipError_t e = launch_prep_khat(kp, T::kCode, s);
   if (e != hipSuccess) return e;
   const int blocks = p.nqb * p.B * p.Hq;
   return launch_named("flash_fwd", flash_fwd_kernel<T, EP, DV>, dim3(blocks), dim3(kThreads), s, p);
@@ -423,6 +429,13 @@ hipError_t dispatch(const FlashFwdParams& p, hipStream_t s) {
 
 hipError_t launch_flash_fwd(const FlashFwdParams& p, int dtype, hipStream_t s) {
   return dtype == 2 ? dispatch<BF16>(p, s) : dispatch<F16>(p, s);
+}
+
+hipError_t launch_prep_khat(const KhatParams& p, int dtype, hipStream_t s) {
+  const int64_t n = (int64_t)p.B * p.Hk * p.NkP * (p.EP / 8);
+  const dim3 grid((unsigned)((n + 255) / 256));
+  return dtype == 2 ? launch_named("prep_khat", prep_khat_kernel<BF16>, grid, dim3(256), s, p)
+                    : launch_named("prep_khat", prep_khat_kernel<F16>, grid, dim3(256), s, p);
 }
 
 }  // namespace pope

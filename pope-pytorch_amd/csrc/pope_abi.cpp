@@ -103,13 +103,12 @@ int check_ws(size_t need, void* ws, size_t have) {
 }
 
 // Flash backward workspace pieces, in order after the phase table (each 256-byte aligned):
-//   Q_hat (B, Hq, NqP, EP), Q_hat^T (B, Hq, EP, NqP), dO^T (B, Hq, DV, NqP),
-//   K_hat (B, Hk, NkP, EP), K_hat^T (B, Hk, EP, NkP)   -- 16-bit elements
-//   delta (B, Hq, NqP)                                  -- fp32
+//   Q_hat (B, Hq, NqP, EP), K_hat (B, Hk, NkP, EP)   -- 16-bit elements
+//   delta (B, Hq, NqP)                               -- fp32
 // with EP = round_up(D + R, 32), DV = round_up(D, 32), NqP / NkP = round_up(N, 128).
 struct BwdLayout {
   int EP, DV, NqP, NkP;
-  size_t qh, qht, dot, kh, kht, delta, total;
+  size_t qh, kh, delta, total;
 };
 
 BwdLayout bwd_layout(const pope_desc& d) {
@@ -120,10 +119,7 @@ BwdLayout bwd_layout(const pope_desc& d) {
   L.NkP = round_up(d.Nk, 128);
   size_t off = geometry(d, d.Hq).table;
   L.qh = off;    off += align_up((size_t)d.B * d.Hq * L.NqP * L.EP * 2);
-  L.qht = off;   off += align_up((size_t)d.B * d.Hq * L.NqP * L.EP * 2);
-  L.dot = off;   off += align_up((size_t)d.B * d.Hq * L.NqP * L.DV * 2);
   L.kh = off;    off += align_up((size_t)d.B * d.Hk * L.NkP * L.EP * 2);
-  L.kht = off;   off += align_up((size_t)d.B * d.Hk * L.NkP * L.EP * 2);
   L.delta = off; off += align_up((size_t)d.B * d.Hq * L.NqP * sizeof(float));
   L.total = off;
   return L;
@@ -403,10 +399,7 @@ int pope_flash_bwd(const pope_desc* d, const void* dout, const void* q, const vo
   p.dfreqs = dfreqs;
   p.dbias = dbias;
   p.qh = reinterpret_cast<uint16_t*>(ws + L.qh);
-  p.qht = reinterpret_cast<uint16_t*>(ws + L.qht);
-  p.dot = reinterpret_cast<uint16_t*>(ws + L.dot);
   p.kh = reinterpret_cast<uint16_t*>(ws + L.kh);
-  p.kht = reinterpret_cast<uint16_t*>(ws + L.kht);
   p.delta = reinterpret_cast<float*>(ws + L.delta);
   p.B = d->B; p.Hq = d->Hq; p.Hk = d->Hk; p.Nq = d->Nq; p.Nk = d->Nk; p.D = d->D; p.R = d->R;
   p.E = d->D + d->R;

@@ -30,6 +30,7 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 // Element-type traits for the half-precision MFMA paths.
 struct BF16 {
+  static constexpr int kCode = 2;   // pope_dtype code
   typedef __bf16 scalar;
   typedef bf16x8 vec8;
   static __device__ __forceinline__ float to_float(uint16_t bits) {
@@ -49,6 +50,7 @@ struct BF16 {
 };
 
 struct F16 {
+  static constexpr int kCode = 1;
   typedef _Float16 scalar;
   typedef f16x8 vec8;
   static __device__ __forceinline__ float to_float(uint16_t bits) {
@@ -110,5 +112,28 @@ __device__ __forceinline__ int xcd_remap(int hw_id, int total) {
 }
 
 __device__ __forceinline__ float wave_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+// LDS transpose read (ds_read_b64_tr_b16).  Within each group of 16 lanes, lane
+// j supplies the address of 4 consecutive 16-bit elements; output lane 4a + c
+// receives element c of the chunks addressed by lanes a, a + 4, a + 8, a + 12
+// (in that order).  Pointed at rows r0 + j / 4 and columns n0 + 4 (j % 4) of a
+// row-major tile, every lane gets 4 consecutive rows of its own column n0 + j.
+typedef __attribute__((ext_vector_type(4))) short v4i16;
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((v4i16 __attribute__((address_space(3)))*)p);
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// 8-element operand of a 32x32x16 MFMA taken from a row-major LDS tile X
+// (row stride ld elements) transposed: lane l gets column n0 + l % 32 and rows
+// [ra, ra + 4) followed by [rb, rb + 4), where ra / rb are the lane half's row
+// runs.  Rows index the MFMA k dimension.
+__device__ __forceinline__ u32x4 lds_operand_tr(const uint16_t* X, int ld, int ra, int rb, int n0, int lane) {
+  const int j = lane & 15, gi = lane >> 4;
+  const int col = n0 + 16 * (gi & 1) + 4 * (j & 3);
+  const u32x2 lo = lds_read_tr16(X + (ra + (j >> 2)) * ld + col);
+  const u32x2 hi = lds_read_tr16(X + (rb + (j >> 2)) * ld + col);
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
+}
 
 }  // namespace pope

@@ -47,6 +47,16 @@ struct FlashFwdParams {
 // dtype: 1 = f16, 2 = bf16.  Returns hipErrorInvalidValue for an uncovered (E, D) shape.
 hipError_t launch_flash_fwd(const FlashFwdParams& p, int dtype, hipStream_t s);
 
+// K_hat = polar transform of the keys, (B, Hk, NkP, EP) 16-bit rows, zero past Nk and past E
+// (flash_fwd.hip; used by the forward and the backward).
+struct KhatParams {
+  const uint16_t* k; int64_t k_s[3];
+  const float2* table; int64_t t_sb, t_sh;   // cos/sin(F) rows, see TableParams
+  uint16_t* kh;
+  int B, Hk, Nk, NkP, D, R, EP;
+};
+hipError_t launch_prep_khat(const KhatParams& p, int dtype, hipStream_t s);
+
 struct FlashBwdParams {
   const uint16_t* q; const uint16_t* k; const uint16_t* v; const uint16_t* o; const uint16_t* dout;
   const float* lse; const float* freqs; const float* bias; const uint8_t* mask;
@@ -55,12 +65,10 @@ struct FlashBwdParams {
   float* dfreqs; float* dbias;
   // workspace, written by the prep kernels (rows past Nq / Nk and columns past E are zero)
   uint16_t* qh;              // (B, Hq, NqP, EP)  expanded queries Q_hat
-  uint16_t* qht;             // (B, Hq, EP, NqP)  Q_hat transposed
-  uint16_t* dot;             // (B, Hq, DV, NqP)  dO transposed
   uint16_t* kh;              // (B, Hk, NkP, EP)  expanded keys K_hat
-  uint16_t* kht;             // (B, Hk, EP, NkP)  K_hat transposed
   float* delta;              // (B, Hq, NqP)      rowsum(O * dO)
   int B, Hq, Hk, Nq, Nk, D, R, E, EP, DV, NqP, NkP, causal, has_mask;
+  int n_kv_jobs, interleave; // dK/dV jobs of the fused launch; 1 = pair dK/dV and dQ jobs by cost
   float scale, scale_log2;
   int64_t q_s[3], k_s[3], v_s[3], o_s[3], do_s[3], dq_s[3], dk_s[3], dv_s[3], f_s[3], df_s[3];
   int64_t bias_sh, mask_sb, t_sb, t_sh;
