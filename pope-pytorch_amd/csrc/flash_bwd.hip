@@ -174,6 +174,7 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
 
   const uint8_t* mrow = p.has_mask ? p.mask + (int64_t)b * p.mask_sb : nullptr;
   const bool kvis = kj < Nk && (!p.has_mask || mrow[kj] != 0);
+  const TrLane dotr = tr_lane<false>(DO, lane), qhtr = tr_lane<false>(QH, lane);
   for (int e = tid; e < EP; e += kThreads) dbias_s[e] = 0.f;
 
   vec8 kreg[KS], vreg[DS];
@@ -294,13 +295,13 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
       for (int g2 = 0; g2 < 2; ++g2) {
         const vec8 ap = as_vec8<vec8>(pack8<T>(s, g2));
         const vec8 ads = as_vec8<vec8>(pack8<T>(dp, g2));
-        const int ra = 32 * qs + 16 * g2 + 4 * hf;
+        const int r0 = 32 * qs + 16 * g2;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
-          dva[db] = T::mfma32(ap, as_vec8<vec8>(lds_operand_tr(do_s, DO, ra, ra + 8, 32 * db, lane)), dva[db]);
+          dva[db] = T::mfma32(ap, as_vec8<vec8>(lds_operand_tr(do_s, dotr, DO, r0, 32 * db)), dva[db]);
 #pragma unroll
         for (int eb = 0; eb < EB; ++eb)
-          dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_operand_tr(qh_s, QH, ra, ra + 8, 32 * eb, lane)), dka[eb]);
+          dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_operand_tr(qh_s, qhtr, QH, r0, 32 * eb)), dka[eb]);
       }
     }
     if (st + 1 < nsteps) stage(buf ^ 1);
@@ -385,6 +386,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
   const int q_off = Nk - Nq;
   const int qi = qb * 128 + 32 * wave + lr;
   const bool qvalid = qi < Nq;
+  const TrLane khtr = tr_lane<false>(KH, lane);
 
   vec8 qreg[KS], doreg[DS];
   {
@@ -496,10 +498,9 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
 #pragma unroll
       for (int g2 = 0; g2 < 2; ++g2) {
         const vec8 bds = as_vec8<vec8>(pack8<T>(dp, g2));
-        const int ra = 32 * ks + 16 * g2 + 4 * hf;
 #pragma unroll
         for (int eb = 0; eb < EB; ++eb)
-          dqa[eb] = T::mfma32(as_vec8<vec8>(lds_operand_tr(kh_s, KH, ra, ra + 8, 32 * eb, lane)), bds, dqa[eb]);
+          dqa[eb] = T::mfma32(as_vec8<vec8>(lds_operand_tr(kh_s, khtr, KH, 32 * ks + 16 * g2, 32 * eb)), bds, dqa[eb]);
       }
     }
     if (kt + 1 < nt) stage(buf ^ 1);

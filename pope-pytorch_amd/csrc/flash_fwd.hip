@@ -21,9 +21,12 @@
 //   key), B = the wave's Q_hat held in registers (lane = query).  The result
 //   has one query per lane and keys in registers, so the softmax row
 //   reductions stay in-lane (plus one swap between the two lane halves).
-//   O^T += Vt P^T reuses the probabilities straight from the S registers as the
-//   B operand (a key permutation inside each 16-key group that the Vt reads
-//   follow); V is transposed into LDS as key pairs packed per 32-bit word.
+//   O^T += V^T P^T reuses the probabilities straight from the S registers as
+//   the B operand (a key permutation inside each 16-key group); the A operand
+//   comes from the row-major V tile through LDS transpose reads in the same key
+//   order.  Tiles with every key visible to every row of the wave skip the
+//   per-element masks, and the accumulator is rescaled only when a row's
+//   running max moves.
 // Scheduling
 //   blockIdx -> (query block, batch*head) with the heaviest causal blocks first
 //   and batch*head fastest, so consecutive workgroups land on different XCDs
@@ -96,26 +99,26 @@ __global__ __launch_bounds__(256) void prep_khat_kernel(KhatParams p) {
 // ---------------------------------------------------------------------------
 template <typename T, int EP, int DV>
 struct FwdCfg {
-  static constexpr int KH = EP + 8;            // K_hat row stride (elements)
-  static constexpr int VT = 2 * kBN + 8;       // Vt row stride (elements): both tiles of a pair
-  static constexpr int BUF = (2 * kBN * KH + DV * VT) * 2;   // bytes of one staged pair
-  static constexpr int NBUF = 2 * BUF + 64 * 4 <= kLdsMax ? 2 : 1;
+  static constexpr int KH = 8 * lds_units_rows(EP / 8);   // K_hat row stride: row reads only
+  static constexpr int VS = 8 * lds_units_tr(DV / 8);     // V row stride: transpose reads only
+  static constexpr int BUF = (2 * kBN * KH + 2 * kBN * VS) * 2;   // bytes of one staged pair
+  static constexpr int NBUF = 2 * BUF + 64 <= kLdsMax ? 2 : 1;
   static constexpr int MERGE = 4 * 64 * (2 + 16 * (DV / 32)) * 4;   // group 1's (m, l, O) hand-off
   static constexpr int LDS = NBUF * BUF > MERGE ? NBUF * BUF : MERGE;
   static constexpr int KCH = 2 * kBN * (EP / 8);               // 16-byte K_hat chunks per pair
   static constexpr int KLD = (KCH + kThreads - 1) / kThreads;  // per thread
-  static constexpr int VCH = kBN * (DV / 8);                   // key-pair x 8-dim chunks per pair
+  static constexpr int VCH = 2 * kBN * (DV / 8);               // 16-byte V chunks per pair
   static constexpr int VLD = (VCH + kThreads - 1) / kThreads;
 };
 
 template <typename T, int EP, int DV>
 __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p) {
   typedef FwdCfg<T, EP, DV> C;
-  constexpr int KS = EP / 16, NDB = DV / 32, KH = C::KH, VT = C::VT;
+  constexpr int KS = EP / 16, NDB = DV / 32, KH = C::KH, VS = C::VS;
   typedef typename T::vec8 vec8;
 
   __shared__ __attribute__((aligned(16))) char smem[C::LDS];
-  __shared__ uint32_t mskw[2][2 * kBN / 4];
+  __shared__ uint64_t mbits_s[2][2];   // [buffer][tile of the pair]: bit j = key j0 + j visible
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int grp = wave >> 2, wq = wave & 3;
@@ -125,8 +128,11 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const int D = p.D, R = p.R, E = D + R, Nk = p.Nk, Nq = p.Nq;
   const int q_off = Nk - Nq;
-  const int qi = qb * kBM + wq * 32 + lr;
+  const int qw0 = qb * kBM + wq * 32;   // first query row of this wave
+  const int qi = qw0 + lr;
   const bool qvalid = qi < Nq;
+  const bool fast_ok = p.scale_log2 > 0.f;   // max commutes with the scale
+  const TrLane vtr = tr_lane<false>(C::VS, lane);
 
   // ---- Q_hat for this lane's query row, in MFMA B-operand order ----------
   vec8 qreg[KS];
@@ -186,67 +192,43 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   const uint8_t* mrow = p.has_mask ? p.mask + (int64_t)b * p.mask_sb : nullptr;
 
   // ---- staging of a pair of tiles: global -> registers -> LDS ----------------
-  u32x4 kpf[C::KLD], vpf0[C::VLD], vpf1[C::VLD];
-  uint32_t mpf = 0;
+  u32x4 kpf[C::KLD], vpf[C::VLD];
+  uint64_t mpf = 0;
   auto fetch = [&](int pr) {
     const int j0 = pr * 2 * kBN;
 #pragma unroll
     for (int m = 0; m < C::KLD; ++m) {
       const int c = tid + m * kThreads;
-      if (c < C::KCH) {
-        const int row = c / (EP / 8), c8 = c % (EP / 8);
-        kpf[m] = ld16(khg + (int64_t)(j0 + row) * EP + 8 * c8);
-      }
+      if (c < C::KCH) kpf[m] = ld16(khg + (int64_t)(j0 + c / (EP / 8)) * EP + 8 * (c % (EP / 8)));
     }
 #pragma unroll
     for (int m = 0; m < C::VLD; ++m) {
       const int c = tid + m * kThreads;
-      vpf0[m] = u32x4{0u, 0u, 0u, 0u};
-      vpf1[m] = u32x4{0u, 0u, 0u, 0u};
+      vpf[m] = u32x4{0u, 0u, 0u, 0u};
       if (c < C::VCH) {
-        const int kp = c / (DV / 8), c8 = c % (DV / 8), key = j0 + 2 * kp;
-        if (c8 < nch) {
-          if (key < Nk) vpf0[m] = ld16(vg + (int64_t)key * p.v_s[2] + 8 * c8);
-          if (key + 1 < Nk) vpf1[m] = ld16(vg + (int64_t)(key + 1) * p.v_s[2] + 8 * c8);
-        }
+        const int row = c / (DV / 8), c8 = c % (DV / 8), key = j0 + row;
+        if (c8 < nch && key < Nk) vpf[m] = ld16(vg + (int64_t)key * p.v_s[2] + 8 * c8);
       }
     }
-    if (tid < 2 * kBN / 4) {
-      uint32_t w = 0;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int key = j0 + 4 * tid + s;
-        const bool ok = key < Nk && (!p.has_mask || mrow[key] != 0);
-        w |= ok ? (1u << (8 * s)) : 0u;
-      }
-      mpf = w;
+    if (wave < 2) {   // wave w: visibility bits of tile w of the pair
+      const int key = j0 + tid;
+      mpf = __ballot(key < Nk && (!p.has_mask || mrow[key] != 0));
     }
   };
   auto stage = [&](int buf) {
     uint16_t* kh = reinterpret_cast<uint16_t*>(smem + buf * C::BUF);
-    uint16_t* vt = kh + 2 * kBN * KH;
+    uint16_t* vs = kh + 2 * kBN * KH;
 #pragma unroll
     for (int m = 0; m < C::KLD; ++m) {
       const int c = tid + m * kThreads;
-      if (c < C::KCH) {
-        const int row = c / (EP / 8), c8 = c % (EP / 8);
-        st16(kh + row * KH + 8 * c8, kpf[m]);
-      }
+      if (c < C::KCH) st16(kh + (c / (EP / 8)) * KH + 8 * (c % (EP / 8)), kpf[m]);
     }
 #pragma unroll
     for (int m = 0; m < C::VLD; ++m) {
       const int c = tid + m * kThreads;
-      if (c < C::VCH) {
-        const int kp = c / (DV / 8), c8 = c % (DV / 8), d0 = 8 * c8;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          *reinterpret_cast<uint32_t*>(vt + (d0 + 2 * s) * VT + 2 * kp) = u16lo(vpf0[m][s]) | (u16lo(vpf1[m][s]) << 16);
-          *reinterpret_cast<uint32_t*>(vt + (d0 + 2 * s + 1) * VT + 2 * kp) =
-              u16hi(vpf0[m][s]) | (u16hi(vpf1[m][s]) << 16);
-        }
-      }
+      if (c < C::VCH) st16(vs + (c / (DV / 8)) * VS + 8 * (c % (DV / 8)), vpf[m]);
     }
-    if (tid < 2 * kBN / 4) mskw[buf & (C::NBUF - 1)][tid] = mpf;
+    if (wave < 2 && lane == 0) mbits_s[buf][wave] = mpf;
   };
 
   if (npair > 0) {
@@ -260,11 +242,15 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
     if (t + 1 < npair) fetch(t + 1);
 
     const int tile = 2 * t + grp;
-    if (tile < nt) {
+    const int j0 = tile * kBN;
+    // keys visible to some row of this wave: not all masked, not all after the wave's last query
+    const uint64_t mraw = mbits_s[buf][grp];
+    const uint64_t mb = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)mraw) |
+                        ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(mraw >> 32)) << 32);
+    const bool live = tile < nt && mb != 0 && !(p.causal && j0 > qw0 + 31);
+    if (live) {
       const uint16_t* kh = reinterpret_cast<const uint16_t*>(smem + buf * C::BUF) + grp * kBN * KH;
-      const uint16_t* vt = reinterpret_cast<const uint16_t*>(smem + buf * C::BUF) + 2 * kBN * KH + grp * kBN;
-      const uint32_t* mw_s = &mskw[buf][grp * kBN / 4];
-      const int j0 = tile * kBN;
+      const uint16_t* vs = reinterpret_cast<const uint16_t*>(smem + buf * C::BUF) + 2 * kBN * KH + grp * kBN * VS;
 
       // ---- S^T = K_hat Q_hat^T ---------------------------------------------
       f32x16 sacc[2];
@@ -278,30 +264,51 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
           sacc[kb] = T::mfma32(a, qreg[kk], sacc[kb]);
         }
       }
-      // ---- scale + masks + running max --------------------------------------
+      // ---- masks (partial tiles only) + running max -------------------------
+      // full tile: every key visible and (causal) every key <= the wave's first query
+      const bool full = fast_ok && mb == ~0ull && !(p.causal && j0 + kBN - 1 > qw0);
       float mt = -INFINITY;
+      if (full) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const uint32_t mw = mw_s[8 * kb + 2 * g + hf];
+          for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb][r]);
+        mt *= p.scale_log2;
+      } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = 4 * g + i;
-            const int key = j0 + 32 * kb + 8 * g + 4 * hf + i;
-            const bool ok = ((mw >> (8 * i)) & 0xffu) && (!p.causal || key <= qi);
-            const float s = ok ? sacc[kb][r] * p.scale_log2 : -INFINITY;
-            sacc[kb][r] = s;
-            mt = fmaxf(mt, s);
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int kr = 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
+            const bool ok = ((mb >> kr) & 1ull) && (!p.causal || j0 + kr <= qi);
+            const float sv = ok ? sacc[kb][r] * p.scale_log2 : -INFINITY;
+            sacc[kb][r] = sv;
+            mt = fmaxf(mt, sv);
           }
-        }
       }
       mt = fmaxf(mt, wave_shfl_xor(mt, 32));
-      if (__any(mt > -INFINITY)) {
-        const float m_new = fmaxf(m_run, mt);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float m_new = fmaxf(m_run, mt);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      if (__any(m_new != m_run)) {   // rescale only when some row's max moved
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        float psum = 0.f;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+        m_run = m_new;
+      }
+      float psum = 0.f;
+      if (full) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float pr = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r], p.scale_log2, -m_use));
+            sacc[kb][r] = pr;
+            psum += pr;
+          }
+      } else {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -310,32 +317,21 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
             sacc[kb][r] = pr;
             psum += pr;
           }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+      }
+      l_run += psum;
 
-        // ---- O^T += Vt P^T -------------------------------------------------
+      // ---- O^T += V^T P^T: A = V tile read transposed ----------------------
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-          for (int g = 0; g < 2; ++g) {
-            u32x4 pw;
+        for (int g = 0; g < 2; ++g) {
+          u32x4 pw;
 #pragma unroll
-            for (int s = 0; s < 4; ++s) pw[s] = T::pack2(sacc[kb][8 * g + 2 * s], sacc[kb][8 * g + 2 * s + 1]);
-            const vec8 pb = as_vec8<vec8>(pw);
-            const int kc = 32 * kb + 16 * g + 4 * hf;
+          for (int s = 0; s < 4; ++s) pw[s] = T::pack2(sacc[kb][8 * g + 2 * s], sacc[kb][8 * g + 2 * s + 1]);
+          const vec8 pb = as_vec8<vec8>(pw);
 #pragma unroll
-            for (int db = 0; db < NDB; ++db) {
-              const uint16_t* vr = vt + (32 * db + lr) * VT + kc;
-              const u32x2 lo = *reinterpret_cast<const u32x2*>(vr);
-              const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 8);
-              const u32x4 aw = {lo[0], lo[1], hi[0], hi[1]};
-              oacc[db] = T::mfma32(as_vec8<vec8>(aw), pb, oacc[db]);
-            }
-          }
+          for (int db = 0; db < NDB; ++db)
+            oacc[db] = T::mfma32(as_vec8<vec8>(lds_operand_tr(vs, vtr, VS, 32 * kb + 16 * g, 32 * db)), pb, oacc[db]);
         }
       }
     }

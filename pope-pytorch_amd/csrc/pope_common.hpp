@@ -113,6 +113,19 @@ __device__ __forceinline__ int xcd_remap(int hw_id, int total) {
 
 __device__ __forceinline__ float wave_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// LDS row strides.  The LDS serves 64 banks of 4 bytes; counted in 16-byte
+// units, a 128-bit row read by 16 lanes (rows r0..r0+15, one unit each) is
+// conflict-free when the row stride is odd, and a transpose read by 32 lanes
+// (4 rows x 4 consecutive units, lds_operand_tr) when the stride is 4 or 12
+// mod 16.  A tile read both ways takes a stride of 4 or 12 mod 16 units and
+// swizzles: unit u of row r lives at u ^ ((r >> 2) & 3) (rows of one transpose
+// read share the swizzle; 16 consecutive rows spread over all 16 bank groups).
+__host__ __device__ constexpr int lds_units_rows(int units) { return units | 1; }
+__host__ __device__ constexpr int lds_units_tr(int units) {
+  return (units % 16 == 4 || units % 16 == 12) ? units : lds_units_tr(units + 4 - units % 4);
+}
+__device__ __forceinline__ int lds_swz(int row, int unit) { return unit ^ ((row >> 2) & 3); }
+
 // LDS transpose read (ds_read_b64_tr_b16).  Within each group of 16 lanes, lane
 // j supplies the address of 4 consecutive 16-bit elements; output lane 4a + c
 // receives element c of the chunks addressed by lanes a, a + 4, a + 8, a + 12
@@ -125,14 +138,32 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
 }
 
 // 8-element operand of a 32x32x16 MFMA taken from a row-major LDS tile X
-// (row stride ld elements) transposed: lane l gets column n0 + l % 32 and rows
-// [ra, ra + 4) followed by [rb, rb + 4), where ra / rb are the lane half's row
-// runs.  Rows index the MFMA k dimension.
-__device__ __forceinline__ u32x4 lds_operand_tr(const uint16_t* X, int ld, int ra, int rb, int n0, int lane) {
-  const int j = lane & 15, gi = lane >> 4;
-  const int col = n0 + 16 * (gi & 1) + 4 * (j & 3);
-  const u32x2 lo = lds_read_tr16(X + (ra + (j >> 2)) * ld + col);
-  const u32x2 hi = lds_read_tr16(X + (rb + (j >> 2)) * ld + col);
+// (row stride ld elements) transposed: lane l gets column n0 + l % 32 and the
+// rows [R0 + 4 h, R0 + 4 h + 4) followed by [R0 + 8 + 4 h, R0 + 12 + 4 h),
+// h = l / 32 -- the k order of a 16-wide group of a 32x32 MFMA result read
+// back as an operand.  R0 is a multiple of 16, n0 of 32.  The lane-dependent
+// part of the addresses is computed once (TrLane), so every read is the lane
+// base plus a compile-time offset.  With SWZ the tile uses the lds_swz layout:
+// the two row runs then sit at different swizzles, hence two bases.
+struct TrLane {
+  int lo, hi;
+};
+template <bool SWZ>
+__device__ __forceinline__ TrLane tr_lane(int ld, int lane) {
+  const int j = lane & 15, gi = lane >> 4, h = lane >> 5;
+  const int u = 2 * (gi & 1) + ((j >> 1) & 1);   // unit within the 4-unit group at n0
+  const int row = 4 * h + (j >> 2);
+  const int sub = 4 * (j & 1);
+  TrLane t;
+  // rows R0 + 4 h + ..: (row >> 2) & 3 == h;  rows R0 + 8 + 4 h + ..: == h + 2
+  t.lo = row * ld + 8 * (SWZ ? (u ^ h) : u) + sub;
+  t.hi = (row + 8) * ld + 8 * (SWZ ? (u ^ (h + 2)) : u) + sub;
+  return t;
+}
+__device__ __forceinline__ u32x4 lds_operand_tr(const uint16_t* X, const TrLane& t, int ld, int R0, int n0) {
+  const uint16_t* p = X + R0 * ld + n0;
+  const u32x2 lo = lds_read_tr16(p + t.lo);
+  const u32x2 hi = lds_read_tr16(p + t.hi);
   return u32x4{lo[0], lo[1], hi[0], hi[1]};
 }
 
