@@ -140,11 +140,14 @@ struct BwdCfg {
   static constexpr int BMK = kBig ? 32 : 64;   // query tile of a dK/dV job
   static constexpr int BNQ = kBig ? 32 : 64;   // key tile of a dQ job
   static constexpr int MINB = kBig ? 1 : 2;
-  static constexpr int QH = EP + 8, DO = DV + 8;
+  // Q_hat / dO (dK/dV jobs) and K_hat (dQ jobs) are read by rows and transposed: swizzled
+  // strides; V (dQ jobs) only by rows.
+  static constexpr int QH = 8 * lds_units_tr(EP / 8), DO = 8 * lds_units_tr(DV / 8);
+  static constexpr int VR = 8 * lds_units_rows(DV / 8);
   // dK/dV stage: Q_hat tile, dO tile, lse and delta
   static constexpr int KV_STAGE = (BMK * QH + BMK * DO) * 2 + 2 * BMK * 4;
   // dQ stage: K_hat tile, V tile
-  static constexpr int Q_STAGE = (BNQ * QH + BNQ * DO) * 2;
+  static constexpr int Q_STAGE = (BNQ * QH + BNQ * VR) * 2;
   static constexpr int STAGE = KV_STAGE > Q_STAGE ? KV_STAGE : Q_STAGE;
   static constexpr int EPI = 32 * (EP + 1) * 4;
   static constexpr int LDS = 2 * STAGE > EPI ? 2 * STAGE : EPI;
@@ -174,7 +177,7 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
 
   const uint8_t* mrow = p.has_mask ? p.mask + (int64_t)b * p.mask_sb : nullptr;
   const bool kvis = kj < Nk && (!p.has_mask || mrow[kj] != 0);
-  const TrLane dotr = tr_lane<false>(DO, lane), qhtr = tr_lane<false>(QH, lane);
+  const TrLane dotr = tr_lane<true>(DO, lane), qhtr = tr_lane<true>(QH, lane);
   for (int e = tid; e < EP; e += kThreads) dbias_s[e] = 0.f;
 
   vec8 kreg[KS], vreg[DS];
@@ -200,6 +203,8 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
 #pragma unroll
     for (int r = 0; r < 16; ++r) dka[x][r] = 0.f;
 
+  const bool wave_vis = __all(kvis);
+  const float masked = p.scale_log2 >= 0.f ? -INFINITY : INFINITY;
   const int any_key = __syncthreads_or(kvis ? 1 : 0);
   const int nqt = (Nq + BM - 1) / BM;
   const int qt0 = p.causal ? min(j0 / BM, nqt) : 0;
@@ -243,12 +248,14 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
 #pragma unroll
     for (int m = 0; m < QLD; ++m) {
       const int c = tid + m * kThreads;
-      if (c < QCH) st16(qh_s + (c / (EP / 8)) * QH + 8 * (c % (EP / 8)), qpf[m]);
+      const int row = c / (EP / 8);
+      if (c < QCH) st16(qh_s + row * QH + 8 * lds_swz(row, c % (EP / 8)), qpf[m]);
     }
 #pragma unroll
     for (int m = 0; m < DLD; ++m) {
       const int c = tid + m * kThreads;
-      if (c < DCH) st16(do_s + (c / (DV / 8)) * DO + 8 * (c % (DV / 8)), dpf[m]);
+      const int row = c / (DV / 8);
+      if (c < DCH) st16(do_s + row * DO + 8 * lds_swz(row, c % (DV / 8)), dpf[m]);
     }
     if (tid < BM) {
       lse_s[tid] = lpf;
@@ -279,15 +286,24 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
       }
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk)
-        s = T::mfma32(as_vec8<vec8>(ld16(qh_s + (32 * qs + lr) * QH + 16 * kk + 8 * hf)), kreg[kk], s);
+        s = T::mfma32(as_vec8<vec8>(ld16(qh_s + (32 * qs + lr) * QH + 8 * lds_swz(lr, 2 * kk + hf))), kreg[kk], s);
 #pragma unroll
       for (int kk = 0; kk < DS; ++kk)
-        dp = T::mfma32(as_vec8<vec8>(ld16(do_s + (32 * qs + lr) * DO + 16 * kk + 8 * hf)), vreg[kk], dp);
+        dp = T::mfma32(as_vec8<vec8>(ld16(do_s + (32 * qs + lr) * DO + 8 * lds_swz(lr, 2 * kk + hf))), vreg[kk], dp);
+      // Partial sub-tile (some key of the wave masked, or on the causal diagonal): masked
+      // scores become -inf (+inf for a negative scale) so that P = 0.  Rows past Nq and fully
+      // masked rows carry lse = +inf, which gives P = 0 without a test.
+      if (!wave_vis || (p.causal && i0 + 32 * qs < j0 + 32 * wave + 31)) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qr = 32 * qs + 8 * (r >> 2) + 4 * hf + (r & 3);
+          if (!(kvis && (!p.causal || kj <= i0 + qr))) s[r] = masked;
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int qr = 32 * qs + 8 * (r >> 2) + 4 * hf + (r & 3);
-        const bool vis = kvis && (!p.causal || kj <= i0 + qr);
-        const float pv = vis ? __builtin_amdgcn_exp2f(fmaf(s[r], p.scale_log2, -lse_s[qr])) : 0.f;
+        const float pv = __builtin_amdgcn_exp2f(fmaf(s[r], p.scale_log2, -lse_s[qr]));
         s[r] = pv;
         dp[r] = pv * (dp[r] - dl_s[qr]);
       }
@@ -370,11 +386,10 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
 // Results: lane = query, registers = keys; dS^T is the B operand of
 //   dQ_hat^T += K_hat^T dS^T   A = K_hat tile read transposed.
 template <typename T, int EP, int DV>
-__device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint8_t (*msk_s)[64], int qb,
-                                       int bh) {
+__device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint64_t* mbits_s, int qb, int bh) {
   typedef BwdCfg<EP, DV> C;
   constexpr int BN = C::BNQ, KS = EP / 16, DS = DV / 16, EB = EP / 32, NB = BN / 32;
-  constexpr int KH = C::QH, VR = C::DO;
+  constexpr int KH = C::QH, VR = C::VR;
   constexpr int KCH = BN * (EP / 8), VCH = BN * (DV / 8);
   constexpr int KLD = (KCH + kThreads - 1) / kThreads, VLD = (VCH + kThreads - 1) / kThreads;
   typedef typename T::vec8 vec8;
@@ -386,7 +401,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
   const int q_off = Nk - Nq;
   const int qi = qb * 128 + 32 * wave + lr;
   const bool qvalid = qi < Nq;
-  const TrLane khtr = tr_lane<false>(KH, lane);
+  const TrLane khtr = tr_lane<true>(KH, lane);
 
   vec8 qreg[KS], doreg[DS];
   {
@@ -401,6 +416,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
       doreg[kk] = as_vec8<vec8>((qvalid && d0 < D) ? ld16(dr + d0) : zero4());
     }
   }
+  const float masked = p.scale_log2 >= 0.f ? -INFINITY : INFINITY;
   float lse2 = INFINITY, dl = 0.f;
   if (qvalid) {
     const float l = p.lse[(int64_t)bh * Nq + qi];
@@ -424,7 +440,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
   const uint8_t* mrow = p.has_mask ? p.mask + (int64_t)b * p.mask_sb : nullptr;
 
   u32x4 kpf[KLD], vpf[VLD];
-  uint8_t mpf = 0;
+  uint64_t mpf = 0;
   auto fetch = [&](int kt) {
     const int j0 = kt * BN;
 #pragma unroll
@@ -441,9 +457,9 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
         if (j0 + row < Nk && 8 * c8 < D) vpf[m] = ld16(v_g + (int64_t)(j0 + row) * p.v_s[2] + 8 * c8);
       }
     }
-    if (tid < BN) {
-      const int key = j0 + tid;
-      mpf = (key < Nk && (!p.has_mask || mrow[key] != 0)) ? 1 : 0;
+    if (wave == 0) {   // bit j: key j0 + j visible
+      const int key = j0 + lane;
+      mpf = __ballot(lane < BN && key < Nk && (!p.has_mask || mrow[key] != 0));
     }
   };
   auto stage = [&](int buf) {
@@ -452,14 +468,15 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
 #pragma unroll
     for (int m = 0; m < KLD; ++m) {
       const int c = tid + m * kThreads;
-      if (c < KCH) st16(kh_s + (c / (EP / 8)) * KH + 8 * (c % (EP / 8)), kpf[m]);
+      const int row = c / (EP / 8);
+      if (c < KCH) st16(kh_s + row * KH + 8 * lds_swz(row, c % (EP / 8)), kpf[m]);
     }
 #pragma unroll
     for (int m = 0; m < VLD; ++m) {
       const int c = tid + m * kThreads;
       if (c < VCH) st16(v_s + (c / (DV / 8)) * VR + 8 * (c % (DV / 8)), vpf[m]);
     }
-    if (tid < BN) msk_s[buf][tid] = mpf;
+    if (tid == 0) mbits_s[buf] = mpf;
   };
 
   if (nt > 0) {
@@ -473,7 +490,17 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
     const int j0 = kt * BN;
     const uint16_t* kh_s = reinterpret_cast<const uint16_t*>(smem + buf * C::STAGE);
     const uint16_t* v_s = kh_s + BN * KH;
-    const uint8_t* mk = msk_s[buf];
+    const uint64_t mraw = mbits_s[buf];
+    const uint64_t mb = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)mraw) |
+                        ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(mraw >> 32)) << 32);
+    const uint64_t all_bits = BN == 64 ? ~0ull : ((1ull << BN) - 1);
+    // every key visible and (causal) every key at or before the wave's first query
+    const bool full = mb == all_bits && !(p.causal && j0 + BN - 1 > qb * 128 + 32 * wave);
+    if (mb == 0) {   // every key of this tile masked
+      if (kt + 1 < nt) stage(buf ^ 1);
+      __syncthreads();
+      continue;
+    }
 #pragma unroll
     for (int ks = 0; ks < NB; ++ks) {
       f32x16 s, dp;
@@ -484,17 +511,19 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
       }
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk)
-        s = T::mfma32(as_vec8<vec8>(ld16(kh_s + (32 * ks + lr) * KH + 16 * kk + 8 * hf)), qreg[kk], s);
+        s = T::mfma32(as_vec8<vec8>(ld16(kh_s + (32 * ks + lr) * KH + 8 * lds_swz(lr, 2 * kk + hf))), qreg[kk], s);
 #pragma unroll
       for (int kk = 0; kk < DS; ++kk)
         dp = T::mfma32(as_vec8<vec8>(ld16(v_s + (32 * ks + lr) * VR + 16 * kk + 8 * hf)), doreg[kk], dp);
+      if (!full) {   // masked scores -> -inf (+inf for a negative scale): P = 0
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kr = 32 * ks + 8 * (r >> 2) + 4 * hf + (r & 3);
-        const bool ok = mk[kr] && (!p.causal || j0 + kr <= qi);
-        const float pv = ok ? __builtin_amdgcn_exp2f(fmaf(s[r], p.scale_log2, -lse2)) : 0.f;
-        dp[r] = pv * (dp[r] - dl);
+        for (int r = 0; r < 16; ++r) {
+          const int kr = 32 * ks + 8 * (r >> 2) + 4 * hf + (r & 3);
+          if (!(((mb >> kr) & 1ull) && (!p.causal || j0 + kr <= qi))) s[r] = masked;
+        }
       }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dp[r] = __builtin_amdgcn_exp2f(fmaf(s[r], p.scale_log2, -lse2)) * (dp[r] - dl);
 #pragma unroll
       for (int g2 = 0; g2 < 2; ++g2) {
         const vec8 bds = as_vec8<vec8>(pack8<T>(dp, g2));
@@ -549,7 +578,7 @@ template <typename T, int EP, int DV>
 __global__ __launch_bounds__(kThreads, (BwdCfg<EP, DV>::MINB)) void bwd_main_kernel(FlashBwdParams p) {
   __shared__ __attribute__((aligned(16))) char smem[BwdCfg<EP, DV>::LDS];
   __shared__ float dbias_s[EP];
-  __shared__ uint8_t msk_s[2][64];
+  __shared__ uint64_t mbits_s[2];
   const int nqb = p.NqP / 128;
   const int id = blockIdx.x;
   int kind, blk, head;   // kind 0 = dK/dV job (head = b * Hk + hk), 1 = dQ job (head = b * Hq + h)
@@ -576,7 +605,7 @@ __global__ __launch_bounds__(kThreads, (BwdCfg<EP, DV>::MINB)) void bwd_main_ker
   if (kind == 0)
     dkdv_job<T, EP, DV>(p, smem, dbias_s, blk, head);
   else
-    dq_job<T, EP, DV>(p, smem, msk_s, blk, head);
+    dq_job<T, EP, DV>(p, smem, mbits_s, blk, head);
 }
 
 template <typename T, int EP, int DV>
