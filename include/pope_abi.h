@@ -128,10 +128,11 @@ int pope_flash_bwd(const pope_desc* desc, const void* dout, const void* q, const
                    void* stream);
 
 /*
- * Bandwidth-bound forward for short query blocks (Nq <= 16, e.g. single-token
- * decode against a long KV cache): split-K over the keys plus an LSE merge.
- * Same contract as pope_flash_fwd.  Replaces flash_attn_forward at seqlen_q = 1
- * (triton_pope_flash_attn.py:222-271 with grid (1, B*H)).
+ * Bandwidth-bound forward for a single non-causal query row against a long KV
+ * cache (decode): split-K over the keys plus an LSE merge.  Same contract as
+ * pope_flash_fwd; returns POPE_ERR_UNSUPPORTED for Nq != 1, causal, or head dim
+ * above 128 (callers then use pope_flash_fwd).  Replaces flash_attn_forward at
+ * seqlen_q = 1 (triton_pope_flash_attn.py:222-271 with grid (1, B*H)).
  */
 int pope_flash_decode(const pope_desc* desc, const void* q, const void* k, const void* v,
                       const float* freqs, const float* bias, const uint8_t* mask, void* o,

@@ -156,17 +156,11 @@ size_t sim_ws(const pope_desc& d, int op) {
   return n;
 }
 
-// Decode workspace: [table | partial O (rows, splits, D) | partial (m, l) (rows, splits, 2)].
+// Decode workspace: [table | partial O (rows, splits, D) | partial (m, l) (rows, splits, 2)],
+// one split per pope::decode_split_keys() keys.
 int decode_splits(const pope_desc& d) {
-  // Enough (batch, head, split) work items to cover 256 CUs several times over,
-  // with at least 256 keys per split.
-  const int rows = d.B * d.Hq;
-  int splits = (2048 + rows - 1) / rows;
-  const int max_by_len = (d.Nk + 255) / 256;
-  if (splits > max_by_len) splits = max_by_len;
-  if (splits < 1) splits = 1;
-  if (splits > 256) splits = 256;
-  return splits;
+  const int per = pope::decode_split_keys();
+  return (d.Nk + per - 1) / per;
 }
 
 size_t decode_ws(const pope_desc& d) {
@@ -431,7 +425,9 @@ int pope_flash_decode(const pope_desc* d, const void* q, const void* k, const vo
                       size_t workspace_bytes, void* stream) {
   int rc = check_flash_common(d, q, k, v, freqs, bias, mask, o, lse);
   if (rc) return rc;
-  if (d->Nq > 16) return fail(POPE_ERR_UNSUPPORTED, "decode kernel covers up to 16 query rows (got %d)", d->Nq);
+  if (d->Nq != 1 || d->causal || d->D > 128)
+    return fail(POPE_ERR_UNSUPPORTED, "decode kernel covers one non-causal query row with head dim <= 128 "
+                                      "(got %d rows, causal %d, head dim %d)", d->Nq, d->causal, d->D);
   if ((rc = check_ws(decode_ws(*d), workspace, workspace_bytes))) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const Geo g = geometry(*d, d->Hq);

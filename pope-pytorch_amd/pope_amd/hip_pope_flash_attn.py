@@ -137,7 +137,8 @@ def flash_fwd_op(q: Tensor, k: Tensor, v: Tensor, freqs: Optional[Tensor], bias:
         d.mask_sb = mask.stride(0)
     ws = _lib.workspace(_lib.OP_FLASH_FWD, d, q.device)
     wsz = 0 if ws is None else ws.numel()
-    use_decode = q.shape[2] <= 16 and k.shape[2] >= 1024
+    # one non-causal query row against a long cache: the split-K decode kernel
+    use_decode = q.shape[2] == 1 and not causal and k.shape[2] >= 1024
     fn = L.pope_flash_decode if use_decode else L.pope_flash_fwd
     if use_decode:
         ws = _lib.workspace(_lib.OP_FLASH_DECODE, d, q.device)

@@ -119,7 +119,7 @@ def test_sim_and_decode_validation():
     assert st == 2 and "fp32" in _lib.last_error()
     d = _desc(Nq=64, dtype=_lib.POPE_BF16)
     st = L.pope_flash_decode(ctypes.byref(d), _A, _A, _A, _A, _A, None, _A, _A, _A, 1 << 16, None)
-    assert st == 2 and "16 query rows" in _lib.last_error()
+    assert st == 2 and "one non-causal query row" in _lib.last_error()
     d = _desc(dtype=_lib.POPE_F32, D=64, R=64)
     d.bias_sh = -1
     st = L.pope_sim_bwd(ctypes.byref(d), _A, _A, _A, _A, _A, _A, _A, None, None, _A, 1 << 16, None)

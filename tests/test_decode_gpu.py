@@ -1,0 +1,91 @@
+"""Single-query decode against a long KV cache on the GPU: the split-K decode
+kernel (flash_decode) vs the CPU oracle.
+
+Tolerance: the north star's 2e-2 absolute against an fp32+ reference for bf16
+flash, with the oracle in float64 on the same bf16/fp16-rounded inputs.  Cases
+follow BASELINE config C5 in miniature (one query row, PoPE with full rotation,
+valid prefix lengths per batch via the key-padding mask) plus ragged cache
+lengths, head dims 32..128 (including 96, whose 12 chunks of 8 dims leave lanes
+idle), GQA, a batch row with every key masked, fp16, and the backward through
+the decode's log-sum-exp.
+"""
+import pytest
+import torch
+
+from gpu_common import make_pope_inputs, max_abs, oracle_attention
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _decode_inputs(seed, B, Hq, Hk, Nk, D, R, dtype, lengths=None, dead_row=False):
+    inp = make_pope_inputs(seed, B, Hq, Hk, 1, Nk, D, R, dtype, "none")
+    mask = torch.ones(B, Nk, dtype=torch.bool)
+    g = torch.Generator().manual_seed(seed + 1)
+    for b in range(B):
+        L = lengths[b] if lengths is not None else int(torch.randint(Nk // 8, Nk + 1, (1,), generator=g))
+        mask[b, L:] = False
+    if dead_row:
+        mask[0] = False
+    inp["mask"] = mask.to("cuda")
+    return inp
+
+
+def _run(inp, need_grads=False):
+    import pope_amd
+    q, k, v = (inp[n].detach().clone().requires_grad_(need_grads) for n in ("q", "k", "v"))
+    freqs = inp["freqs"].detach().clone().requires_grad_(need_grads)
+    bias = inp["bias"].detach().clone().requires_grad_(need_grads)
+    o = pope_amd.flash_attn_with_pope(q, k, v, pos_emb=(freqs, bias), mask=inp["mask"], causal=False)
+    res = dict(o=o)
+    if need_grads:
+        o.backward(inp["do"])
+        res.update(dq=q.grad, dk=k.grad, dv=v.grad, dbias=bias.grad)
+    return res
+
+
+CASES = [
+    # B, Hq, Hk, Nk, D, R, dtype
+    (2, 4, 4, 8192, 64, 64, torch.bfloat16),
+    (3, 4, 4, 5000 + 37, 64, 64, torch.bfloat16),     # ragged cache length
+    (2, 8, 2, 4096, 64, 32, torch.bfloat16),          # GQA 4:1, partial rotation
+    (2, 2, 2, 3000, 128, 64, torch.bfloat16),         # D = 128
+    (2, 2, 2, 3000, 96, 96, torch.bfloat16),          # D = 96 (axial-style)
+    (2, 2, 2, 2048, 32, 16, torch.float16),           # D = 32, fp16
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(str(x) for x in c[:6]))
+def test_decode_forward(cuda, case):
+    B, Hq, Hk, Nk, D, R, dtype = case
+    inp = _decode_inputs(31, B, Hq, Hk, Nk, D, R, dtype)
+    res = _run(inp)
+    ref = oracle_attention(inp, False, grads=False)
+    err = max_abs(res["o"], ref["o"])
+    print(f"o={err:.2e}")
+    assert err <= TOL
+
+
+def test_decode_lse_and_dead_row(cuda):
+    from pope_amd.hip_pope_flash_attn import flash_attn_forward
+    inp = _decode_inputs(5, 3, 4, 4, 6000, 64, 64, torch.bfloat16, lengths=[6000, 1, 4097], dead_row=True)
+    tr = lambda t: t.transpose(1, 2)
+    o, lse = flash_attn_forward(tr(inp["q"]), tr(inp["k"]), tr(inp["v"]), inp["freqs"], inp["bias"], inp["mask"])
+    ref = oracle_attention(inp, False, grads=False)
+    assert max_abs(tr(o), ref["o"]) <= TOL
+    finite = torch.isfinite(ref["lse"])
+    assert torch.equal(torch.isfinite(lse.cpu()), finite)           # batch 0: every key masked
+    assert (lse.cpu()[finite] - ref["lse"][finite]).abs().max().item() <= TOL
+    assert tr(o)[0].abs().max().item() == 0.0
+
+
+def test_decode_backward(cuda):
+    inp = _decode_inputs(9, 2, 4, 4, 4096, 64, 64, torch.bfloat16)
+    res = _run(inp, need_grads=True)
+    ref = oracle_attention(inp, False)
+    for n in ("o", "dq", "dk", "dv", "dbias"):
+        e = max_abs(res[n], ref[n])
+        t = TOL * (max(1.0, ref[n].abs().max().item()) if n == "dbias" else 1.0)
+        print(f"{n}={e:.2e}")
+        assert e <= t, n
