@@ -8,16 +8,21 @@
 //
 // The path is bound by HBM: every valid key costs 2 * D * 2 bytes of K and V
 // and a handful of flops.  Work decomposition:
-//   decode_split : one workgroup (4 waves) per (batch, query head, split of
-//                  kSplit keys).  A split whose keys are all masked exits after
-//                  reading its mask bytes.  Pass 1 streams K: LPK lanes share one
-//                  key row (16 bytes each, coalesced), apply the polar transform
-//                  of the key -- softplus(k) times cos / sin of the key phase from
-//                  the per-call table -- fold in the query's (cos, sin) weights
-//                  and reduce the score across the LPK lanes; the scaled scores
-//                  of the split go to LDS.  Pass 2 takes the split's max, streams
-//                  V with the same lane mapping and accumulates p * v; the
-//                  partial (m, l, o) is written to the workspace.
+//   decode_split : one workgroup (4 waves) per (batch, split of kSplit keys),
+//                  covering every query head of the batch.  A split whose keys
+//                  are all masked exits after reading its mask bytes.  The split's
+//                  rows of the cos / sin(F_j) table (fp16 pairs) are staged in LDS
+//                  once and shared by all heads.  LPK lanes share one key row of
+//                  one head (16 bytes each, coalesced); a thread streams every
+//                  KP-th key of the split for its head.  Pass 1 streams K: the
+//                  polar transform of the key (softplus(k) times the staged cos /
+//                  sin) folded with the query's (cos, sin) weights, reduced
+//                  across the LPK lanes, scaled scores to LDS.  Pass 2 takes each
+//                  head's max over the split and streams V, accumulating p * v.
+//                  In both passes the loads of the next batch of keys are issued
+//                  before the current batch is computed.  The KP partial states
+//                  of a head merge through LDS into one (m, l, o) per (batch,
+//                  head, split).
 //   decode_combine : merges the splits of each (batch, head) by their log-sum-exp
 //                  and writes o (input dtype) and lse (natural log, -inf when
 //                  every key is masked).
@@ -33,211 +38,307 @@ namespace pope {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kSplit = 512;    // keys per split (one workgroup)
-constexpr int kUnroll = 4;     // key steps whose loads are issued together
+constexpr int kSplit = 128;    // keys per split (one workgroup)
+constexpr int kMaxHG = 16;     // query heads per pass of a workgroup
+constexpr int kBatch = 8;      // keys per batch (loads issued together)
+constexpr int kMaxR = 128;
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-template <typename T, int LPK>
-__global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p) {
-  constexpr int KPW = 64 / LPK;                // keys per wave step
-  constexpr int KPS = 4 * KPW;                 // keys per workgroup step
-  constexpr int NSTEP = kSplit / KPS;
-  __shared__ float s_lds[kSplit];
-  __shared__ float red[4][128];
-  __shared__ float red_l[4];
+__device__ __forceinline__ float2 half2f(uint32_t w) {
+  const f16x2 v = __builtin_bit_cast(f16x2, w);
+  return make_float2((float)v[0], (float)v[1]);
+}
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+// Thread layout: t = c + LPK * (hl + HG * kp): c = 8-dim chunk of the head dim, hl =
+// head within the pass, kp = key parity (the thread streams keys kp, kp + KP, ...).
+template <typename T, int LPK, int RMAX>
+__global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams p, int HG, int KP) {
+  // fp16 (cos, sin) per dim; rows padded by 16 bytes so the key groups of a wave start on
+  // different banks
+  constexpr int TS = RMAX + 4;
+  __shared__ __attribute__((aligned(16))) uint32_t tab_s[kSplit * TS];
+  __shared__ float s_lds[kMaxHG][kSplit];
+  __shared__ float red_o[kThreads][8];
+  __shared__ float red_ml[kThreads / LPK][2];
+  __shared__ uint8_t vis_s[kSplit];
+
+  const int tid = threadIdx.x;
   const int split = blockIdx.x % p.splits;
-  const int bh = blockIdx.x / p.splits;
-  const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
+  const int b = blockIdx.x / p.splits;
   const int D = p.D, R = p.R, Nk = p.Nk;
-  const int ks = lane / LPK, c = lane % LPK, d0 = 8 * c;
-  const bool cact = d0 < D;
+  const int c = tid % LPK, rest = tid / LPK, hl = rest % HG, kp = rest / HG;
+  const bool active = kp < KP;
+  const int d0 = 8 * c;
+  const bool cact = active && d0 < D;
+  const bool rot = cact && d0 < R;   // R is a multiple of 8: a chunk is all rotated or all pass-through
   const int j_begin = split * kSplit;
+  const int nkeys = min(kSplit, Nk - j_begin);
   const uint8_t* mrow = p.has_mask ? p.mask + (int64_t)b * p.mask_sb : nullptr;
-  float* po = p.part_o + ((int64_t)bh * p.splits + split) * D;
-  float* pml = p.part_ml + ((int64_t)bh * p.splits + split) * 2;
 
-  // ---- skip splits without a visible key ----------------------------------
+  // ---- key visibility of the split into LDS; skip splits without a visible key ----
   int vis_any = 0;
-  for (int j = j_begin + tid; j < min(j_begin + kSplit, Nk); j += kThreads)
-    vis_any |= (!p.has_mask || mrow[j] != 0);
+  for (int j = tid; j < kSplit; j += kThreads) {
+    const int v = j < nkeys && (!p.has_mask || mrow[j_begin + j] != 0);
+    vis_s[j] = (uint8_t)v;
+    vis_any |= v;
+  }
   if (!__syncthreads_or(vis_any)) {
-    if (tid < D) po[tid] = 0.f;
-    if (tid == 0) {
-      pml[0] = -INFINITY;
-      pml[1] = 0.f;
+    for (int i = tid; i < p.Hq * (D + 2); i += kThreads) {
+      const int h = i / (D + 2), e = i % (D + 2);
+      const int64_t row = ((int64_t)b * p.Hq + h) * p.splits + split;
+      if (e < D) p.part_o[row * D + e] = 0.f;
+      else p.part_ml[row * 2 + (e - D)] = e == D ? -INFINITY : 0.f;
     }
     return;
   }
 
-  // ---- query weights of this lane's 8 dims ----------------------------------
-  float wa[8], wb[8];
-  {
-    const int q_off = Nk - 1;
-    const uint16_t* qrow = p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1];
-    float x[8];
-    unpack8<T>(cact ? ld16(qrow + d0) : u32x4{0u, 0u, 0u, 0u}, x);
-    const float* frow = R ? p.freqs + (int64_t)b * p.f_s[0] + (int64_t)h * p.f_s[1] + (int64_t)q_off * p.f_s[2] : nullptr;
-    const float* brow = R ? p.bias + (int64_t)hk * p.bias_sh : nullptr;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int d = d0 + s;
-      if (cact && d < R) {
-        float sn, cs;
-        sincos_acc(frow[d] - brow[d], &sn, &cs);
-        const float a = softplus_f(x[s]);
-        wa[s] = a * cs;
-        wb[s] = a * sn;
-      } else {
-        wa[s] = cact ? x[s] : 0.f;
-        wb[s] = 0.f;
-      }
+  // ---- stage the split's table rows (rows past Nk repeat the last row) ---------
+  if (R) {
+    const uint32_t* tsrc = p.table + (int64_t)b * p.t_sb;
+    const int n4 = kSplit * R / 4;
+    for (int i = tid; i < n4; i += kThreads) {
+      const int r = i / (R / 4), c4 = i % (R / 4);
+      const int jj = min(j_begin + r, Nk - 1);
+      *reinterpret_cast<u32x4*>(tab_s + r * TS + 4 * c4) = reinterpret_cast<const u32x4*>(tsrc + (int64_t)jj * R)[c4];
     }
   }
+  __syncthreads();
 
-  const uint16_t* kbase = p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1];
-  const uint16_t* vbase = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
-  const float2* tbase = R ? p.table + (int64_t)b * p.t_sb + (int64_t)h * p.t_sh : nullptr;
-  const bool rot = cact && d0 < R;   // R is a multiple of 8: a chunk is all rotated or all pass-through
+  const int nb = (nkeys - kp + KP * kBatch - 1) / (KP * kBatch);   // batches of this thread
+  // keys of a batch past the split end read clamped rows and score -inf (vis_s = 0)
+  for (int hg0 = 0; hg0 < p.Hq; hg0 += HG) {
+    const int h = hg0 + hl;
+    const bool hact = active && h < p.Hq;
+    const int hs = hact ? h : 0;
+    const int hk = hs % p.Hk;
+    const int nbh = hact ? nb : 0;
 
-  // ---- pass 1: scaled scores of the split's keys into LDS ---------------------
-  for (int st0 = 0; st0 < NSTEP; st0 += kUnroll) {
-    u32x4 kr[kUnroll];
-    float4 tc[kUnroll][4];
-    bool ok[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int j = j_begin + (st0 + u) * KPS + wave * KPW + ks;
-      ok[u] = j < Nk && (!p.has_mask || mrow[j] != 0);
-      const int jj = min(j, Nk - 1);
-      kr[u] = (ok[u] && cact) ? ld16(kbase + (int64_t)jj * p.k_s[2] + d0) : u32x4{0u, 0u, 0u, 0u};
-      if (rot) {
-        const float4* t = reinterpret_cast<const float4*>(tbase + (int64_t)jj * R + d0);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) tc[u][q] = t[q];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    // ---- query weights of this thread's 8 dims (scale and log2(e) folded in) -----
+    // rotated dims: (wa, wb) as an fp16 pair for v_dot2 with the (cos, sin) table pair
+    float wa[8], wb[8];
+    f16x2 wab[8];
+    {
+      const uint16_t* qrow = p.q + (int64_t)b * p.q_s[0] + (int64_t)hs * p.q_s[1];
       float x[8];
-      unpack8<T>(kr[u], x);
-      float part = 0.f;
-      if (rot) {
+      unpack8<T>(cact ? ld16(qrow + d0) : u32x4{0u, 0u, 0u, 0u}, x);
+      const float* frow = R ? p.freqs + (int64_t)b * p.f_s[0] + (int64_t)(Nk - 1) * p.f_s[2] : nullptr;
+      const float* brow = R ? p.bias + (int64_t)hk * p.bias_sh : nullptr;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 t = tc[u][q];   // (cos, sin) of dims d0 + 2q, d0 + 2q + 1
-          part += softplus_f(x[2 * q]) * (wa[2 * q] * t.x + wb[2 * q] * t.y);
-          part += softplus_f(x[2 * q + 1]) * (wa[2 * q + 1] * t.z + wb[2 * q + 1] * t.w);
+      for (int s = 0; s < 8; ++s) {
+        const int d = d0 + s;
+        if (rot) {
+          float sn, cs;
+          sincos_acc(frow[d] - brow[d], &sn, &cs);
+          const float a = softplus_f(x[s]);
+          wa[s] = a * cs * p.scale_log2;
+          wb[s] = a * sn * p.scale_log2;
+        } else {
+          wa[s] = cact ? x[s] * p.scale_log2 : 0.f;
+          wb[s] = 0.f;
         }
-      } else {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) part += wa[s] * x[s];
+        wab[s] = f16x2{(_Float16)wa[s], (_Float16)wb[s]};
       }
+    }
+    const uint16_t* kbase = p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1];
+    const uint16_t* vbase = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
+
+    // ---- pass 1: scaled scores into LDS ---------------------------------------------
+    // two register sets alternate (no copies): while one batch is computed, the next
+    // one's loads are in flight
+    u32x4 bufA[kBatch], bufB[kBatch];
+    auto fetch = [&](u32x4* buf, const uint16_t* base, int64_t row_stride, int bt) {
 #pragma unroll
-      for (int m = 1; m < LPK; m <<= 1) part += __shfl_xor(part, m, 64);
+      for (int u = 0; u < kBatch; ++u) {
+        // unconditional loads (rows past the cache clamp to its last row): no load waits on
+        // a mask byte, masked keys are dropped at the score
+        const int j = min(j_begin + kp + (bt * kBatch + u) * KP, Nk - 1);
+        buf[u] = cact ? ld16(base + (int64_t)j * row_stride + d0) : u32x4{0u, 0u, 0u, 0u};
+      }
+    };
+    auto score = [&](const u32x4* cur, int bt) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int jl = kp + (bt * kBatch + u) * KP;
+        float x[8];
+        unpack8<T>(cur[u], x);
+        float part = 0.f;
+        if (rot) {
+          const u32x4* t = reinterpret_cast<const u32x4*>(tab_s + min(jl, kSplit - 1) * TS + d0);
+          const u32x4 t0 = t[0], t1 = t[1];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            // (cos, sin) of dim d0 + q dotted with (wa, wb), accumulated in fp32
+            const f16x2 cs = __builtin_bit_cast(f16x2, q < 4 ? t0[q] : t1[q - 4]);
+            part = fmaf(softplus_f(x[q]), __builtin_amdgcn_fdot2(cs, wab[q], 0.f, false), part);
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) part += wa[q] * x[q];
+        }
+#pragma unroll
+        for (int m = 1; m < LPK; m <<= 1) part += __shfl_xor(part, m, 64);
+        if (c == 0 && jl < kSplit) s_lds[hl][jl] = vis_s[jl] ? part : -INFINITY;
+      }
+    };
+    if (nbh > 0) fetch(bufA, kbase, p.k_s[2], 0);
+    for (int bt = 0; bt < nbh; bt += 2) {
+      if (bt + 1 < nbh) fetch(bufB, kbase, p.k_s[2], bt + 1);
+      score(bufA, bt);
+      if (bt + 1 < nbh) {
+        if (bt + 2 < nbh) fetch(bufA, kbase, p.k_s[2], bt + 2);
+        score(bufB, bt + 1);
+      }
+    }
+    __syncthreads();
+
+    // ---- each head's max over the split (LPK * KP threads per head) -----------------
+    float mx = -INFINITY;
+    if (hact)
+      for (int i = c + LPK * kp; i < kSplit; i += LPK * KP) mx = fmaxf(mx, s_lds[hl][i]);
+    red_o[tid][0] = mx;   // partial max per (hl, kp, c)
+    __syncthreads();
+    if (hact) {
+      float m2 = -INFINITY;
+      for (int k2 = 0; k2 < KP; ++k2)
+        for (int c2 = 0; c2 < LPK; ++c2) m2 = fmaxf(m2, red_o[(hl + HG * k2) * LPK + c2][0]);
+      mx = m2;
+    }
+    __syncthreads();
+    const float mu = mx == -INFINITY ? 0.f : mx;
+
+    // ---- pass 2: p = exp2(s - m), o += p v ---------------------------------------
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float lsum = 0.f;
+    auto accumulate = [&](const u32x4* cur, int bt) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int jl = kp + (bt * kBatch + u) * KP;
+        const float pv = jl < kSplit ? __builtin_amdgcn_exp2f(s_lds[hl][jl] - mu) : 0.f;   // 0 when masked
+        float x[8];
+        unpack8<T>(cur[u], x);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) acc[s] = fmaf(pv, x[s], acc[s]);
+        lsum += pv;
+      }
+    };
+    if (nbh > 0) fetch(bufA, vbase, p.v_s[2], 0);
+    for (int bt = 0; bt < nbh; bt += 2) {
+      if (bt + 1 < nbh) fetch(bufB, vbase, p.v_s[2], bt + 1);
+      accumulate(bufA, bt);
+      if (bt + 1 < nbh) {
+        if (bt + 2 < nbh) fetch(bufA, vbase, p.v_s[2], bt + 2);
+        accumulate(bufB, bt + 1);
+      }
+    }
+
+    // ---- merge the KP key parities of each (head, chunk), write the partial -------
+#pragma unroll
+    for (int s = 0; s < 8; ++s) red_o[tid][s] = acc[s];
+    if (c == 0) red_ml[rest][1] = lsum;
+    __syncthreads();
+    if (hact && kp == 0) {
+      float o8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      float L = 0.f;
+      for (int k2 = 0; k2 < KP; ++k2) {
+        const int r2 = hl + HG * k2;
+        L += red_ml[r2][1];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) o8[s] += red_o[r2 * LPK + c][s];
+      }
+      const int64_t row = ((int64_t)b * p.Hq + h) * p.splits + split;
+      if (cact) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+          if (d0 + s < D) p.part_o[row * D + d0 + s] = o8[s];
+      }
       if (c == 0) {
-        const int jl = (st0 + u) * KPS + wave * KPW + ks;
-        s_lds[jl] = ok[u] ? part * p.scale_log2 : -INFINITY;
+        p.part_ml[row * 2] = mx;
+        p.part_ml[row * 2 + 1] = L;
       }
     }
-  }
-  __syncthreads();
-
-  // ---- split max ---------------------------------------------------------------
-  float mx = -INFINITY;
-  for (int i = tid; i < kSplit; i += kThreads) mx = fmaxf(mx, s_lds[i]);
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-  if (lane == 0) red[wave][0] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0]));
-  __syncthreads();
-
-  // ---- pass 2: p = exp2(s - m), o += p v ---------------------------------------
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float lsum = 0.f;
-  for (int st0 = 0; st0 < NSTEP; st0 += kUnroll) {
-    u32x4 vr[kUnroll];
-    float pv[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int jl = (st0 + u) * KPS + wave * KPW + ks;
-      const int j = j_begin + jl;
-      pv[u] = __builtin_amdgcn_exp2f(s_lds[jl] - mx);   // 0 for masked keys (s = -inf)
-      vr[u] = (pv[u] > 0.f && cact) ? ld16(vbase + (int64_t)min(j, Nk - 1) * p.v_s[2] + d0) : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      float x[8];
-      unpack8<T>(vr[u], x);
-#pragma unroll
-      for (int s = 0; s < 8; ++s) acc[s] = fmaf(pv[u], x[s], acc[s]);
-      lsum += pv[u];
-    }
-  }
-  // reduce over the key slots of the wave (lanes with the same chunk), then over waves
-#pragma unroll
-  for (int m = LPK; m < 64; m <<= 1) {
-#pragma unroll
-    for (int s = 0; s < 8; ++s) acc[s] += __shfl_xor(acc[s], m, 64);
-    lsum += __shfl_xor(lsum, m, 64);
-  }
-  if (ks == 0) {
-#pragma unroll
-    for (int s = 0; s < 8; ++s) red[wave][d0 + s] = acc[s];
-    if (c == 0) red_l[wave] = lsum;
-  }
-  __syncthreads();
-  if (tid < D) po[tid] = red[0][tid] + red[1][tid] + red[2][tid] + red[3][tid];
-  if (tid == 0) {
-    pml[0] = mx;
-    pml[1] = red_l[0] + red_l[1] + red_l[2] + red_l[3];
+    __syncthreads();
   }
 }
 
-// One wave per (batch, head): merge the splits by log-sum-exp.
+// One workgroup per (batch, head): merge the splits by log-sum-exp.
 template <typename T>
-__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
-  const int bh = blockIdx.x, lane = threadIdx.x;
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
+  __shared__ float w_s[1024];
+  __shared__ float red[4];
+  __shared__ float part[4][128];
+  const int bh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = bh / p.Hq, h = bh % p.Hq;
   const int D = p.D, S = p.splits;
   const float* pml = p.part_ml + (int64_t)bh * S * 2;
   const float* po = p.part_o + (int64_t)bh * S * D;
   float M = -INFINITY;
-  for (int s = lane; s < S; s += 64) M = fmaxf(M, pml[2 * s]);
+  for (int s = tid; s < S; s += 256) M = fmaxf(M, pml[2 * s]);
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) M = fmaxf(M, __shfl_xor(M, m, 64));
+  if (lane == 0) red[wave] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float Mu = M == -INFINITY ? 0.f : M;
+  __syncthreads();
   float L = 0.f;
-  for (int s = lane; s < S; s += 64) L += pml[2 * s + 1] * __builtin_amdgcn_exp2f(pml[2 * s] - Mu);
+  for (int s = tid; s < S; s += 256) {
+    const float w = __builtin_amdgcn_exp2f(pml[2 * s] - Mu);
+    if (s < 1024) w_s[s] = w;
+    L += pml[2 * s + 1] * w;
+  }
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) L += __shfl_xor(L, m, 64);
+  if (lane == 0) red[wave] = L;
+  __syncthreads();
+  L = red[0] + red[1] + red[2] + red[3];
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1];
-  for (int d = lane; d < D; d += 64) {
+  // thread = (split group g of 4, dim d): 4 groups x up to 64 dims per pass
+  for (int d0 = 0; d0 < D; d0 += 64) {
+    const int d = d0 + lane;
     float acc = 0.f;
-    for (int s = 0; s < S; ++s) acc += po[(int64_t)s * D + d] * __builtin_amdgcn_exp2f(pml[2 * s] - Mu);
-    orow[d] = T::bits(acc * inv);
+    if (d < D) {
+      int s = wave;
+      for (; s + 28 < S; s += 32) {   // 8 independent loads in flight
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = po[(int64_t)(s + 4 * u) * D + d];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int su = s + 4 * u;
+          acc += v[u] * (su < 1024 ? w_s[su] : __builtin_amdgcn_exp2f(pml[2 * su] - Mu));
+        }
+      }
+      for (; s < S; s += 4) acc += po[(int64_t)s * D + d] * (s < 1024 ? w_s[s] : __builtin_amdgcn_exp2f(pml[2 * s] - Mu));
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && d < D) {
+      uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1];
+      orow[d] = T::bits((part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane]) * inv);
+    }
+    __syncthreads();
   }
-  if (lane == 0) p.lse[bh] = L > 0.f ? (M + __builtin_amdgcn_logf(L)) * kLn2 : -INFINITY;
+  if (tid == 0) p.lse[bh] = L > 0.f ? (M + __builtin_amdgcn_logf(L)) * kLn2 : -INFINITY;
 }
 
-template <typename T, int LPK>
+template <typename T, int LPK, int RMAX>
 hipError_t launch_t(const DecodeParams& p, hipStream_t s) {
-  hipError_t e = launch_named("flash_decode_split", decode_split_kernel<T, LPK>, dim3(p.B * p.Hq * p.splits),
-                              dim3(kThreads), s, p);
+  int HG = kThreads / LPK < kMaxHG ? kThreads / LPK : kMaxHG;
+  if (p.Hq < HG) HG = p.Hq;
+  const int KP = (kThreads / LPK) / HG;
+  hipError_t e = launch_named("flash_decode_split", decode_split_kernel<T, LPK, RMAX>, dim3(p.B * p.splits),
+                              dim3(kThreads), s, p, HG, KP);
   if (e != hipSuccess) return e;
-  return launch_named("flash_decode_combine", decode_combine_kernel<T>, dim3(p.B * p.Hq), dim3(64), s, p);
+  return launch_named("flash_decode_combine", decode_combine_kernel<T>, dim3(p.B * p.Hq), dim3(256), s, p);
 }
 
 template <typename T>
 hipError_t dispatch(const DecodeParams& p, hipStream_t s) {
   const int chunks = p.D / 8;
-  if (chunks <= 4) return launch_t<T, 4>(p, s);
-  if (chunks <= 8) return launch_t<T, 8>(p, s);
-  if (chunks <= 16) return launch_t<T, 16>(p, s);
+  if (chunks <= 4) return launch_t<T, 4, 32>(p, s);
+  if (chunks <= 8) return launch_t<T, 8, 64>(p, s);
+  if (chunks <= 16) return p.R <= 64 ? launch_t<T, 16, 64>(p, s) : launch_t<T, 16, 128>(p, s);
   return hipErrorInvalidValue;
 }
 
@@ -246,7 +347,8 @@ hipError_t dispatch(const DecodeParams& p, hipStream_t s) {
 int decode_split_keys() { return kSplit; }
 
 hipError_t launch_flash_decode(const DecodeParams& p, int dtype, hipStream_t s) {
-  if (p.Nq != 1 || p.causal || p.D > 128) return hipErrorInvalidValue;
+  // per-head phase tables would need a table chunk per head: the general forward covers them
+  if (p.Nq != 1 || p.causal || p.D > 128 || p.t_sh != 0) return hipErrorInvalidValue;
   return dtype == 2 ? dispatch<BF16>(p, s) : dispatch<F16>(p, s);
 }
 

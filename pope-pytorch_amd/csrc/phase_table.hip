@@ -1,6 +1,6 @@
 // Per-call cos/sin table of the PoPE phases.
 //
-// tab[((bt * Ht + ht) * rows + n) * R + d] = (cos th, sin th),
+// tab[((bt * Ht + ht) * rows + n) * R + d] = (cos th, sin th), fp32 pairs or fp16 pairs,
 //   th = fl(F[bt, ht, n, d] + bias[ht, d])   (bias optional)
 // The sum is rounded to fp32 before the trig call, as the reference does
 // (freqs_with_bias = freqs + bias, pope.py:56; theta_k = fk + bias,
@@ -24,7 +24,12 @@ __global__ __launch_bounds__(256) void phase_table_kernel(TableParams p) {
     if (p.bias) th = th + p.bias[(int64_t)ht * p.bias_sh + d];
     float s, c;
     sincos_acc(th, &s, &c);
-    p.out[idx] = make_float2(c, s);
+    if (p.out16) {
+      const f16x2 v = {(_Float16)c, (_Float16)s};
+      p.out16[idx] = __builtin_bit_cast(uint32_t, v);
+    } else {
+      p.out[idx] = make_float2(c, s);
+    }
   }
 }
 

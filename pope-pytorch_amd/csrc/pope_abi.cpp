@@ -163,16 +163,22 @@ int decode_splits(const pope_desc& d) {
   return (d.Nk + per - 1) / per;
 }
 
-size_t decode_ws(const pope_desc& d) {
+size_t decode_table_bytes(const pope_desc& d) {
   const Geo g = geometry(d, d.Hq);
+  return d.R > 0 ? align_up((size_t)g.Bt * g.Ht * d.Nk * d.R * sizeof(uint32_t)) : 0;
+}
+
+size_t decode_ws(const pope_desc& d) {
   const int splits = decode_splits(d);
   const size_t rows = (size_t)d.B * d.Hq * d.Nq;
-  return g.table + align_up(rows * splits * d.D * sizeof(float)) + align_up(rows * splits * 2 * sizeof(float));
+  return decode_table_bytes(d) + align_up(rows * splits * d.D * sizeof(float)) +
+         align_up(rows * splits * 2 * sizeof(float));
 }
 
 hipError_t build_table(const pope_desc& d, const float* freqs, const float* bias, int Bt, int Ht,
-                       float2* out, hipStream_t s) {
+                       float2* out, hipStream_t s, uint32_t* out16 = nullptr) {
   pope::TableParams t;
+  t.out16 = out16;
   t.freqs = freqs;
   t.f_sb = d.f_s[0];
   t.f_sh = d.f_s[1];
@@ -434,11 +440,12 @@ int pope_flash_decode(const pope_desc* d, const void* q, const void* k, const vo
   char* ws = static_cast<char*>(workspace);
   const int splits = decode_splits(*d);
   const size_t rows = (size_t)d->B * d->Hq * d->Nq;
-  float2* table = reinterpret_cast<float2*>(ws);
-  float* part_o = reinterpret_cast<float*>(ws + g.table);
-  float* part_ml = reinterpret_cast<float*>(ws + g.table + align_up(rows * splits * d->D * sizeof(float)));
+  uint32_t* table = reinterpret_cast<uint32_t*>(ws);
+  const size_t tb = decode_table_bytes(*d);
+  float* part_o = reinterpret_cast<float*>(ws + tb);
+  float* part_ml = reinterpret_cast<float*>(ws + tb + align_up(rows * splits * d->D * sizeof(float)));
   if (d->R > 0) {
-    hipError_t e = build_table(*d, freqs, nullptr, g.Bt, g.Ht, table, s);
+    hipError_t e = build_table(*d, freqs, nullptr, g.Bt, g.Ht, nullptr, s, table);
     if (e != hipSuccess) return hip_fail(e, "phase table launch");
   }
   pope::DecodeParams p;

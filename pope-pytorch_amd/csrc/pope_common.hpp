@@ -69,11 +69,12 @@ struct F16 {
   }
 };
 
-// softplus in fp32 with hardware exp2/log2: max(x,0) + ln(1 + e^-|x|), x > 20 -> x.
+// softplus in fp32 with hardware exp2/log2: max(x, 0) + ln(1 + e^-|x|).  For |x| > 16.6,
+// e^-|x| < 2^-24 and fl(1 + e^-|x|) = 1, so the result is max(x, 0) exactly: the
+// reference's threshold (x > 20 -> x, beta = 1) holds without a test.
 __device__ __forceinline__ float softplus_f(float x) {
-  float e = __builtin_amdgcn_exp2f(-fabsf(x) * kLog2e);
-  float y = fmaxf(x, 0.f) + __builtin_amdgcn_logf(1.f + e) * kLn2;
-  return x > 20.f ? x : y;
+  const float e = __builtin_amdgcn_exp2f(-fabsf(x) * kLog2e);
+  return fmaf(__builtin_amdgcn_logf(1.f + e), kLn2, fmaxf(x, 0.f));
 }
 
 // d softplus / dx = sigmoid(x).

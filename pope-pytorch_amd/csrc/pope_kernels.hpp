@@ -29,7 +29,8 @@ struct TableParams {
   const float* freqs; int64_t f_sb, f_sh, f_sn;
   const float* bias; int64_t bias_sh;  // may be null
   int Bt, Ht, rows, R;
-  float2* out;
+  float2* out;               // fp32 (cos, sin), or
+  uint32_t* out16;           // fp16 (cos, sin) pairs packed per 32-bit word when non-null
 };
 hipError_t launch_phase_table(const TableParams& p, hipStream_t s);
 
@@ -93,7 +94,7 @@ hipError_t launch_sim_bwd_ws(const SimParams& p, float* U, float* W, hipStream_t
 struct DecodeParams {
   const uint16_t* q; const uint16_t* k; const uint16_t* v;
   const float* freqs; const float* bias; const uint8_t* mask;
-  const float2* table;
+  const uint32_t* table;     // fp16 (cos, sin) of F[b, h, n, d] for n < Nk, packed per 32-bit word
   uint16_t* o; float* lse;
   float* part_o; float* part_ml;   // split-K partials (B*Hq*Nq, splits, D) and (.., splits, 2)
   int B, Hq, Hk, Nq, Nk, D, R, causal, has_mask, splits, keys_per_split;
