@@ -84,9 +84,11 @@ __global__ __launch_bounds__(256) void bwd_prep_q_kernel(FlashBwdParams p) {
   const int q_off = p.Nk - p.Nq;
   uint16_t* qh_row = p.qh + ((int64_t)bh * NqP + i) * EP;
 
-  if (c == nitem - 1) {   // delta = rowsum(O * dO)
-    float dl = 0.f;
+  if (c == nitem - 1) {   // (lse * log2 e, delta = rowsum(O * dO))
+    float dl = 0.f, l2 = INFINITY;
     if (valid) {
+      const float l = p.lse[(int64_t)bh * p.Nq + i];
+      l2 = l == -INFINITY ? INFINITY : l * kLog2e;
       const uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1] + (int64_t)i * p.o_s[2];
       const uint16_t* drow = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1] + (int64_t)i * p.do_s[2];
       for (int d0 = 0; d0 < D; d0 += 8) {
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(256) void bwd_prep_q_kernel(FlashBwdParams p) {
         for (int s = 0; s < 8; ++s) dl += xo[s] * xd[s];
       }
     }
-    p.delta[(int64_t)bh * NqP + i] = dl;
+    p.ld[(int64_t)bh * NqP + i] = make_float2(l2, dl);
     return;
   }
   if (c >= D / 8) {   // zero padding columns [E, EP)
@@ -145,7 +147,7 @@ struct BwdCfg {
   static constexpr int QH = 8 * lds_units_tr(EP / 8), DO = 8 * lds_units_tr(DV / 8);
   static constexpr int VR = 8 * lds_units_rows(DV / 8);
   // dK/dV stage: Q_hat tile, dO tile, lse and delta
-  static constexpr int KV_STAGE = (BMK * QH + BMK * DO) * 2 + 2 * BMK * 4;
+  static constexpr int KV_STAGE = (BMK * QH + BMK * DO) * 2 + BMK * 8;
   // dQ stage: K_hat tile, V tile
   static constexpr int Q_STAGE = (BNQ * QH + BNQ * VR) * 2;
   static constexpr int STAGE = KV_STAGE > Q_STAGE ? KV_STAGE : Q_STAGE;
@@ -169,7 +171,7 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
   constexpr int QLD = (QCH + kThreads - 1) / kThreads, DLD = (DCH + kThreads - 1) / kThreads;
   typedef typename T::vec8 vec8;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
+  const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int b = bhk / p.Hk, hk = bhk % p.Hk;
   const int D = p.D, R = p.R, Nq = p.Nq, Nk = p.Nk, NqP = p.NqP;
   const int j0 = kb * 128;
@@ -212,78 +214,78 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
   const int per_head = nqt - qt0;
   const int nsteps = any_key ? groups * per_head : 0;
 
-  // staging of one query tile: global -> registers -> LDS
+  // staging of one query tile: global -> registers -> LDS.  The fetch cursor (fg, fqt) walks
+  // the group heads and query tiles in step order; pointers are per-job bases plus offsets.
   u32x4 qpf[QLD], dpf[DLD];
-  float lpf = 0.f, dlpf = 0.f;
-  auto fetch = [&](int st) {
-    const int g = st / per_head, qt = qt0 + st % per_head;
-    const int h = hk + g * p.Hk, bh = b * p.Hq + h, i0 = qt * BM;
-    const uint16_t* qh_g = p.qh + ((int64_t)bh * NqP + i0) * EP;
-    const uint16_t* do_g = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1];
+  float2 ldpf = make_float2(0.f, 0.f);
+  const uint16_t* qh_job = p.qh + (int64_t)(b * p.Hq + hk) * NqP * EP;
+  const int64_t qh_hstride = (int64_t)p.Hk * NqP * EP;
+  const uint16_t* do_job = p.dout + (int64_t)b * p.do_s[0] + (int64_t)hk * p.do_s[1];
+  const int64_t do_hstride = (int64_t)p.Hk * p.do_s[1];
+  const int do_rs = (int)p.do_s[2];
+  const float2* ld_job = p.ld + (int64_t)(b * p.Hq + hk) * NqP;
+  const int64_t ld_hstride = (int64_t)p.Hk * NqP;
+  int fg = 0, fqt = qt0;
+  auto fetch = [&]() {
+    const int i0 = fqt * BM;
+    const uint16_t* qh_g = qh_job + fg * qh_hstride + (int64_t)i0 * EP;
+    const uint16_t* do_g = do_job + fg * do_hstride;
+    // Branch-free: chunk counts are whole multiples of the thread count where possible; rows
+    // past Nq clamp to the last row (their P is 0: lse = +inf) and dims past D to the last
+    // chunk (those columns only meet zero V columns, and their dV is never stored).
 #pragma unroll
     for (int m = 0; m < QLD; ++m) {
       const int c = tid + m * kThreads;
-      if (c < QCH) qpf[m] = ld16(qh_g + (int64_t)(c / (EP / 8)) * EP + 8 * (c % (EP / 8)));
+      if (QCH % kThreads == 0 || c < QCH) qpf[m] = ld16(qh_g + (c / (EP / 8)) * EP + 8 * (c % (EP / 8)));
     }
 #pragma unroll
     for (int m = 0; m < DLD; ++m) {
       const int c = tid + m * kThreads;
-      dpf[m] = zero4();
-      if (c < DCH) {
-        const int row = c / (DV / 8), c8 = c % (DV / 8);
-        if (i0 + row < Nq && 8 * c8 < D) dpf[m] = ld16(do_g + (int64_t)(i0 + row) * p.do_s[2] + 8 * c8);
+      if (DCH % kThreads == 0 || c < DCH) {
+        const int row = min(i0 + c / (DV / 8), Nq - 1), d8 = min(8 * (c % (DV / 8)), D - 8);
+        dpf[m] = ld16(do_g + (int64_t)row * do_rs + d8);
       }
     }
-    if (tid < BM) {
-      const int i = i0 + tid;
-      const float l = i < Nq ? p.lse[(int64_t)bh * Nq + i] : -INFINITY;
-      lpf = l == -INFINITY ? INFINITY : l * kLog2e;
-      dlpf = p.delta[(int64_t)bh * NqP + i];
+    if (tid < BM) ldpf = ld_job[fg * ld_hstride + i0 + tid];
+    if (++fqt == nqt) {
+      fqt = qt0;
+      ++fg;
     }
   };
   auto stage = [&](int buf) {
     uint16_t* qh_s = reinterpret_cast<uint16_t*>(smem + buf * C::STAGE);
     uint16_t* do_s = qh_s + BM * QH;
-    float* lse_s = reinterpret_cast<float*>(do_s + BM * DO);
+    float2* ld_s = reinterpret_cast<float2*>(do_s + BM * DO);
 #pragma unroll
     for (int m = 0; m < QLD; ++m) {
       const int c = tid + m * kThreads;
       const int row = c / (EP / 8);
-      if (c < QCH) st16(qh_s + row * QH + 8 * lds_swz(row, c % (EP / 8)), qpf[m]);
+      if (QCH % kThreads == 0 || c < QCH) st16(qh_s + row * QH + 8 * lds_swz(row, c % (EP / 8)), qpf[m]);
     }
 #pragma unroll
     for (int m = 0; m < DLD; ++m) {
       const int c = tid + m * kThreads;
       const int row = c / (DV / 8);
-      if (c < DCH) st16(do_s + row * DO + 8 * lds_swz(row, c % (DV / 8)), dpf[m]);
+      if (DCH % kThreads == 0 || c < DCH) st16(do_s + row * DO + 8 * lds_swz(row, c % (DV / 8)), dpf[m]);
     }
-    if (tid < BM) {
-      lse_s[tid] = lpf;
-      lse_s[BM + tid] = dlpf;
-    }
+    if (tid < BM) ld_s[tid] = ldpf;
   };
 
   if (nsteps > 0) {
-    fetch(0);
+    fetch();
     stage(0);
   }
   __syncthreads();
+  int i0 = qt0 * BM;   // query tile of the current step
   for (int st = 0; st < nsteps; ++st) {
     const int buf = st & 1;
-    if (st + 1 < nsteps) fetch(st + 1);
-    const int i0 = (qt0 + st % per_head) * BM;
+    if (st + 1 < nsteps) fetch();
     const uint16_t* qh_s = reinterpret_cast<const uint16_t*>(smem + buf * C::STAGE);
     const uint16_t* do_s = qh_s + BM * QH;
-    const float* lse_s = reinterpret_cast<const float*>(do_s + BM * DO);
-    const float* dl_s = lse_s + BM;
+    const float2* ld_s = reinterpret_cast<const float2*>(do_s + BM * DO);
 #pragma unroll
     for (int qs = 0; qs < QB; ++qs) {
-      f32x16 s, dp;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] = 0.f;
-        dp[r] = 0.f;
-      }
+      f32x16 s = {}, dp = {};
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk)
         s = T::mfma32(as_vec8<vec8>(ld16(qh_s + (32 * qs + lr) * QH + 8 * lds_swz(lr, 2 * kk + hf))), kreg[kk], s);
@@ -294,18 +296,20 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
       // scores become -inf (+inf for a negative scale) so that P = 0.  Rows past Nq and fully
       // masked rows carry lse = +inf, which gives P = 0 without a test.
       if (!wave_vis || (p.causal && i0 + 32 * qs < j0 + 32 * wave + 31)) {
+        POPE_COLD_PATH();
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int qr = 32 * qs + 8 * (r >> 2) + 4 * hf + (r & 3);
-          if (!(kvis && (!p.causal || kj <= i0 + qr))) s[r] = masked;
+          s[r] = (kvis && (!p.causal || kj <= i0 + qr)) ? s[r] : masked;
         }
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int qr = 32 * qs + 8 * (r >> 2) + 4 * hf + (r & 3);
-        const float pv = __builtin_amdgcn_exp2f(fmaf(s[r], p.scale_log2, -lse_s[qr]));
+        const float2 ld = ld_s[qr];
+        const float pv = __builtin_amdgcn_exp2f(fmaf(s[r], p.scale_log2, -ld.x));
         s[r] = pv;
-        dp[r] = pv * (dp[r] - dl_s[qr]);
+        dp[r] = pv * (dp[r] - ld.y);
       }
 #pragma unroll
       for (int g2 = 0; g2 < 2; ++g2) {
@@ -322,6 +326,7 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
     }
     if (st + 1 < nsteps) stage(buf ^ 1);
     __syncthreads();
+    i0 = i0 + BM == nqt * BM ? qt0 * BM : i0 + BM;
   }
 
   // ---- dV: lane = d column, registers = the wave's keys -----------------------
@@ -394,7 +399,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
   constexpr int KLD = (KCH + kThreads - 1) / kThreads, VLD = (VCH + kThreads - 1) / kThreads;
   typedef typename T::vec8 vec8;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
+  const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const int bhk = b * p.Hk + hk;
   const int D = p.D, R = p.R, Nq = p.Nq, Nk = p.Nk, NkP = p.NkP;
@@ -417,12 +422,8 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
     }
   }
   const float masked = p.scale_log2 >= 0.f ? -INFINITY : INFINITY;
-  float lse2 = INFINITY, dl = 0.f;
-  if (qvalid) {
-    const float l = p.lse[(int64_t)bh * Nq + qi];
-    lse2 = l == -INFINITY ? INFINITY : l * kLog2e;
-    dl = p.delta[(int64_t)bh * p.NqP + qi];
-  }
+  const float2 ld = p.ld[(int64_t)bh * p.NqP + qi];   // rows past Nq: lse = +inf
+  const float lse2 = ld.x, dl = ld.y;
 
   f32x16 dqa[EB];
 #pragma unroll
@@ -443,18 +444,19 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
   uint64_t mpf = 0;
   auto fetch = [&](int kt) {
     const int j0 = kt * BN;
+    // Branch-free as in the dK/dV job: keys past Nk clamp to the last row (masked, P = 0) and
+    // dims past D to the last chunk (those columns only meet zero dO columns).
 #pragma unroll
     for (int m = 0; m < KLD; ++m) {
       const int c = tid + m * kThreads;
-      if (c < KCH) kpf[m] = ld16(kh_g + (int64_t)(j0 + c / (EP / 8)) * EP + 8 * (c % (EP / 8)));
+      if (KCH % kThreads == 0 || c < KCH) kpf[m] = ld16(kh_g + (int64_t)(j0 + c / (EP / 8)) * EP + 8 * (c % (EP / 8)));
     }
 #pragma unroll
     for (int m = 0; m < VLD; ++m) {
       const int c = tid + m * kThreads;
-      vpf[m] = zero4();
-      if (c < VCH) {
-        const int row = c / (DV / 8), c8 = c % (DV / 8);
-        if (j0 + row < Nk && 8 * c8 < D) vpf[m] = ld16(v_g + (int64_t)(j0 + row) * p.v_s[2] + 8 * c8);
+      if (VCH % kThreads == 0 || c < VCH) {
+        const int row = min(j0 + c / (DV / 8), Nk - 1), d8 = min(8 * (c % (DV / 8)), D - 8);
+        vpf[m] = ld16(v_g + (int64_t)row * p.v_s[2] + d8);
       }
     }
     if (wave == 0) {   // bit j: key j0 + j visible
@@ -469,12 +471,12 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
     for (int m = 0; m < KLD; ++m) {
       const int c = tid + m * kThreads;
       const int row = c / (EP / 8);
-      if (c < KCH) st16(kh_s + row * KH + 8 * lds_swz(row, c % (EP / 8)), kpf[m]);
+      if (KCH % kThreads == 0 || c < KCH) st16(kh_s + row * KH + 8 * lds_swz(row, c % (EP / 8)), kpf[m]);
     }
 #pragma unroll
     for (int m = 0; m < VLD; ++m) {
       const int c = tid + m * kThreads;
-      if (c < VCH) st16(v_s + (c / (DV / 8)) * VR + 8 * (c % (DV / 8)), vpf[m]);
+      if (VCH % kThreads == 0 || c < VCH) st16(v_s + (c / (DV / 8)) * VR + 8 * (c % (DV / 8)), vpf[m]);
     }
     if (tid == 0) mbits_s[buf] = mpf;
   };
@@ -503,12 +505,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
     }
 #pragma unroll
     for (int ks = 0; ks < NB; ++ks) {
-      f32x16 s, dp;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] = 0.f;
-        dp[r] = 0.f;
-      }
+      f32x16 s = {}, dp = {};
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk)
         s = T::mfma32(as_vec8<vec8>(ld16(kh_s + (32 * ks + lr) * KH + 8 * lds_swz(lr, 2 * kk + hf))), qreg[kk], s);
@@ -516,10 +513,11 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
       for (int kk = 0; kk < DS; ++kk)
         dp = T::mfma32(as_vec8<vec8>(ld16(v_s + (32 * ks + lr) * VR + 16 * kk + 8 * hf)), doreg[kk], dp);
       if (!full) {   // masked scores -> -inf (+inf for a negative scale): P = 0
+        POPE_COLD_PATH();
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kr = 32 * ks + 8 * (r >> 2) + 4 * hf + (r & 3);
-          if (!(((mb >> kr) & 1ull) && (!p.causal || j0 + kr <= qi))) s[r] = masked;
+          s[r] = (((mb >> kr) & 1ull) && (!p.causal || j0 + kr <= qi)) ? s[r] : masked;
         }
       }
 #pragma unroll

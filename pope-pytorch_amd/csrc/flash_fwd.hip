@@ -120,7 +120,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   __shared__ __attribute__((aligned(16))) char smem[C::LDS];
   __shared__ uint64_t mbits_s[2][2];   // [buffer][tile of the pair]: bit j = key j0 + j visible
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
+  const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int grp = wave >> 2, wq = wave & 3;
   const int BH = p.B * p.Hq;
   const int bh = blockIdx.x % BH;
@@ -186,7 +186,6 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
     nt = min(nt, last_q / kBN + 1);
   }
   const int npair = (nt + 1) / 2;
-  const int nch = D / 8;
   const uint16_t* khg = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;
   const uint16_t* vg = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
   const uint8_t* mrow = p.has_mask ? p.mask + (int64_t)b * p.mask_sb : nullptr;
@@ -196,18 +195,19 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   uint64_t mpf = 0;
   auto fetch = [&](int pr) {
     const int j0 = pr * 2 * kBN;
+    // Branch-free: keys past Nk clamp to the last row (masked, P = 0) and dims past D to the
+    // last chunk (those O columns are never stored).
 #pragma unroll
     for (int m = 0; m < C::KLD; ++m) {
       const int c = tid + m * kThreads;
-      if (c < C::KCH) kpf[m] = ld16(khg + (int64_t)(j0 + c / (EP / 8)) * EP + 8 * (c % (EP / 8)));
+      if (C::KCH % kThreads == 0 || c < C::KCH) kpf[m] = ld16(khg + (int64_t)(j0 + c / (EP / 8)) * EP + 8 * (c % (EP / 8)));
     }
 #pragma unroll
     for (int m = 0; m < C::VLD; ++m) {
       const int c = tid + m * kThreads;
-      vpf[m] = u32x4{0u, 0u, 0u, 0u};
-      if (c < C::VCH) {
-        const int row = c / (DV / 8), c8 = c % (DV / 8), key = j0 + row;
-        if (c8 < nch && key < Nk) vpf[m] = ld16(vg + (int64_t)key * p.v_s[2] + 8 * c8);
+      if (C::VCH % kThreads == 0 || c < C::VCH) {
+        const int key = min(j0 + c / (DV / 8), Nk - 1), d8 = min(8 * (c % (DV / 8)), D - 8);
+        vpf[m] = ld16(vg + (int64_t)key * p.v_s[2] + d8);
       }
     }
     if (wave < 2) {   // wave w: visibility bits of tile w of the pair
@@ -221,12 +221,12 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
 #pragma unroll
     for (int m = 0; m < C::KLD; ++m) {
       const int c = tid + m * kThreads;
-      if (c < C::KCH) st16(kh + (c / (EP / 8)) * KH + 8 * (c % (EP / 8)), kpf[m]);
+      if (C::KCH % kThreads == 0 || c < C::KCH) st16(kh + (c / (EP / 8)) * KH + 8 * (c % (EP / 8)), kpf[m]);
     }
 #pragma unroll
     for (int m = 0; m < C::VLD; ++m) {
       const int c = tid + m * kThreads;
-      if (c < C::VCH) st16(vs + (c / (DV / 8)) * VS + 8 * (c % (DV / 8)), vpf[m]);
+      if (C::VCH % kThreads == 0 || c < C::VCH) st16(vs + (c / (DV / 8)) * VS + 8 * (c % (DV / 8)), vpf[m]);
     }
     if (wave < 2 && lane == 0) mbits_s[buf][wave] = mpf;
   };
@@ -253,11 +253,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
       const uint16_t* vs = reinterpret_cast<const uint16_t*>(smem + buf * C::BUF) + 2 * kBN * KH + grp * kBN * VS;
 
       // ---- S^T = K_hat Q_hat^T ---------------------------------------------
-      f32x16 sacc[2];
+      f32x16 sacc[2] = {{}, {}};
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) {
           const vec8 a = as_vec8<vec8>(ld16(kh + (32 * kb + lr) * KH + 16 * kk + 8 * hf));
@@ -275,6 +273,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
           for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb][r]);
         mt *= p.scale_log2;
       } else {
+        POPE_COLD_PATH();
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll

@@ -104,7 +104,7 @@ int check_ws(size_t need, void* ws, size_t have) {
 
 // Flash backward workspace pieces, in order after the phase table (each 256-byte aligned):
 //   Q_hat (B, Hq, NqP, EP), K_hat (B, Hk, NkP, EP)   -- 16-bit elements
-//   delta (B, Hq, NqP)                               -- fp32
+//   (lse * log2 e, delta) (B, Hq, NqP)               -- fp32 pairs
 // with EP = round_up(D + R, 32), DV = round_up(D, 32), NqP / NkP = round_up(N, 128).
 struct BwdLayout {
   int EP, DV, NqP, NkP;
@@ -120,7 +120,7 @@ BwdLayout bwd_layout(const pope_desc& d) {
   size_t off = geometry(d, d.Hq).table;
   L.qh = off;    off += align_up((size_t)d.B * d.Hq * L.NqP * L.EP * 2);
   L.kh = off;    off += align_up((size_t)d.B * d.Hk * L.NkP * L.EP * 2);
-  L.delta = off; off += align_up((size_t)d.B * d.Hq * L.NqP * sizeof(float));
+  L.delta = off; off += align_up((size_t)d.B * d.Hq * L.NqP * 2 * sizeof(float));
   L.total = off;
   return L;
 }
@@ -400,7 +400,7 @@ int pope_flash_bwd(const pope_desc* d, const void* dout, const void* q, const vo
   p.dbias = dbias;
   p.qh = reinterpret_cast<uint16_t*>(ws + L.qh);
   p.kh = reinterpret_cast<uint16_t*>(ws + L.kh);
-  p.delta = reinterpret_cast<float*>(ws + L.delta);
+  p.ld = reinterpret_cast<float2*>(ws + L.delta);
   p.B = d->B; p.Hq = d->Hq; p.Hk = d->Hk; p.Nq = d->Nq; p.Nk = d->Nk; p.D = d->D; p.R = d->R;
   p.E = d->D + d->R;
   p.EP = L.EP;

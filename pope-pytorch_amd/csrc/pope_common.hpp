@@ -114,6 +114,14 @@ __device__ __forceinline__ int xcd_remap(int hw_id, int total) {
 
 __device__ __forceinline__ float wave_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// Marks a rarely taken branch body so the compiler keeps it a branch instead of
+// speculating it into per-lane selects on every path.
+#define POPE_COLD_PATH() asm volatile("")
+
+// Wave index within the workgroup as a scalar: the compiler's divergence analysis then
+// treats conditions on it as uniform and emits scalar branches instead of per-lane selects.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // LDS row strides.  The LDS serves 64 banks of 4 bytes; counted in 16-byte
 // units, a 128-bit row read by 16 lanes (rows r0..r0+15, one unit each) is
 // conflict-free when the row stride is odd, and a transpose read by 32 lanes

@@ -67,7 +67,8 @@ struct FlashBwdParams {
   // workspace, written by the prep kernels (rows past Nq / Nk and columns past E are zero)
   uint16_t* qh;              // (B, Hq, NqP, EP)  expanded queries Q_hat
   uint16_t* kh;              // (B, Hk, NkP, EP)  expanded keys K_hat
-  float* delta;              // (B, Hq, NqP)      rowsum(O * dO)
+  float2* ld;                // (B, Hq, NqP)      (lse * log2(e), rowsum(O * dO)); rows past Nq and
+                             //                   rows with every key masked carry lse = +inf
   int B, Hq, Hk, Nq, Nk, D, R, E, EP, DV, NqP, NkP, causal, has_mask;
   int n_kv_jobs, interleave; // dK/dV jobs of the fused launch; 1 = pair dK/dV and dQ jobs by cost
   float scale, scale_log2;

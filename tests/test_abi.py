@@ -52,8 +52,8 @@ def test_workspace_sizes():
     st, n = _ws(_lib.OP_FLASH_FWD, d)
     assert st == 0 and n == table + 2 * 8 * 256 * 96 * 2            # + K_hat (E = 96 columns)
     st, nb = _ws(_lib.OP_FLASH_BWD, d)
-    # + Q_hat, K_hat (E = 96 columns), delta
-    assert st == 0 and nb == table + 2 * (2 * 8 * 256 * 96 * 2) + 2 * 8 * 256 * 4
+    # + Q_hat, K_hat (E = 96 columns), (lse, delta) pairs
+    assert st == 0 and nb == table + 2 * (2 * 8 * 256 * 96 * 2) + 2 * 8 * 256 * 8
     d3 = _desc(R=0, Nk=200)                                         # no table; K_hat rows padded to 256
     assert _ws(_lib.OP_FLASH_FWD, d3) == (0, 2 * 8 * 256 * 64 * 2)
     ds = _desc(dtype=_lib.POPE_F32, R=64)
