@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define POPE_ABI_VERSION 1
+#define POPE_ABI_VERSION 2
 
 enum pope_dtype { POPE_F32 = 0, POPE_F16 = 1, POPE_BF16 = 2 };
 
@@ -44,6 +44,18 @@ enum pope_status {
 
 enum pope_op { POPE_OP_SIM_FWD = 0, POPE_OP_SIM_BWD = 1, POPE_OP_FLASH_FWD = 2,
                POPE_OP_FLASH_BWD = 3, POPE_OP_FLASH_DECODE = 4 };
+
+/* pope_desc.flags (flash backward only; 0 everywhere else). */
+enum pope_flags {
+  /* The workspace holds the preparation (expanded K/Q rows, phase tables, key visibility)
+   * written by a pope_flash_fwd call with the same descriptor, q, k, freqs, bias and mask,
+   * and not modified since: the backward reuses it instead of recomputing it.  The flash
+   * forward and backward workspaces have the same size and layout. */
+  POPE_FLAG_PREPARED = 1,
+  /* dfreqs / dbias are overwritten (cleared by the library before it accumulates into them)
+   * instead of accumulated into. */
+  POPE_FLAG_ZERO_GRADS = 2
+};
 
 /*
  * Problem descriptor shared by every entry point.
@@ -64,6 +76,7 @@ typedef struct pope_desc {
   int32_t dtype;          /* enum pope_dtype of q, k, v, o and their grads */
   int32_t causal;         /* top-left causal: key j visible to query i iff j <= i */
   float softmax_scale;    /* flash only; the reference default is D ** -0.5 */
+  int32_t flags;          /* enum pope_flags */
   int64_t q_s[3], k_s[3], v_s[3], o_s[3];
   int64_t do_s[3], dq_s[3], dk_s[3], dv_s[3];
   int64_t sim_s[3];       /* similarity output (b, h, i); column stride 1 */
@@ -117,7 +130,9 @@ int pope_flash_fwd(const pope_desc* desc, const void* q, const void* k, const vo
 
 /*
  * Flash attention backward with PoPE.  dq, dk, dv are written (not accumulated);
- * dfreqs / dbias are fp32 and ACCUMULATED into (caller zeroes; NULL = not wanted).
+ * dfreqs / dbias are fp32 and ACCUMULATED into (caller zeroes; NULL = not wanted),
+ * or overwritten with POPE_FLAG_ZERO_GRADS.  With POPE_FLAG_PREPARED the workspace of
+ * the matching pope_flash_fwd call is reused as is.
  * Replaces flash_attn_backward (triton_pope_flash_attn.py:273-335; kernels
  * _bwd_preprocess :119-130 and _bwd_kernel :132-218).
  */

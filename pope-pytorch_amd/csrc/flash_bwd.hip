@@ -18,9 +18,14 @@
 // bias equals the summed key-phase derivative (the reference adds the same
 // quantity, tl.sum(dfk, 0), triton_pope_flash_attn.py:210).
 //
+// Q_hat, K_hat, the cos/sin tables and the key visibility words come from the shared
+// preparation (flash_prep.hip).  Q_hat is pre-scaled by s = softmax_scale * log2(e), so the
+// recomputed score Q_hat K_hat^T is already in log2 units (P = exp2(score - lse * log2 e)) and
+// the dK_hat accumulator dS^T Q_hat carries a factor s that the epilogue turns into
+// softmax_scale by multiplying with ln 2.
+//
 // Launches (all on the caller's stream, no atomics except dfreqs / dbias):
-//   prep_khat  : K_hat rows (flash_fwd.hip, shared with the forward)
-//   prep_q     : Q_hat rows and delta = rowsum(O * dO) in fp32
+//   delta      : (lse * log2 e, rowsum(O * dO)) per query row
 //   bwd_main   : one launch holding two kinds of jobs, one per workgroup of 4 waves
 //     dK/dV job: 128 keys (32 per wave) of one (batch, kv head); loops over the
 //                query heads of its group and the query tiles that can see its
@@ -65,74 +70,46 @@ __device__ __forceinline__ u32x4 pack8(const f32x16& x, int g) {
 }
 
 // ---------------------------------------------------------------------------
-// prep_q: one thread per (batch * query head, padded query row, work item);
-// items [0, R/8) are rotated 8-dim chunks (one sincos per dim feeds both the
-// cos and the sin column), [R/8, D/8) pass-through chunks, then the zero
-// padding chunks up to EP, and a last item computes delta.
+// delta: one thread per (batch * query head, padded query row): (lse * log2 e, rowsum(O * dO))
+// (_bwd_preprocess, triton_pope_flash_attn.py:119-130).  Rows past Nq and rows with every key
+// masked carry lse = +inf, so their P = exp2(s - lse) is 0 without a test.  With `zero_grads`
+// the first threads also clear dfreqs / dbias, which the main kernel accumulates into.
 template <typename T>
-__global__ __launch_bounds__(256) void bwd_prep_q_kernel(FlashBwdParams p) {
-  const int D = p.D, R = p.R, E = p.E, EP = p.EP, NqP = p.NqP;
-  const int nitem = D / 8 + (EP - E) / 8 + 1;
+__global__ __launch_bounds__(256) void bwd_delta_kernel(FlashBwdParams p) {
+  const int D = p.D, NqP = p.NqP;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)p.B * p.Hq * NqP * nitem) return;
-  const int c = (int)(idx % nitem);
-  const int64_t row = idx / nitem;
-  const int i = (int)(row % NqP);
-  const int bh = (int)(row / NqP);
-  const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
-  const bool valid = i < p.Nq;
-  const int q_off = p.Nk - p.Nq;
-  uint16_t* qh_row = p.qh + ((int64_t)bh * NqP + i) * EP;
-
-  if (c == nitem - 1) {   // (lse * log2 e, delta = rowsum(O * dO))
-    float dl = 0.f, l2 = INFINITY;
-    if (valid) {
-      const float l = p.lse[(int64_t)bh * p.Nq + i];
-      l2 = l == -INFINITY ? INFINITY : l * kLog2e;
-      const uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1] + (int64_t)i * p.o_s[2];
-      const uint16_t* drow = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1] + (int64_t)i * p.do_s[2];
-      for (int d0 = 0; d0 < D; d0 += 8) {
-        float xo[8], xd[8];
-        unpack8<T>(ld16(orow + d0), xo);
-        unpack8<T>(ld16(drow + d0), xd);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) dl += xo[s] * xd[s];
+  if (p.zero_grads) {
+    if (p.dbias && idx < (int64_t)p.Hb * p.R) p.dbias[(idx / p.R) * p.bias_sh + idx % p.R] = 0.f;
+    const int64_t ndf = (int64_t)p.Bt * p.Ht * p.Nk * p.R;
+    if (p.dfreqs)
+      for (int64_t x = idx; x < ndf; x += (int64_t)gridDim.x * 256) {
+        const int d = (int)(x % p.R);
+        int64_t rest = x / p.R;
+        const int n = (int)(rest % p.Nk);
+        rest /= p.Nk;
+        const int ht = (int)(rest % p.Ht), bt = (int)(rest / p.Ht);
+        p.dfreqs[(int64_t)bt * p.df_s[0] + (int64_t)ht * p.df_s[1] + (int64_t)n * p.df_s[2] + d] = 0.f;
       }
+  }
+  if (idx >= (int64_t)p.B * p.Hq * NqP) return;
+  const int i = (int)(idx % NqP);
+  const int bh = (int)(idx / NqP);
+  const int b = bh / p.Hq, h = bh % p.Hq;
+  float dl = 0.f, l2 = INFINITY;
+  if (i < p.Nq) {
+    const float l = p.lse[(int64_t)bh * p.Nq + i];
+    l2 = l == -INFINITY ? INFINITY : l * kLog2e;
+    const uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1] + (int64_t)i * p.o_s[2];
+    const uint16_t* drow = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1] + (int64_t)i * p.do_s[2];
+    for (int d0 = 0; d0 < D; d0 += 8) {
+      float xo[8], xd[8];
+      unpack8<T>(ld16(orow + d0), xo);
+      unpack8<T>(ld16(drow + d0), xd);
+#pragma unroll
+      for (int s = 0; s < 8; ++s) dl += xo[s] * xd[s];
     }
-    p.ld[(int64_t)bh * NqP + i] = make_float2(l2, dl);
-    return;
   }
-  if (c >= D / 8) {   // zero padding columns [E, EP)
-    st16(qh_row + E + 8 * (c - D / 8), zero4());
-    return;
-  }
-  const int d0 = 8 * c;
-  u32x4 raw = zero4();
-  if (valid) raw = ld16(p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + (int64_t)i * p.q_s[2] + d0);
-  if (d0 >= R) {
-    st16(qh_row + R + d0, raw);
-    return;
-  }
-  float x[8], oc[8], os[8];
-  unpack8<T>(raw, x);
-  const float* frow = p.freqs + (int64_t)b * p.f_s[0] + (int64_t)h * p.f_s[1] + (int64_t)(q_off + i) * p.f_s[2];
-  const float* brow = p.bias + (int64_t)hk * p.bias_sh;
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    float sn = 0.f, cs = 0.f;
-    if (valid) sincos_acc(frow[d0 + s] - brow[d0 + s], &sn, &cs);
-    const float a = valid ? softplus_f(x[s]) : 0.f;
-    oc[s] = a * cs;
-    os[s] = a * sn;
-  }
-  u32x4 wc, ws;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    wc[s] = T::pack2(oc[2 * s], oc[2 * s + 1]);
-    ws[s] = T::pack2(os[2 * s], os[2 * s + 1]);
-  }
-  st16(qh_row + d0, wc);
-  st16(qh_row + R + d0, ws);
+  p.ld[idx] = make_float2(l2, dl);
 }
 
 // ---------------------------------------------------------------------------
@@ -206,7 +183,7 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
     for (int r = 0; r < 16; ++r) dka[x][r] = 0.f;
 
   const bool wave_vis = __all(kvis);
-  const float masked = p.scale_log2 >= 0.f ? -INFINITY : INFINITY;
+  const float masked = -INFINITY;
   const int any_key = __syncthreads_or(kvis ? 1 : 0);
   const int nqt = (Nq + BM - 1) / BM;
   const int qt0 = p.causal ? min(j0 / BM, nqt) : 0;
@@ -293,7 +270,7 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
       for (int kk = 0; kk < DS; ++kk)
         dp = T::mfma32(as_vec8<vec8>(ld16(do_s + (32 * qs + lr) * DO + 8 * lds_swz(lr, 2 * kk + hf))), vreg[kk], dp);
       // Partial sub-tile (some key of the wave masked, or on the causal diagonal): masked
-      // scores become -inf (+inf for a negative scale) so that P = 0.  Rows past Nq and fully
+      // scores become -inf so that P = 0.  Rows past Nq and fully
       // masked rows carry lse = +inf, which gives P = 0 without a test.
       if (!wave_vis || (p.causal && i0 + 32 * qs < j0 + 32 * wave + 31)) {
         POPE_COLD_PATH();
@@ -307,7 +284,7 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
       for (int r = 0; r < 16; ++r) {
         const int qr = 32 * qs + 8 * (r >> 2) + 4 * hf + (r & 3);
         const float2 ld = ld_s[qr];
-        const float pv = __builtin_amdgcn_exp2f(fmaf(s[r], p.scale_log2, -ld.x));
+        const float pv = __builtin_amdgcn_exp2f(s[r] - ld.x);
         s[r] = pv;
         dp[r] = pv * (dp[r] - ld.y);
       }
@@ -368,13 +345,13 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
       if (d < R) {
         const float x = T::to_float(kb_ptr[(int64_t)key * p.k_s[2] + d]);
         const float2 cs = tb[(int64_t)key * R + d];
-        const float uc = row[d] * p.scale, us = row[R + d] * p.scale;
+        const float uc = row[d] * kLn2, us = row[R + d] * kLn2;
         g = sigmoid_f(x) * (cs.x * uc + cs.y * us);
         const float dpsi = softplus_f(x) * (cs.x * us - cs.y * uc);
         if (dfb) atomicAdd(dfb + (int64_t)key * p.df_s[2] + d, dpsi);
         if (p.dbias) atomicAdd(&dbias_s[d], dpsi);
       } else {
-        g = row[R + d] * p.scale;
+        g = row[R + d] * kLn2;
       }
       dkb[(int64_t)key * p.dk_s[2] + d] = T::bits(g);
     }
@@ -421,7 +398,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
       doreg[kk] = as_vec8<vec8>((qvalid && d0 < D) ? ld16(dr + d0) : zero4());
     }
   }
-  const float masked = p.scale_log2 >= 0.f ? -INFINITY : INFINITY;
+  const float masked = -INFINITY;
   const float2 ld = p.ld[(int64_t)bh * p.NqP + qi];   // rows past Nq: lse = +inf
   const float lse2 = ld.x, dl = ld.y;
 
@@ -512,7 +489,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
 #pragma unroll
       for (int kk = 0; kk < DS; ++kk)
         dp = T::mfma32(as_vec8<vec8>(ld16(v_s + (32 * ks + lr) * VR + 16 * kk + 8 * hf)), doreg[kk], dp);
-      if (!full) {   // masked scores -> -inf (+inf for a negative scale): P = 0
+      if (!full) {   // masked scores -> -inf: P = 0
         POPE_COLD_PATH();
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -521,7 +498,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
         }
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dp[r] = __builtin_amdgcn_exp2f(fmaf(s[r], p.scale_log2, -lse2)) * (dp[r] - dl);
+      for (int r = 0; r < 16; ++r) dp[r] = __builtin_amdgcn_exp2f(s[r] - lse2) * (dp[r] - dl);
 #pragma unroll
       for (int g2 = 0; g2 < 2; ++g2) {
         const vec8 bds = as_vec8<vec8>(pack8<T>(dp, g2));
@@ -539,8 +516,8 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
   float* ebuf = reinterpret_cast<float*>(smem);
   const uint16_t* qb_ptr = p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1];
   uint16_t* dqb = p.dq + (int64_t)b * p.dq_s[0] + (int64_t)h * p.dq_s[1];
-  const float* fb = R ? p.freqs + (int64_t)b * p.f_s[0] + (int64_t)h * p.f_s[1] : nullptr;
-  const float* brow = R ? p.bias + (int64_t)hk * p.bias_sh : nullptr;
+  const float2* tq = R ? p.table + (int64_t)b * p.t_sb + (int64_t)h * p.t_sh : nullptr;
+  const float2* bq = R ? p.btab + (p.Hb > 1 ? hk : 0) * R : nullptr;
   float* dfb = p.dfreqs ? p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)h * p.df_s[1] : nullptr;
   for (int w = 0; w < 4; ++w) {
     __syncthreads();
@@ -559,8 +536,9 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
       float g;
       if (d < R) {
         const float x = T::to_float(qb_ptr[(int64_t)i * p.q_s[2] + d]);
-        float sn, cs;
-        sincos_acc(fb[(int64_t)(q_off + i) * p.f_s[2] + d] - brow[d], &sn, &cs);
+        // cos / sin(F[q_off + i] - bias) from the tables of F and of the bias
+        const float2 tf = tq[(int64_t)(q_off + i) * R + d], tb = bq[d];
+        const float cs = fmaf(tf.x, tb.x, tf.y * tb.y), sn = fmaf(tf.y, tb.x, -tf.x * tb.y);
         const float uc = row[d] * p.scale, us = row[R + d] * p.scale;
         g = sigmoid_f(x) * (cs * uc + sn * us);
         if (dfb) atomicAdd(dfb + (int64_t)(q_off + i) * p.df_s[2] + d, softplus_f(x) * (cs * us - sn * uc));
@@ -609,19 +587,9 @@ __global__ __launch_bounds__(kThreads, (BwdCfg<EP, DV>::MINB)) void bwd_main_ker
 template <typename T, int EP, int DV>
 hipError_t launch_t(const FlashBwdParams& p0, hipStream_t s) {
   FlashBwdParams p = p0;
-  KhatParams kp;
-  kp.k = p.k;
-  kp.k_s[0] = p.k_s[0]; kp.k_s[1] = p.k_s[1]; kp.k_s[2] = p.k_s[2];
-  kp.table = p.table;
-  kp.t_sb = p.t_sb;
-  kp.t_sh = p.t_sh;
-  kp.kh = p.kh;
-  kp.B = p.B; kp.Hk = p.Hk; kp.Nk = p.Nk; kp.NkP = p.NkP; kp.D = p.D; kp.R = p.R; kp.EP = EP;
-  hipError_t e = launch_prep_khat(kp, T::kCode, s);
-  if (e != hipSuccess) return e;
-  const int nitem = p.D / 8 + (EP - p.E) / 8 + 1;
-  const int64_t nq = (int64_t)p.B * p.Hq * p.NqP * nitem;
-  e = launch_named("flash_bwd_prep_q", bwd_prep_q_kernel<T>, dim3((unsigned)((nq + 255) / 256)), dim3(256), s, p);
+  const int64_t nrows = (int64_t)p.B * p.Hq * p.NqP;
+  hipError_t e = launch_named("flash_bwd_delta", bwd_delta_kernel<T>, dim3((unsigned)((nrows + 255) / 256)),
+                              dim3(256), s, p);
   if (e != hipSuccess) return e;
   const int nkb = p.NkP / 128, nqb = p.NqP / 128;
   p.n_kv_jobs = nkb * p.B * p.Hk;

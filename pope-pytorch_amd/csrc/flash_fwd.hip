@@ -3,49 +3,42 @@
 // Reference semantics: triton_pope_flash_attn.py:23-117 (kernel) and :222-271
 // (launcher); PyTorch path attention.py:106-145.
 //
-// Two launches:
-//   fwd_prep_k : K_hat = the polar transform of the keys, written once per call
-//                as (B, Hk, NkP, EP) 16-bit rows (zero past Nk and past E);
-//   flash_fwd  : the attention sweep.
+// Inputs come from the shared preparation (flash_prep.hip): K_hat rows, Q_hat rows pre-scaled
+// by softmax_scale * log2(e) (so S = Q_hat K_hat^T is the score in log2 units) and the key
+// visibility words.  V is read from the caller's tensor.
 //
-// flash_fwd work decomposition
-//   one workgroup = 8 waves = 128 query rows of one (batch, query head).  Waves
-//   0-3 (group 0) and 4-7 (group 1) own the same 128 rows, 32 per wave, and
-//   split the key axis: per iteration the workgroup stages a pair of 64-key
-//   tiles in LDS, group g takes tile 2 t + g.  Each group keeps its own online
-//   softmax state; group 1 hands (m, l, O) to group 0 through LDS at the end.
-//   The next pair of tiles is fetched into registers while the current pair is
-//   computed (LDS double-buffered when it fits the 160 KB of a CU).
-// Per tile and wave
-//   S^T = K_hat Q_hat^T on v_mfma_f32_32x32x16: A = K_hat tile rows (lane =
-//   key), B = the wave's Q_hat held in registers (lane = query).  The result
-//   has one query per lane and keys in registers, so the softmax row
-//   reductions stay in-lane (plus one swap between the two lane halves).
-//   O^T += V^T P^T reuses the probabilities straight from the S registers as
-//   the B operand (a key permutation inside each 16-key group); the A operand
-//   comes from the row-major V tile through LDS transpose reads in the same key
-//   order.  Tiles with every key visible to every row of the wave skip the
-//   per-element masks, and the accumulator is rescaled only when a row's
-//   running max moves.
-// Scheduling
-//   blockIdx -> (query block, batch*head) with the heaviest causal blocks first
-//   and batch*head fastest, so consecutive workgroups land on different XCDs
-//   while every workgroup of one (batch, head) lands on the same XCD (the
-//   dispatcher deals workgroup ids round-robin over the 8 XCDs): its K_hat / V
-//   stay in one L2.  One workgroup per CU; twice as many workgroups as CUs keep
-//   the causal triangle balanced.
-// Phases
-//   The learned bias is moved to the query side: cos(phi - (F_j + b)) =
-//   cos((phi - b) - F_j), so Q_hat = a * (cos, sin)(F[q_off+i] - b) is computed
-//   with accurate sincos and K_hat = c * (cos, sin)(F_j) uses the per-call table
-//   of cos/sin(F).  Differences to the reference's fl(F_j + b) rounding are
-//   below bf16 resolution.
+// Work decomposition
+//   one workgroup = 8 waves = 128 query rows of one (batch, query head).  Waves 0-3 (group 0)
+//   and 4-7 (group 1) own the same 128 rows, 32 per wave, and split the key axis: the
+//   workgroup stages pairs of BN-key tiles, group g takes tile 2 t + g.  Each group keeps its
+//   own online-softmax state; group 1 hands (m, l, O) to group 0 through LDS at the end.
+// Staging
+//   K_hat and V tiles go straight from global memory into LDS (global_load_lds_dwordx4, no
+//   registers), into a ring of three stage slots: while pair t is consumed, pair t + 1 is
+//   resident and pair t + 2 is in flight.  Tiles are unpadded and XOR-swizzled (tile_swz).
+// Per wave and tile
+//   S^T = K_hat Q_hat^T on v_mfma_f32_32x32x16: A = K_hat rows from LDS (lane = key), B = the
+//   wave's Q_hat rows held in registers (lane = query), so every query's scores sit in one
+//   lane pair and the softmax reductions stay in-lane (plus one permlane32 swap).  The
+//   accumulator starts from -m (the running reference max), so the MFMA returns s - m.
+//   O^T += V^T P^T takes the probabilities straight from the S registers as the B operand; V^T
+//   comes from the row-major V tile through LDS transpose reads in the same key order.
+//   The scores of tile t + 1 are multiplied while the softmax of tile t runs on the VALU.
+// Online softmax
+//   p = exp2(s - m) with a lazily updated reference m: m moves only when a row's tile maximum
+//   exceeds it by more than 8 (p <= 2^8 stays exact in fp32 / bf16 range), or on the row's
+//   first visible key.  The row sum is taken from the bf16 probabilities that feed the MFMA
+//   (v_dot2_f32_bf16 against (1, 1)).
 // Masking
-//   top-left causal (key j visible to query i iff j <= i, the SDPA convention
-//   the reference uses, triton_pope_flash_attn.py:64,86-87), key padding mask
-//   (nonzero = keep), keys >= Nk.  Key tiles past the causal diagonal are never
-//   visited; a tile that leaves every row of a wave masked is skipped.  Fully
-//   masked rows give O = 0 and LSE = -inf (:114,117).
+//   top-left causal (key j visible to query i iff j <= i, the SDPA convention the reference
+//   uses, triton_pope_flash_attn.py:64,86-87), key padding mask (nonzero = keep), keys >= Nk.
+//   Tiles past the causal diagonal or past the batch's last visible key are never loaded.
+//   Fully masked rows give O = 0 and LSE = -inf (:114,117).
+// Scheduling
+//   blockIdx -> (query block, batch*head) with the heaviest causal blocks first and
+//   batch*head fastest, so every workgroup of one (batch, head) lands on the same XCD (the
+//   dispatcher deals workgroup ids round-robin over the 8 XCDs) and its K_hat / V stay in one
+//   L2.  One workgroup per CU; twice as many workgroups as CUs balance the causal triangle.
 #include "pope_common.hpp"
 #include "pope_kernels.hpp"
 
@@ -54,71 +47,46 @@ namespace pope {
 namespace {
 
 constexpr int kBM = 128;        // query rows per workgroup
-constexpr int kBN = 64;         // keys per tile (one tile per wave group per iteration)
 constexpr int kThreads = 512;   // 8 waves
-constexpr int kLdsMax = 160 * 1024;
+constexpr int kStages = 3;
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
-__device__ __forceinline__ void st16(uint16_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
-// ---------------------------------------------------------------------------
-// prep_khat: one thread per (batch * kv head, padded key row, 8-column chunk).
-template <typename T>
-__global__ __launch_bounds__(256) void prep_khat_kernel(KhatParams p) {
-  const int nch = p.EP / 8;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)p.B * p.Hk * p.NkP * nch) return;
-  const int c = (int)(idx % nch);
-  const int64_t row = idx / nch;
-  const int j = (int)(row % p.NkP);
-  const int bhk = (int)(row / p.NkP);
-  const int b = bhk / p.Hk, hk = bhk % p.Hk;
-  const int R = p.R, E = p.D + p.R, e0 = 8 * c;
-  u32x4 w = {0u, 0u, 0u, 0u};
-  if (j < p.Nk && e0 < E) {
-    const bool is_cos = e0 < R, is_sin = !is_cos && e0 < 2 * R;
-    const int d0 = is_cos ? e0 : e0 - R;
-    const u32x4 raw = ld16(p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1] + (int64_t)j * p.k_s[2] + d0);
-    if (is_cos || is_sin) {
-      float x[8];
-      unpack8<T>(raw, x);
-      const float2* t = p.table + (int64_t)b * p.t_sb + (int64_t)hk * p.t_sh + (int64_t)j * R + d0;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float2 t0 = t[2 * s], t1 = t[2 * s + 1];
-        const float a0 = softplus_f(x[2 * s]), a1 = softplus_f(x[2 * s + 1]);
-        w[s] = is_cos ? T::pack2(a0 * t0.x, a1 * t1.x) : T::pack2(a0 * t0.y, a1 * t1.y);
-      }
-    } else {
-      w = raw;
-    }
-  }
-  st16(p.kh + ((int64_t)bhk * p.NkP + j) * p.EP + e0, w);
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Direct global -> LDS load of 16 bytes per lane: lane l's bytes land at dst + 16 l (dst is
+// wave-uniform).
+__device__ __forceinline__ void load_lds16(const void* src, void* dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)dst, 16, 0, 0);
 }
 
-// ---------------------------------------------------------------------------
-template <typename T, int EP, int DV>
+template <int EP, int DV>
 struct FwdCfg {
-  static constexpr int KH = 8 * lds_units_rows(EP / 8);   // K_hat row stride: row reads only
-  static constexpr int VS = 8 * lds_units_tr(DV / 8);     // V row stride: transpose reads only
-  static constexpr int BUF = (2 * kBN * KH + 2 * kBN * VS) * 2;   // bytes of one staged pair
-  static constexpr int NBUF = 2 * BUF + 64 <= kLdsMax ? 2 : 1;
-  static constexpr int MERGE = 4 * 64 * (2 + 16 * (DV / 32)) * 4;   // group 1's (m, l, O) hand-off
-  static constexpr int LDS = NBUF * BUF > MERGE ? NBUF * BUF : MERGE;
-  static constexpr int KCH = 2 * kBN * (EP / 8);               // 16-byte K_hat chunks per pair
-  static constexpr int KLD = (KCH + kThreads - 1) / kThreads;  // per thread
-  static constexpr int VCH = 2 * kBN * (DV / 8);               // 16-byte V chunks per pair
-  static constexpr int VLD = (VCH + kThreads - 1) / kThreads;
+  static constexpr int BN = (EP + DV <= 192 && DV <= 64) ? 64 : 32;   // keys per tile
+  static constexpr int KB = BN / 32;                                  // 32-key blocks per tile
+  static constexpr int KS = EP / 16;                                  // 16-wide k steps of S
+  static constexpr int NDB = DV / 32;                                 // 32-row blocks of O^T
+  static constexpr int EPU = EP / 8, DVU = DV / 8;                    // 16-byte units per row
+  static constexpr int KTILE = BN * EP;                               // elements per K_hat tile
+  static constexpr int VTILE = BN * DV;
+  static constexpr int STAGE = 2 * (KTILE + VTILE) * 2;               // bytes per stage slot
+  static constexpr int UNITS = STAGE / 16;
+  static constexpr int KUNITS = 2 * KTILE / 8;
+  static constexpr int LPT = (UNITS + kThreads - 1) / kThreads;       // direct loads per thread
+  static constexpr int MS = 3 + 16 * NDB;                             // floats per lane in the merge
+  static constexpr int MERGE = 4 * 64 * MS * 4;
+  static constexpr int LDS = kStages * STAGE > MERGE ? kStages * STAGE : MERGE;
+  static_assert(KUNITS % 64 == 0 && UNITS % 64 == 0, "loads must split at wave boundaries");
+  static_assert(LDS <= 160 * 1024, "LDS budget");
 };
 
 template <typename T, int EP, int DV>
 __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p) {
-  typedef FwdCfg<T, EP, DV> C;
-  constexpr int KS = EP / 16, NDB = DV / 32, KH = C::KH, VS = C::VS;
+  typedef FwdCfg<EP, DV> C;
+  constexpr int BN = C::BN, KB = C::KB, KS = C::KS, NDB = C::NDB;
   typedef typename T::vec8 vec8;
 
   __shared__ __attribute__((aligned(16))) char smem[C::LDS];
-  __shared__ uint64_t mbits_s[2][2];   // [buffer][tile of the pair]: bit j = key j0 + j visible
 
   const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int grp = wave >> 2, wq = wave & 3;
@@ -126,228 +94,238 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   const int bh = blockIdx.x % BH;
   const int qb = p.nqb - 1 - (int)(blockIdx.x / BH);
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
-  const int D = p.D, R = p.R, E = D + R, Nk = p.Nk, Nq = p.Nq;
-  const int q_off = Nk - Nq;
+  const int Nk = p.Nk, Nq = p.Nq, D = p.D;
   const int qw0 = qb * kBM + wq * 32;   // first query row of this wave
   const int qi = qw0 + lr;
-  const bool qvalid = qi < Nq;
-  const bool fast_ok = p.scale_log2 > 0.f;   // max commutes with the scale
-  const TrLane vtr = tr_lane<false>(C::VS, lane);
 
-  // ---- Q_hat for this lane's query row, in MFMA B-operand order ----------
+  // ---- the wave's Q_hat rows as MFMA B operands --------------------------------
   vec8 qreg[KS];
   {
-    const uint16_t* qrow = p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + (int64_t)min(qi, Nq - 1) * p.q_s[2];
-    const float* frow = R ? p.freqs + (int64_t)b * p.f_s[0] + (int64_t)h * p.f_s[1] +
-                                (int64_t)(q_off + min(qi, Nq - 1)) * p.f_s[2]
-                          : nullptr;
-    const float* brow = R ? p.bias + (int64_t)hk * p.bias_sh : nullptr;
+    const uint16_t* qrow = p.qh + ((int64_t)bh * p.NqP + qi) * EP;
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      const int e0 = 16 * kk + 8 * hf;
-      float out[8];
-      if (!qvalid || e0 >= E) {
+    for (int kk = 0; kk < KS; ++kk) qreg[kk] = as_vec8<vec8>(ld16(qrow + 16 * kk + 8 * hf));
+  }
+
+  // ---- key range: causal bound of the block's last query, last visible key of the batch ----
+  int nkeys = min(p.kend[b], Nk);
+  if (p.causal) nkeys = min(nkeys, min(qb * kBM + kBM, Nq));
+  const int nt = (nkeys + BN - 1) / BN;
+  const int npair = (nt + 1) / 2;
+  const uint64_t* mw = p.mwords + (int64_t)b * p.NW;
+
+  // ---- direct-load plan: unit c = m * 512 + tid of a stage slot ---------------------
+  // K_hat units first (tile g, row r, swizzled unit), then V units.  Offsets are relative
+  // to the pair's first key row j0.
+  const uint16_t* khg = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;
+  const uint16_t* vg = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
+  const int vs2 = (int)p.v_s[2];
+  int ld_row[C::LPT], ld_col[C::LPT];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) out[s] = 0.f;
-      } else {
-        const bool is_cos = e0 < R, is_sin = !is_cos && e0 < 2 * R;
-        const int d0 = is_cos ? e0 : e0 - R;
-        float x[8];
-        unpack8<T>(ld16(qrow + d0), x);
-        if (is_cos || is_sin) {
+  for (int m = 0; m < C::LPT; ++m) {
+    const int c = m * kThreads + tid;
+    if (c < C::KUNITS) {
+      const int g = c / (BN * C::EPU), rem = c % (BN * C::EPU);
+      const int r = rem / C::EPU, u = (rem % C::EPU) ^ tile_swz(C::EPU, r);
+      ld_row[m] = g * BN + r;
+      ld_col[m] = 8 * u;
+    } else {
+      const int cv = c - C::KUNITS;
+      const int g = cv / (BN * C::DVU), rem = cv % (BN * C::DVU);
+      const int r = rem / C::DVU, u = (rem % C::DVU) ^ tile_swz(C::DVU, r);
+      ld_row[m] = g * BN + r;
+      ld_col[m] = min(8 * u, D - 8);   // columns past D repeat the last chunk (never stored)
+    }
+  }
+  auto issue = [&](int pr) {
+    char* slot = smem + (pr % kStages) * C::STAGE;
+    const int j0 = pr * 2 * BN;
 #pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            float sn, cs;
-            sincos_acc(frow[d0 + s] - brow[d0 + s], &sn, &cs);
-            out[s] = softplus_f(x[s]) * (is_cos ? cs : sn);
-          }
-        } else {
+    for (int m = 0; m < C::LPT; ++m) {
+      const int c0 = m * kThreads + wave * 64;   // first unit of this wave's instruction
+      if (C::UNITS % kThreads != 0 && c0 >= C::UNITS) continue;
+      const void* src;
+      if (c0 < C::KUNITS)
+        src = khg + (j0 + ld_row[m]) * EP + ld_col[m];   // K_hat rows are padded to NkP
+      else
+        src = vg + (int64_t)min(j0 + ld_row[m], Nk - 1) * vs2 + ld_col[m];
+      load_lds16(src, slot + c0 * 16);
+    }
+  };
+
+  // ---- LDS operand addressing -------------------------------------------------------
+  // K_hat A operand: row 32 kb + lr, unit 2 kk + hf of tile grp.
+  int koff[KS];
 #pragma unroll
-          for (int s = 0; s < 8; ++s) out[s] = x[s];
-        }
-      }
-      u32x4 w;
+  for (int kk = 0; kk < KS; ++kk) koff[kk] = lr * EP + 8 * ((2 * kk + hf) ^ tile_swz(C::EPU, lr));
+  // V^T A operand (transpose read): rows R0 + 4 h + j / 4 and R0 + 8 + 4 h + j / 4, columns
+  // n0 + 8 u + 4 (j & 1) with u = 2 (gi & 1) + ((j >> 1) & 1) inside the 4-unit group at n0.
+  int voff_lo[NDB], voff_hi[NDB];
+  {
+    const int j = lane & 15, gi = lane >> 4;
+    const int u = 2 * (gi & 1) + ((j >> 1) & 1), sub = 4 * (j & 1);
+    const int rlo = 4 * hf + (j >> 2), rhi = rlo + 8;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) w[s] = T::pack2(out[2 * s], out[2 * s + 1]);
-      qreg[kk] = as_vec8<vec8>(w);
+    for (int db = 0; db < NDB; ++db) {
+      voff_lo[db] = rlo * DV + 8 * ((4 * db + u) ^ tile_swz(C::DVU, rlo)) + sub;
+      voff_hi[db] = rhi * DV + 8 * ((4 * db + u) ^ tile_swz(C::DVU, rhi)) + sub;
     }
   }
 
+  // ---- state -----------------------------------------------------------------------------
   f32x16 oacc[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
-
-  int nt = (Nk + kBN - 1) / kBN;
-  if (p.causal) {
-    const int last_q = min(qb * kBM + kBM, Nq) - 1;
-    nt = min(nt, last_q / kBN + 1);
-  }
-  const int npair = (nt + 1) / 2;
-  const uint16_t* khg = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;
-  const uint16_t* vg = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
-  const uint8_t* mrow = p.has_mask ? p.mask + (int64_t)b * p.mask_sb : nullptr;
-
-  // ---- staging of a pair of tiles: global -> registers -> LDS ----------------
-  u32x4 kpf[C::KLD], vpf[C::VLD];
-  uint64_t mpf = 0;
-  auto fetch = [&](int pr) {
-    const int j0 = pr * 2 * kBN;
-    // Branch-free: keys past Nk clamp to the last row (masked, P = 0) and dims past D to the
-    // last chunk (those O columns are never stored).
+  f32x16 negm;   // -m in every register: the initial accumulator of S
 #pragma unroll
-    for (int m = 0; m < C::KLD; ++m) {
-      const int c = tid + m * kThreads;
-      if (C::KCH % kThreads == 0 || c < C::KCH) kpf[m] = ld16(khg + (int64_t)(j0 + c / (EP / 8)) * EP + 8 * (c % (EP / 8)));
+  for (int r = 0; r < 16; ++r) negm[r] = 0.f;
+  float m_ref = 0.f, l_run = 0.f;
+  bool m_set = false;
+  f32x16 sacc[KB];
+
+  auto kh_tile = [&](int pr) -> const uint16_t* {
+    return reinterpret_cast<const uint16_t*>(smem + (pr % kStages) * C::STAGE) + grp * C::KTILE;
+  };
+  auto v_tile = [&](int pr) -> const uint16_t* {
+    return reinterpret_cast<const uint16_t*>(smem + (pr % kStages) * C::STAGE) + 2 * C::KTILE + grp * C::VTILE;
+  };
+  // S^T - m for the group's tile of pair pr
+  auto qk = [&](int pr, f32x16* s) {
+    const uint16_t* kt = kh_tile(pr);
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      s[kb] = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt + 32 * kb * EP + koff[0])), qreg[0], negm);
+#pragma unroll
+      for (int kk = 1; kk < KS; ++kk)
+        s[kb] = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt + 32 * kb * EP + koff[kk])), qreg[kk], s[kb]);
     }
+  };
+  // masks of the group's tile of pair pr (cold: diagonal and partially visible tiles)
+  auto mask = [&](int pr, f32x16* s) {
+    const int tile = 2 * pr + grp;
+    const int j0 = tile * BN;
+    uint64_t mb = 0;
+    if (tile < nt) {
+      mb = mw[j0 >> 6];
+      if (BN == 32) mb = (mb >> (j0 & 32)) & 0xffffffffull;
+    }
+    const uint64_t all = BN == 64 ? ~0ull : 0xffffffffull;
+    const bool full = mb == all && !(p.causal && j0 + BN - 1 > qw0);
+    if (!full) {
+      POPE_COLD_PATH();
+      // the lane's keys are 32 kb + 8 (r >> 2) + (r & 3) past 4 hf: compile-time bit positions
+      const uint64_t w = mb >> (4 * hf);
+      const int lim = p.causal ? qi - j0 - 4 * hf : BN;   // causal: key offset <= lim
 #pragma unroll
-    for (int m = 0; m < C::VLD; ++m) {
-      const int c = tid + m * kThreads;
-      if (C::VCH % kThreads == 0 || c < C::VCH) {
-        const int key = min(j0 + c / (DV / 8), Nk - 1), d8 = min(8 * (c % (DV / 8)), D - 8);
-        vpf[m] = ld16(vg + (int64_t)key * p.v_s[2] + d8);
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kr = 32 * kb + 8 * (r >> 2) + (r & 3);
+          const bool ok = ((uint32_t)(w >> kr) & 1u) && kr <= lim;
+          s[kb][r] = ok ? s[kb][r] : -INFINITY;
+        }
+    }
+  };
+  // row maximum and the lazy reference update (rare, wave-uniform branch)
+  auto rowmax = [&](f32x16* s) {
+    float mt = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
+    mt = half_swap_max(mt);
+    const bool need = mt > -INFINITY && (!m_set || mt > 8.f);
+    if (__any(need)) {
+      POPE_COLD_PATH();
+      const float sh = need ? mt : 0.f;
+      const float alpha = (need && m_set) ? __builtin_amdgcn_exp2f(-mt) : 1.f;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[kb][r] -= sh;
+      m_ref += sh;
+      m_set = m_set || need;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) negm[r] = -m_ref;
+    }
+  };
+  // probabilities (bf16 / fp16 pairs, in B-operand order) and the row sum
+  auto probs = [&](const f32x16* s, u32x4* pw) {
+    const uint32_t ones = T::pack2(1.f, 1.f);
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t w = T::pack2(__builtin_amdgcn_exp2f(s[kb][8 * g + 2 * q]),
+                                      __builtin_amdgcn_exp2f(s[kb][8 * g + 2 * q + 1]));
+          pw[2 * kb + g][q] = w;
+          l_run = T::dot2(w, ones, l_run);
+        }
+  };
+  // O^T += V^T P^T over the tile's 16-key groups
+  auto pv = [&](int pr, const u32x4* pw) {
+    const uint16_t* vt = v_tile(pr);
+#pragma unroll
+    for (int g16 = 0; g16 < BN / 16; ++g16) {
+      const vec8 pb = as_vec8<vec8>(pw[g16]);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const u32x2 lo = lds_read_tr16(vt + 16 * g16 * DV + voff_lo[db]);
+        const u32x2 hi = lds_read_tr16(vt + 16 * g16 * DV + voff_hi[db]);
+        oacc[db] = T::mfma32(as_vec8<vec8>(u32x4{lo[0], lo[1], hi[0], hi[1]}), pb, oacc[db]);
       }
     }
-    if (wave < 2) {   // wave w: visibility bits of tile w of the pair
-      const int key = j0 + tid;
-      mpf = __ballot(key < Nk && (!p.has_mask || mrow[key] != 0));
-    }
-  };
-  auto stage = [&](int buf) {
-    uint16_t* kh = reinterpret_cast<uint16_t*>(smem + buf * C::BUF);
-    uint16_t* vs = kh + 2 * kBN * KH;
-#pragma unroll
-    for (int m = 0; m < C::KLD; ++m) {
-      const int c = tid + m * kThreads;
-      if (C::KCH % kThreads == 0 || c < C::KCH) st16(kh + (c / (EP / 8)) * KH + 8 * (c % (EP / 8)), kpf[m]);
-    }
-#pragma unroll
-    for (int m = 0; m < C::VLD; ++m) {
-      const int c = tid + m * kThreads;
-      if (C::VCH % kThreads == 0 || c < C::VCH) st16(vs + (c / (DV / 8)) * VS + 8 * (c % (DV / 8)), vpf[m]);
-    }
-    if (wave < 2 && lane == 0) mbits_s[buf][wave] = mpf;
   };
 
+  // ---- main loop ---------------------------------------------------------------------
   if (npair > 0) {
-    fetch(0);
-    stage(0);
-  }
-  __syncthreads();
-
-  for (int t = 0; t < npair; ++t) {
-    const int buf = C::NBUF == 2 ? (t & 1) : 0;
-    if (t + 1 < npair) fetch(t + 1);
-
-    const int tile = 2 * t + grp;
-    const int j0 = tile * kBN;
-    // keys visible to some row of this wave: not all masked, not all after the wave's last query
-    const uint64_t mraw = mbits_s[buf][grp];
-    const uint64_t mb = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)mraw) |
-                        ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(mraw >> 32)) << 32);
-    const bool live = tile < nt && mb != 0 && !(p.causal && j0 > qw0 + 31);
-    if (live) {
-      const uint16_t* kh = reinterpret_cast<const uint16_t*>(smem + buf * C::BUF) + grp * kBN * KH;
-      const uint16_t* vs = reinterpret_cast<const uint16_t*>(smem + buf * C::BUF) + 2 * kBN * KH + grp * kBN * VS;
-
-      // ---- S^T = K_hat Q_hat^T ---------------------------------------------
-      f32x16 sacc[2] = {{}, {}};
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk) {
-          const vec8 a = as_vec8<vec8>(ld16(kh + (32 * kb + lr) * KH + 16 * kk + 8 * hf));
-          sacc[kb] = T::mfma32(a, qreg[kk], sacc[kb]);
-        }
-      }
-      // ---- masks (partial tiles only) + running max -------------------------
-      // full tile: every key visible and (causal) every key <= the wave's first query
-      const bool full = fast_ok && mb == ~0ull && !(p.causal && j0 + kBN - 1 > qw0);
-      float mt = -INFINITY;
-      if (full) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb][r]);
-        mt *= p.scale_log2;
-      } else {
-        POPE_COLD_PATH();
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int kr = 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
-            const bool ok = ((mb >> kr) & 1ull) && (!p.causal || j0 + kr <= qi);
-            const float sv = ok ? sacc[kb][r] * p.scale_log2 : -INFINITY;
-            sacc[kb][r] = sv;
-            mt = fmaxf(mt, sv);
-          }
-      }
-      mt = fmaxf(mt, wave_shfl_xor(mt, 32));
-      const float m_new = fmaxf(m_run, mt);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      if (__any(m_new != m_run)) {   // rescale only when some row's max moved
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-        m_run = m_new;
-      }
-      float psum = 0.f;
-      if (full) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float pr = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r], p.scale_log2, -m_use));
-            sacc[kb][r] = pr;
-            psum += pr;
-          }
-      } else {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float pr = __builtin_amdgcn_exp2f(sacc[kb][r] - m_use);
-            sacc[kb][r] = pr;
-            psum += pr;
-          }
-      }
-      l_run += psum;
-
-      // ---- O^T += V^T P^T: A = V tile read transposed ----------------------
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          u32x4 pw;
-#pragma unroll
-          for (int s = 0; s < 4; ++s) pw[s] = T::pack2(sacc[kb][8 * g + 2 * s], sacc[kb][8 * g + 2 * s + 1]);
-          const vec8 pb = as_vec8<vec8>(pw);
-#pragma unroll
-          for (int db = 0; db < NDB; ++db)
-            oacc[db] = T::mfma32(as_vec8<vec8>(lds_operand_tr(vs, vtr, VS, 32 * kb + 16 * g, 32 * db)), pb, oacc[db]);
-        }
-      }
-    }
-
-    if (t + 1 < npair) {
-      if (C::NBUF == 1) __syncthreads();   // every wave is done with the single buffer
-      stage(C::NBUF == 2 ? buf ^ 1 : 0);
+    issue(0);
+    if (npair > 1) {
+      issue(1);
+      __builtin_amdgcn_s_waitcnt(0xf70 | (C::LPT & 15) | ((C::LPT >> 4) << 14));   // stage 0 landed
+    } else {
+      __builtin_amdgcn_s_waitcnt(0xf70);
     }
     __syncthreads();
+    qk(0, sacc);
+    mask(0, sacc);
+    for (int t = 0; t < npair; ++t) {
+      rowmax(sacc);
+      u32x4 pw[2 * KB];
+      const bool more = t + 1 < npair;
+      if (more) {
+        __builtin_amdgcn_s_waitcnt(0xf70);   // this thread's loads of pair t + 1 landed
+        __syncthreads();                     // ... everyone's; and pair t - 1's slot is free
+        if (t + 2 < npair) issue(t + 2);
+        f32x16 snext[KB];
+        qk(t + 1, snext);
+        probs(sacc, pw);
+        pv(t, pw);
+        mask(t + 1, snext);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) sacc[kb] = snext[kb];
+      } else {
+        probs(sacc, pw);
+        pv(t, pw);
+      }
+    }
   }
 
-  // ---- merge group 1 into group 0, epilogue ------------------------------------
+  // ---- merge group 1 into group 0, epilogue ------------------------------------------
+  __syncthreads();   // every wave is done with the stage slots
   float* mg = reinterpret_cast<float*>(smem);
-  constexpr int MS = 2 + 16 * NDB;   // floats per lane in the hand-off
+  const float m_eff = m_set ? m_ref : -INFINITY;
   if (grp == 1) {
-    float* dst = mg + (wq * 64 + lane) * MS;
-    dst[0] = m_run;
+    float* dst = mg + (wq * 64 + lane) * C::MS;
+    dst[0] = m_eff;
     dst[1] = l_run;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
@@ -356,14 +334,15 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   }
   __syncthreads();
   if (grp == 1) return;
+  float m_fin;
   {
-    const float* src = mg + (wq * 64 + lane) * MS;
+    const float* src = mg + (wq * 64 + lane) * C::MS;
     const float m1 = src[0], l1 = src[1];
-    const float m_new = fmaxf(m_run, m1);
+    const float m_new = fmaxf(m_eff, m1);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float a0 = __builtin_amdgcn_exp2f(m_run - m_use), a1 = __builtin_amdgcn_exp2f(m1 - m_use);
+    const float a0 = __builtin_amdgcn_exp2f(m_eff - m_use), a1 = __builtin_amdgcn_exp2f(m1 - m_use);
     l_run = l_run * a0 + l1 * a1;
-    m_run = m_new;
+    m_fin = m_new;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -371,7 +350,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   }
   const float l = l_run + wave_shfl_xor(l_run, 32);
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  if (qvalid) {
+  if (qi < Nq) {
     uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1] + (int64_t)qi * p.o_s[2];
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
@@ -387,22 +366,12 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
       }
     if (hf == 0)
       p.lse[((int64_t)b * p.Hq + h) * Nq + qi] =
-          m_run == -INFINITY ? -INFINITY : (m_run + __builtin_amdgcn_logf(l)) * kLn2;
+          m_fin == -INFINITY ? -INFINITY : (m_fin + __builtin_amdgcn_logf(l)) * kLn2;
   }
 }
 
 template <typename T, int EP, int DV>
 hipError_t launch_t(const FlashFwdParams& p, hipStream_t s) {
-  KhatParams kp;
-  kp.k = p.k;
-  kp.k_s[0] = p.k_s[0]; kp.k_s[1] = p.k_s[1]; kp.k_s[2] = p.k_s[2];
-  kp.table = p.table;
-  kp.t_sb = p.t_sb;
-  kp.t_sh = p.t_sh;
-  kp.kh = p.kh;
-  kp.B = p.B; kp.Hk = p.Hk; kp.Nk = p.Nk; kp.NkP = p.NkP; kp.D = p.D; kp.R = p.R; kp.EP = EP;
-  hipError_t e = launch_prep_khat(kp, T::kCode, s);
-  if (e != hipSuccess) return e;
   const int blocks = p.nqb * p.B * p.Hq;
   return launch_named("flash_fwd", flash_fwd_kernel<T, EP, DV>, dim3(blocks), dim3(kThreads), s, p);
 }
@@ -424,13 +393,6 @@ hipError_t dispatch(const FlashFwdParams& p, hipStream_t s) {
 
 hipError_t launch_flash_fwd(const FlashFwdParams& p, int dtype, hipStream_t s) {
   return dtype == 2 ? dispatch<BF16>(p, s) : dispatch<F16>(p, s);
-}
-
-hipError_t launch_prep_khat(const KhatParams& p, int dtype, hipStream_t s) {
-  const int64_t n = (int64_t)p.B * p.Hk * p.NkP * (p.EP / 8);
-  const dim3 grid((unsigned)((n + 255) / 256));
-  return dtype == 2 ? launch_named("prep_khat", prep_khat_kernel<BF16>, grid, dim3(256), s, p)
-                    : launch_named("prep_khat", prep_khat_kernel<F16>, grid, dim3(256), s, p);
 }
 
 }  // namespace pope

@@ -102,37 +102,74 @@ int check_ws(size_t need, void* ws, size_t have) {
   return POPE_OK;
 }
 
-// Flash backward workspace pieces, in order after the phase table (each 256-byte aligned):
-//   Q_hat (B, Hq, NqP, EP), K_hat (B, Hk, NkP, EP)   -- 16-bit elements
-//   (lse * log2 e, delta) (B, Hq, NqP)               -- fp32 pairs
-// with EP = round_up(D + R, 32), DV = round_up(D, 32), NqP / NkP = round_up(N, 128).
-struct BwdLayout {
-  int EP, DV, NqP, NkP;
-  size_t qh, kh, delta, total;
+// Flash forward / backward workspace (the same layout for both, so the backward can reuse the
+// forward's preparation), each piece 256-byte aligned:
+//   cos/sin(F) (Bt, Ht, Nk, R) float2 | cos/sin(bias) (Hb, R) float2
+//   | K_hat (B, Hk, NkP, EP) | Q_hat (B, Hq, NqP, EP)      16-bit elements
+//   | key visibility words (B, NW) u64 | last visible key + 1 (B) int32
+//   | (lse * log2 e, delta) (B, Hq, NqP) float2            backward only
+// with EP = round_up(D + R, 32), DV = round_up(D, 32), NqP / NkP = round_up(N, 128),
+// NW = NkP / 64.
+void copy3(int64_t* dst, const int64_t* src);
+
+struct FlashLayout {
+  int EP, DV, NqP, NkP, NW, Bt, Ht, Hb;
+  size_t table, btab, kh, qh, mwords, kend, ld, total;
 };
 
-BwdLayout bwd_layout(const pope_desc& d) {
-  BwdLayout L;
+FlashLayout flash_layout(const pope_desc& d) {
+  FlashLayout L;
   L.EP = round_up(d.D + d.R, 32);
   L.DV = round_up(d.D, 32);
   L.NqP = round_up(d.Nq, 128);
   L.NkP = round_up(d.Nk, 128);
-  size_t off = geometry(d, d.Hq).table;
-  L.qh = off;    off += align_up((size_t)d.B * d.Hq * L.NqP * L.EP * 2);
-  L.kh = off;    off += align_up((size_t)d.B * d.Hk * L.NkP * L.EP * 2);
-  L.delta = off; off += align_up((size_t)d.B * d.Hq * L.NqP * 2 * sizeof(float));
+  L.NW = L.NkP / 64;
+  L.Bt = d.f_s[0] != 0 ? d.B : 1;
+  L.Ht = d.f_s[1] != 0 ? d.Hq : 1;
+  L.Hb = d.bias_sh != 0 ? d.Hk : 1;
+  size_t off = 0;
+  L.table = off;  off += d.R > 0 ? align_up((size_t)L.Bt * L.Ht * d.Nk * d.R * sizeof(float2)) : 0;
+  L.btab = off;   off += d.R > 0 ? align_up((size_t)L.Hb * d.R * sizeof(float2)) : 0;
+  L.kh = off;     off += align_up((size_t)d.B * d.Hk * L.NkP * L.EP * 2);
+  L.qh = off;     off += align_up((size_t)d.B * d.Hq * L.NqP * L.EP * 2);
+  L.mwords = off; off += align_up((size_t)d.B * L.NW * sizeof(uint64_t));
+  L.kend = off;   off += align_up((size_t)d.B * sizeof(int32_t));
+  L.ld = off;     off += align_up((size_t)d.B * d.Hq * L.NqP * sizeof(float2));
   L.total = off;
   return L;
 }
 
-// Flash forward workspace: [phase table | K_hat (B, Hk, NkP, EP) 16-bit].
-size_t fwd_kh_bytes(const pope_desc& d) {
-  return align_up((size_t)d.B * d.Hk * round_up(d.Nk, 128) * round_up(d.D + d.R, 32) * 2);
-}
+size_t flash_ws(const pope_desc& d, int) { return flash_layout(d).total; }
 
-size_t flash_ws(const pope_desc& d, int op) {
-  if (op == POPE_OP_FLASH_BWD) return bwd_layout(d).total;
-  return geometry(d, d.Hq).table + fwd_kh_bytes(d);
+// Launches the shared preparation of the flash forward and backward into the workspace.
+hipError_t flash_prepare(const pope_desc& d, const FlashLayout& L, const void* q, const void* k,
+                         const float* freqs, const float* bias, const uint8_t* mask, char* ws, hipStream_t s) {
+  pope::FlashPrep p;
+  std::memset(&p, 0, sizeof p);
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.freqs = d.R > 0 ? freqs : nullptr;
+  p.bias = d.R > 0 ? bias : nullptr;
+  p.mask = mask;
+  p.table = reinterpret_cast<float2*>(ws + L.table);
+  p.btab = reinterpret_cast<float2*>(ws + L.btab);
+  p.qh = reinterpret_cast<uint16_t*>(ws + L.qh);
+  p.kh = reinterpret_cast<uint16_t*>(ws + L.kh);
+  p.mwords = reinterpret_cast<uint64_t*>(ws + L.mwords);
+  p.kend = reinterpret_cast<int*>(ws + L.kend);
+  p.B = d.B; p.Hq = d.Hq; p.Hk = d.Hk; p.Nq = d.Nq; p.Nk = d.Nk; p.D = d.D; p.R = d.R;
+  p.EP = L.EP; p.NqP = L.NqP; p.NkP = L.NkP; p.NW = L.NW;
+  p.Bt = L.Bt; p.Ht = L.Ht; p.Hb = L.Hb;
+  p.has_mask = mask != nullptr;
+  p.qscale = d.softmax_scale * 1.4426950408889634f;
+  copy3(p.q_s, d.q_s);
+  copy3(p.k_s, d.k_s);
+  copy3(p.f_s, d.f_s);
+  p.bias_sh = d.bias_sh;
+  p.mask_sb = d.mask_sb;
+  p.t_sb = L.Bt > 1 ? (int64_t)L.Ht * d.Nk * d.R : 0;
+  p.t_sh = L.Ht > 1 ? (int64_t)d.Nk * d.R : 0;
+  return pope::launch_flash_prep(p, d.dtype, s);
 }
 
 // Similarity workspace: [key table with bias (Bt, Hk) | query table without bias (Bt, Hqt)
@@ -317,41 +354,31 @@ int pope_flash_fwd(const pope_desc* d, const void* q, const void* k, const void*
                    size_t workspace_bytes, void* stream) {
   int rc = check_flash_common(d, q, k, v, freqs, bias, mask, o, lse);
   if (rc) return rc;
-  if ((rc = check_ws(flash_ws(*d, POPE_OP_FLASH_FWD), workspace, workspace_bytes))) return rc;
+  const FlashLayout L = flash_layout(*d);
+  if ((rc = check_ws(L.total, workspace, workspace_bytes))) return rc;
+  if ((int64_t)d->Nk * d->v_s[2] >= ((int64_t)1 << 31))
+    return fail(POPE_ERR_UNSUPPORTED, "v rows span %lld elements per (batch, head); the kernels index them "
+                "with 32-bit offsets", (long long)((int64_t)d->Nk * d->v_s[2]));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const Geo g = geometry(*d, d->Hq);
-  float2* table = reinterpret_cast<float2*>(workspace);
-  if (d->R > 0) {
-    hipError_t e = build_table(*d, freqs, nullptr, g.Bt, g.Ht, table, s);
-    if (e != hipSuccess) return hip_fail(e, "phase table launch");
-  }
+  char* ws = static_cast<char*>(workspace);
+  hipError_t e = flash_prepare(*d, L, q, k, freqs, bias, mask, ws, s);
+  if (e != hipSuccess) return hip_fail(e, "flash preparation launch");
   pope::FlashFwdParams p;
   std::memset(&p, 0, sizeof p);
-  p.q = static_cast<const uint16_t*>(q);
-  p.k = static_cast<const uint16_t*>(k);
+  p.qh = reinterpret_cast<const uint16_t*>(ws + L.qh);
+  p.kh = reinterpret_cast<const uint16_t*>(ws + L.kh);
   p.v = static_cast<const uint16_t*>(v);
-  p.freqs = d->R > 0 ? freqs : nullptr;
-  p.bias = d->R > 0 ? bias : nullptr;
-  p.mask = mask;
-  p.table = d->R > 0 ? table : nullptr;
-  p.kh = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + g.table);
+  p.mwords = reinterpret_cast<const uint64_t*>(ws + L.mwords);
+  p.kend = reinterpret_cast<const int*>(ws + L.kend);
   p.o = static_cast<uint16_t*>(o);
   p.lse = lse;
-  p.B = d->B; p.Hq = d->Hq; p.Hk = d->Hk; p.Nq = d->Nq; p.Nk = d->Nk; p.D = d->D; p.R = d->R;
-  p.EP = round_up(d->D + d->R, 32);
-  p.DV = round_up(d->D, 32);
-  p.NkP = round_up(d->Nk, 128);
+  p.B = d->B; p.Hq = d->Hq; p.Hk = d->Hk; p.Nq = d->Nq; p.Nk = d->Nk; p.D = d->D;
+  p.EP = L.EP; p.DV = L.DV; p.NqP = L.NqP; p.NkP = L.NkP; p.NW = L.NW;
   p.causal = d->causal != 0;
-  p.has_mask = mask != nullptr;
-  p.nqb = (d->Nq + 127) / 128;
-  p.scale_log2 = d->softmax_scale * 1.4426950408889634f;
-  copy3(p.q_s, d->q_s); copy3(p.k_s, d->k_s); copy3(p.v_s, d->v_s);
-  copy3(p.o_s, d->o_s); copy3(p.f_s, d->f_s);
-  p.bias_sh = d->bias_sh;
-  p.mask_sb = d->mask_sb;
-  p.t_sb = g.Bt > 1 ? (int64_t)g.Ht * d->Nk * d->R : 0;
-  p.t_sh = g.Ht > 1 ? (int64_t)d->Nk * d->R : 0;
-  hipError_t e = pope::launch_flash_fwd(p, d->dtype, s);
+  p.nqb = L.NqP / 128;
+  copy3(p.v_s, d->v_s);
+  copy3(p.o_s, d->o_s);
+  e = pope::launch_flash_fwd(p, d->dtype, s);
   if (e == hipErrorInvalidValue)
     return fail(POPE_ERR_UNSUPPORTED, "no flash forward kernel for head dim %d, rotate dim %d", d->D, d->R);
   if (e != hipSuccess) return hip_fail(e, "flash forward launch");
@@ -371,15 +398,15 @@ int pope_flash_bwd(const pope_desc* d, const void* dout, const void* q, const vo
       (rc = check_strides16("dk", d->dk_s)) || (rc = check_strides16("dv", d->dv_s)))
     return rc;
   if (d->R == 0 && (dfreqs || dbias)) return fail(POPE_ERR_INVALID, "dfreqs/dbias requested with rotate dim 0");
-  if ((rc = check_ws(flash_ws(*d, POPE_OP_FLASH_BWD), workspace, workspace_bytes))) return rc;
+  if (d->flags & ~(POPE_FLAG_PREPARED | POPE_FLAG_ZERO_GRADS))
+    return fail(POPE_ERR_INVALID, "unknown flags 0x%x", (unsigned)d->flags);
+  const FlashLayout L = flash_layout(*d);
+  if ((rc = check_ws(L.total, workspace, workspace_bytes))) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const Geo g = geometry(*d, d->Hq);
-  const BwdLayout L = bwd_layout(*d);
   char* ws = static_cast<char*>(workspace);
-  float2* table = reinterpret_cast<float2*>(ws);
-  if (d->R > 0) {
-    hipError_t e = build_table(*d, freqs, nullptr, g.Bt, g.Ht, table, s);
-    if (e != hipSuccess) return hip_fail(e, "phase table launch");
+  if (!(d->flags & POPE_FLAG_PREPARED)) {
+    hipError_t e = flash_prepare(*d, L, q, k, freqs, bias, mask, ws, s);
+    if (e != hipSuccess) return hip_fail(e, "flash preparation launch");
   }
   pope::FlashBwdParams p;
   std::memset(&p, 0, sizeof p);
@@ -389,36 +416,36 @@ int pope_flash_bwd(const pope_desc* d, const void* dout, const void* q, const vo
   p.o = static_cast<const uint16_t*>(o);
   p.dout = static_cast<const uint16_t*>(dout);
   p.lse = lse;
-  p.freqs = d->R > 0 ? freqs : nullptr;
-  p.bias = d->R > 0 ? bias : nullptr;
   p.mask = mask;
-  p.table = d->R > 0 ? table : nullptr;
+  p.table = d->R > 0 ? reinterpret_cast<const float2*>(ws + L.table) : nullptr;
+  p.btab = d->R > 0 ? reinterpret_cast<const float2*>(ws + L.btab) : nullptr;
   p.dq = static_cast<uint16_t*>(dq);
   p.dk = static_cast<uint16_t*>(dk);
   p.dv = static_cast<uint16_t*>(dv);
   p.dfreqs = dfreqs;
   p.dbias = dbias;
-  p.qh = reinterpret_cast<uint16_t*>(ws + L.qh);
-  p.kh = reinterpret_cast<uint16_t*>(ws + L.kh);
-  p.ld = reinterpret_cast<float2*>(ws + L.delta);
+  p.qh = reinterpret_cast<const uint16_t*>(ws + L.qh);
+  p.kh = reinterpret_cast<const uint16_t*>(ws + L.kh);
+  p.ld = reinterpret_cast<float2*>(ws + L.ld);
   p.B = d->B; p.Hq = d->Hq; p.Hk = d->Hk; p.Nq = d->Nq; p.Nk = d->Nk; p.D = d->D; p.R = d->R;
   p.E = d->D + d->R;
   p.EP = L.EP;
   p.DV = L.DV;
   p.NqP = L.NqP;
   p.NkP = L.NkP;
+  p.Bt = L.Bt; p.Ht = L.Ht; p.Hb = L.Hb;
   p.causal = d->causal != 0;
   p.has_mask = mask != nullptr;
+  p.zero_grads = (d->flags & POPE_FLAG_ZERO_GRADS) != 0;
   p.scale = d->softmax_scale;
-  p.scale_log2 = d->softmax_scale * 1.4426950408889634f;
   copy3(p.q_s, d->q_s); copy3(p.k_s, d->k_s); copy3(p.v_s, d->v_s);
   copy3(p.o_s, d->o_s); copy3(p.do_s, d->do_s); copy3(p.dq_s, d->dq_s);
-  copy3(p.dk_s, d->dk_s); copy3(p.dv_s, d->dv_s); copy3(p.f_s, d->f_s);
+  copy3(p.dk_s, d->dk_s); copy3(p.dv_s, d->dv_s);
   copy3(p.df_s, d->df_s);
   p.bias_sh = d->bias_sh;
   p.mask_sb = d->mask_sb;
-  p.t_sb = g.Bt > 1 ? (int64_t)g.Ht * d->Nk * d->R : 0;
-  p.t_sh = g.Ht > 1 ? (int64_t)d->Nk * d->R : 0;
+  p.t_sb = L.Bt > 1 ? (int64_t)L.Ht * d->Nk * d->R : 0;
+  p.t_sh = L.Ht > 1 ? (int64_t)d->Nk * d->R : 0;
   hipError_t e = pope::launch_flash_bwd(p, d->dtype, s);
   if (e == hipErrorInvalidValue)
     return fail(POPE_ERR_UNSUPPORTED, "no flash backward kernel for head dim %d, rotate dim %d", d->D, d->R);

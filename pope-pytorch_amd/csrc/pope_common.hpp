@@ -47,6 +47,10 @@ struct BF16 {
   static __device__ __forceinline__ f32x4 mfma16(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
+  // c + a.x * b.x + a.y * b.y on packed pairs (v_dot2_f32_bf16)
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+  }
 };
 
 struct F16 {
@@ -66,6 +70,10 @@ struct F16 {
   }
   static __device__ __forceinline__ f32x4 mfma16(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  // c + a.x * b.x + a.y * b.y on packed pairs (v_dot2_f32_f16)
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
   }
 };
 
@@ -114,6 +122,14 @@ __device__ __forceinline__ int xcd_remap(int hw_id, int total) {
 
 __device__ __forceinline__ float wave_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// max(v[lane], v[lane ^ 32]) with one v_permlane32_swap: swapping the upper half of a copy of v
+// with the lower half of another leaves lane l holding v[l] and v[l ^ 32] in the two outputs.
+__device__ __forceinline__ float half_swap_max(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
+}
+
 // Marks a rarely taken branch body so the compiler keeps it a branch instead of
 // speculating it into per-lane selects on every path.
 #define POPE_COLD_PATH() asm volatile("")
@@ -134,6 +150,21 @@ __host__ __device__ constexpr int lds_units_tr(int units) {
   return (units % 16 == 4 || units % 16 == 12) ? units : lds_units_tr(units + 4 - units % 4);
 }
 __device__ __forceinline__ int lds_swz(int row, int unit) { return unit ^ ((row >> 2) & 3); }
+
+// XOR swizzle of the 16-byte units of an unpadded LDS tile whose rows hold U units (U a
+// multiple of 4): unit u of row r is stored at r * U + (u ^ tile_swz(U, r)).  The value depends
+// on r % 16 only and keeps u within its row.  With it, both reads the MFMA operands make are
+// free of bank conflicts (64 banks of 4 bytes = 16 units):
+//   row read        16 lanes read unit u of 16 consecutive rows (ds_read_b128);
+//   transpose read  4 consecutive rows (aligned to 4) x 4 consecutive units (aligned to 4)
+//                   (ds_read_b64_tr_b16, lds_read_tr16).
+// Unpadded rows let tiles be filled by direct global-to-LDS loads, which write 64 consecutive
+// units per wave instruction.
+__host__ __device__ constexpr int tile_swz(int U, int r) {
+  return (U % 16 == 0) ? (((r & 3) << 2) | ((r >> 2) & 3))
+         : (U % 8 == 0) ? ((((r >> 1) & 1) << 2) | ((r >> 2) & 3))
+                        : ((r >> 2) & 3);
+}
 
 // LDS transpose read (ds_read_b64_tr_b16).  Within each group of 16 lanes, lane
 // j supplies the address of 4 consecutive 16-bit elements; output lane 4a + c

@@ -34,45 +34,61 @@ struct TableParams {
 };
 hipError_t launch_phase_table(const TableParams& p, hipStream_t s);
 
-struct FlashFwdParams {
-  const uint16_t* q; const uint16_t* k; const uint16_t* v;
+// Shared preparation of the flash forward and backward (flash_prep.hip), written into the
+// caller's workspace once per forward call and reused by the backward:
+//   flash_setup: cos/sin(F) rows n < Nk (fp32 pairs), cos/sin(bias) per (bias row, dim), key
+//                visibility words;
+//   flash_prep : K_hat and the pre-scaled Q_hat rows, 1 + last visible key per batch.
+// The expanded rows (16-bit, EP columns, zero past E and past Nq / Nk) are
+//   K_hat[b, hk, j] = [c cos F_j | c sin F_j | k_rest],                c = softplus(k_j)
+//   Q_hat[b, h, i]  = s [a cos(F_i' - bias) | a sin(F_i' - bias) | q_rest],  a = softplus(q_i),
+// F_i' = F[Nk - Nq + i] and s = softmax_scale * log2(e), so Q_hat K_hat^T is the score in log2
+// units.  The learned bias sits on the query side: cos(phi - (F_j + b)) = cos((phi - b) - F_j).
+struct FlashPrep {
+  const uint16_t* q; const uint16_t* k;
   const float* freqs; const float* bias; const uint8_t* mask;
-  const float2* table;       // cos/sin(F[b, h, n, d]) for n < Nk, no bias
-  uint16_t* kh;              // (B, Hk, NkP, EP) workspace: K_hat rows, written by fwd_prep_k
-  uint16_t* o; float* lse;
-  int B, Hq, Hk, Nq, Nk, D, R, EP, DV, NkP, causal, has_mask, nqb;
-  float scale_log2;          // softmax_scale * log2(e)
-  int64_t q_s[3], k_s[3], v_s[3], o_s[3], f_s[3];
+  float2* table;             // (Bt, Ht, Nk, R)
+  float2* btab;              // (Hb, R)
+  uint16_t* qh;              // (B, Hq, NqP, EP)
+  uint16_t* kh;              // (B, Hk, NkP, EP)
+  uint64_t* mwords;          // (B, NW): bit j of word w <=> key 64 w + j < Nk and unmasked
+  int* kend;                 // (B)
+  int B, Hq, Hk, Nq, Nk, D, R, EP, NqP, NkP, NW, Bt, Ht, Hb, has_mask;
+  float qscale;
+  int64_t q_s[3], k_s[3], f_s[3];
   int64_t bias_sh, mask_sb, t_sb, t_sh;
 };
-// dtype: 1 = f16, 2 = bf16.  Returns hipErrorInvalidValue for an uncovered (E, D) shape.
-hipError_t launch_flash_fwd(const FlashFwdParams& p, int dtype, hipStream_t s);
+// dtype: 1 = f16, 2 = bf16.
+hipError_t launch_flash_prep(const FlashPrep& p, int dtype, hipStream_t s);
 
-// K_hat = polar transform of the keys, (B, Hk, NkP, EP) 16-bit rows, zero past Nk and past E
-// (flash_fwd.hip; used by the forward and the backward).
-struct KhatParams {
-  const uint16_t* k; int64_t k_s[3];
-  const float2* table; int64_t t_sb, t_sh;   // cos/sin(F) rows, see TableParams
-  uint16_t* kh;
-  int B, Hk, Nk, NkP, D, R, EP;
+struct FlashFwdParams {
+  const uint16_t* qh; const uint16_t* kh; const uint16_t* v;   // Q_hat, K_hat of FlashPrep
+  const uint64_t* mwords; const int* kend;
+  uint16_t* o; float* lse;
+  int B, Hq, Hk, Nq, Nk, D, EP, DV, NqP, NkP, NW, causal, nqb;
+  int64_t v_s[3], o_s[3];
 };
-hipError_t launch_prep_khat(const KhatParams& p, int dtype, hipStream_t s);
+// Returns hipErrorInvalidValue for an uncovered (EP, DV) shape.
+hipError_t launch_flash_fwd(const FlashFwdParams& p, int dtype, hipStream_t s);
 
 struct FlashBwdParams {
   const uint16_t* q; const uint16_t* k; const uint16_t* v; const uint16_t* o; const uint16_t* dout;
-  const float* lse; const float* freqs; const float* bias; const uint8_t* mask;
-  const float2* table;       // cos/sin(F[b, h, n, d]) for n < Nk, no bias
+  const float* lse; const uint8_t* mask;
+  const float2* table;       // cos/sin(F[b, h, n, d]) for n < Nk (FlashPrep::table)
+  const float2* btab;        // cos/sin(bias) (FlashPrep::btab)
   uint16_t* dq; uint16_t* dk; uint16_t* dv;
   float* dfreqs; float* dbias;
-  // workspace, written by the prep kernels (rows past Nq / Nk and columns past E are zero)
-  uint16_t* qh;              // (B, Hq, NqP, EP)  expanded queries Q_hat
-  uint16_t* kh;              // (B, Hk, NkP, EP)  expanded keys K_hat
+  // workspace (FlashPrep): expanded rows, zero past Nq / Nk and past E
+  const uint16_t* qh;        // (B, Hq, NqP, EP)  Q_hat * softmax_scale * log2(e)
+  const uint16_t* kh;        // (B, Hk, NkP, EP)  K_hat
   float2* ld;                // (B, Hq, NqP)      (lse * log2(e), rowsum(O * dO)); rows past Nq and
                              //                   rows with every key masked carry lse = +inf
   int B, Hq, Hk, Nq, Nk, D, R, E, EP, DV, NqP, NkP, causal, has_mask;
+  int Bt, Ht, Hb;            // extents of the cos/sin table and of the bias rows
+  int zero_grads;            // clear dfreqs / dbias before accumulating
   int n_kv_jobs, interleave; // dK/dV jobs of the fused launch; 1 = pair dK/dV and dQ jobs by cost
-  float scale, scale_log2;
-  int64_t q_s[3], k_s[3], v_s[3], o_s[3], do_s[3], dq_s[3], dk_s[3], dv_s[3], f_s[3], df_s[3];
+  float scale;
+  int64_t q_s[3], k_s[3], v_s[3], o_s[3], do_s[3], dq_s[3], dk_s[3], dv_s[3], df_s[3];
   int64_t bias_sh, mask_sb, t_sb, t_sh;
 };
 hipError_t launch_flash_bwd(const FlashBwdParams& p, int dtype, hipStream_t s);

@@ -14,7 +14,8 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpope_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
+FLAG_PREPARED, FLAG_ZERO_GRADS = 1, 2
 
 POPE_F32, POPE_F16, POPE_BF16 = 0, 1, 2
 OP_SIM_FWD, OP_SIM_BWD, OP_FLASH_FWD, OP_FLASH_BWD, OP_FLASH_DECODE = range(5)
@@ -31,7 +32,7 @@ class PopeDesc(ctypes.Structure):
         ("B", ctypes.c_int32), ("Hq", ctypes.c_int32), ("Hk", ctypes.c_int32),
         ("Nq", ctypes.c_int32), ("Nk", ctypes.c_int32), ("D", ctypes.c_int32), ("R", ctypes.c_int32),
         ("dtype", ctypes.c_int32), ("causal", ctypes.c_int32), ("softmax_scale", ctypes.c_float),
-        ("q_s", _I64x3), ("k_s", _I64x3), ("v_s", _I64x3), ("o_s", _I64x3),
+        ("flags", ctypes.c_int32), ("q_s", _I64x3), ("k_s", _I64x3), ("v_s", _I64x3), ("o_s", _I64x3),
         ("do_s", _I64x3), ("dq_s", _I64x3), ("dk_s", _I64x3), ("dv_s", _I64x3),
         ("sim_s", _I64x3), ("f_s", _I64x3), ("df_s", _I64x3),
         ("bias_sh", ctypes.c_int64), ("mask_sb", ctypes.c_int64),

@@ -124,8 +124,10 @@ def _check_pope_shapes(q, k, freqs, bias):
 
 @torch.library.custom_op("pope_amd::flash_fwd", mutates_args=(), device_types="cuda")
 def flash_fwd_op(q: Tensor, k: Tensor, v: Tensor, freqs: Optional[Tensor], bias: Optional[Tensor],
-                 mask: Optional[Tensor], causal: bool, softmax_scale: float) -> tuple[Tensor, Tensor]:
-    """q (B,Hq,Nq,D), k/v (B,Hk,Nk,D) bf16/fp16 views -> o like q, lse (B,Hq,Nq) fp32."""
+                 mask: Optional[Tensor], causal: bool, softmax_scale: float) -> tuple[Tensor, Tensor, Tensor]:
+    """q (B,Hq,Nq,D), k/v (B,Hk,Nk,D) bf16/fp16 views -> o like q, lse (B,Hq,Nq) fp32 and the
+    workspace holding the forward's preparation (expanded K/Q rows, phase tables), which the
+    backward reuses; empty when the decode kernel ran."""
     L = _lib.lib()
     q, k, v = _unit_feature(q), _unit_feature(k), _unit_feature(v)
     d = _desc(q, k, freqs, bias, causal, softmax_scale)
@@ -135,36 +137,37 @@ def flash_fwd_op(q: Tensor, k: Tensor, v: Tensor, freqs: Optional[Tensor], bias:
     d.o_s[:] = _lib.strides3(o)
     if exists(mask):
         d.mask_sb = mask.stride(0)
-    ws = _lib.workspace(_lib.OP_FLASH_FWD, d, q.device)
-    wsz = 0 if ws is None else ws.numel()
+    args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(freqs), _lib.ptr(bias), _lib.ptr(mask),
+            _lib.ptr(o), _lib.ptr(lse))
+    stream = _lib.stream_ptr(q.device)
     # one non-causal query row against a long cache: the split-K decode kernel
-    use_decode = q.shape[2] == 1 and not causal and k.shape[2] >= 1024
-    fn = L.pope_flash_decode if use_decode else L.pope_flash_fwd
-    if use_decode:
-        ws = _lib.workspace(_lib.OP_FLASH_DECODE, d, q.device)
-        wsz = 0 if ws is None else ws.numel()
-    st = fn(ctypes.byref(d), _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(freqs), _lib.ptr(bias),
-            _lib.ptr(mask), _lib.ptr(o), _lib.ptr(lse), _lib.ptr(ws), wsz, _lib.stream_ptr(q.device))
-    if st != 0 and use_decode and st == 2:   # decode kernel does not cover this shape
-        ws = _lib.workspace(_lib.OP_FLASH_FWD, d, q.device)
-        wsz = 0 if ws is None else ws.numel()
-        st = L.pope_flash_fwd(ctypes.byref(d), _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(freqs),
-                              _lib.ptr(bias), _lib.ptr(mask), _lib.ptr(o), _lib.ptr(lse), _lib.ptr(ws), wsz,
-                              _lib.stream_ptr(q.device))
+    if q.shape[2] == 1 and not causal and k.shape[2] >= 1024:
+        dws = _lib.workspace(_lib.OP_FLASH_DECODE, d, q.device)
+        st = L.pope_flash_decode(ctypes.byref(d), *args, _lib.ptr(dws), 0 if dws is None else dws.numel(), stream)
+        if st == 0:
+            return o, lse, q.new_empty(0, dtype=torch.uint8)
+        if st != 2:   # 2: the decode kernel does not cover this shape -> general forward
+            _lib.check(st, "flash decode")
+    ws = _lib.workspace(_lib.OP_FLASH_FWD, d, q.device)
+    st = L.pope_flash_fwd(ctypes.byref(d), *args, _lib.ptr(ws), ws.numel(), stream)
     _lib.check(st, "flash forward")
-    return o, lse
+    return o, lse, ws
 
 
 @flash_fwd_op.register_fake
 def _(q, k, v, freqs, bias, mask, causal, softmax_scale):
-    return torch.empty_like(q), q.new_empty(q.shape[:3], dtype=torch.float32)
+    d = _desc(q, k, freqs, bias, causal, softmax_scale)
+    n = _lib.workspace_bytes(_lib.OP_FLASH_FWD, d)
+    return torch.empty_like(q), q.new_empty(q.shape[:3], dtype=torch.float32), q.new_empty(n, dtype=torch.uint8)
 
 
 @torch.library.custom_op("pope_amd::flash_bwd", mutates_args=(), device_types="cuda")
 def flash_bwd_op(do: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor,
                  freqs: Optional[Tensor], bias: Optional[Tensor], mask: Optional[Tensor], causal: bool,
-                 softmax_scale: float, need_dfreqs: bool, need_dbias: bool
+                 softmax_scale: float, need_dfreqs: bool, need_dbias: bool, fwd_ws: Optional[Tensor] = None
                  ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Gradients of flash_fwd.  ``fwd_ws`` is the workspace flash_fwd returned for the same
+    inputs (reused as is); without it the preparation is recomputed."""
     L = _lib.lib()
     q, k, v, o, do = (_unit_feature(t) for t in (q, k, v, o, do))
     if do.dtype != q.dtype:
@@ -174,25 +177,31 @@ def flash_bwd_op(do: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Te
     d.do_s[:] = _lib.strides3(do)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     d.dq_s[:], d.dk_s[:], d.dv_s[:] = _lib.strides3(dq), _lib.strides3(dk), _lib.strides3(dv)
-    dfreqs = torch.zeros(freqs.shape, device=q.device, dtype=torch.float32) if need_dfreqs else q.new_empty(0, dtype=torch.float32)
-    dbias = torch.zeros(bias.shape, device=q.device, dtype=torch.float32) if need_dbias else q.new_empty(0, dtype=torch.float32)
+    # the library clears dfreqs / dbias itself (POPE_FLAG_ZERO_GRADS) before accumulating
+    dfreqs = torch.empty(freqs.shape, device=q.device, dtype=torch.float32) if need_dfreqs else q.new_empty(0, dtype=torch.float32)
+    dbias = torch.empty(bias.shape, device=q.device, dtype=torch.float32) if need_dbias else q.new_empty(0, dtype=torch.float32)
     if need_dfreqs:
         d.df_s[:] = _freqs_strides(dfreqs)
     if exists(mask):
         d.mask_sb = mask.stride(0)
-    ws = _lib.workspace(_lib.OP_FLASH_BWD, d, q.device)
-    wsz = 0 if ws is None else ws.numel()
+    d.flags = _lib.FLAG_ZERO_GRADS
+    need = _lib.workspace_bytes(_lib.OP_FLASH_BWD, d)
+    if exists(fwd_ws) and fwd_ws.numel() == need:
+        ws = fwd_ws
+        d.flags |= _lib.FLAG_PREPARED
+    else:
+        ws = torch.empty(need, dtype=torch.uint8, device=q.device)
     st = L.pope_flash_bwd(ctypes.byref(d), _lib.ptr(do), _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o),
                           _lib.ptr(lse), _lib.ptr(freqs), _lib.ptr(bias), _lib.ptr(mask), _lib.ptr(dq),
                           _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dfreqs) if need_dfreqs else None,
-                          _lib.ptr(dbias) if need_dbias else None, _lib.ptr(ws), wsz,
+                          _lib.ptr(dbias) if need_dbias else None, _lib.ptr(ws), ws.numel(),
                           _lib.stream_ptr(q.device))
     _lib.check(st, "flash backward")
     return dq, dk, dv, dfreqs, dbias
 
 
 @flash_bwd_op.register_fake
-def _(do, q, k, v, o, lse, freqs, bias, mask, causal, softmax_scale, need_dfreqs, need_dbias):
+def _(do, q, k, v, o, lse, freqs, bias, mask, causal, softmax_scale, need_dfreqs, need_dbias, fwd_ws=None):
     df = freqs.new_empty(freqs.shape, dtype=torch.float32) if need_dfreqs else q.new_empty(0, dtype=torch.float32)
     db = bias.new_empty(bias.shape, dtype=torch.float32) if need_dbias else q.new_empty(0, dtype=torch.float32)
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), df, db
@@ -200,17 +209,17 @@ def _(do, q, k, v, o, lse, freqs, bias, mask, causal, softmax_scale, need_dfreqs
 
 def _fwd_setup(ctx, inputs, output):
     q, k, v, freqs, bias, mask, causal, scale = inputs
-    o, lse = output
-    ctx.save_for_backward(q, k, v, freqs, bias, mask, o, lse)
+    o, lse, ws = output
+    ctx.save_for_backward(q, k, v, freqs, bias, mask, o, lse, ws)
     ctx.causal, ctx.scale = causal, scale
 
 
-def _fwd_backward(ctx, do, dlse):
-    q, k, v, freqs, bias, mask, o, lse = ctx.saved_tensors
+def _fwd_backward(ctx, do, dlse, dws):
+    q, k, v, freqs, bias, mask, o, lse, ws = ctx.saved_tensors
     need_df = bool(ctx.needs_input_grad[3]) and exists(freqs)
     need_db = bool(ctx.needs_input_grad[4]) and exists(bias)
     dq, dk, dv, df, db = flash_bwd_op(do, q, k, v, o, lse, freqs, bias, mask, ctx.causal, ctx.scale,
-                                      need_df, need_db)
+                                      need_df, need_db, ws)
     return (dq, dk, dv, df if need_df else None, db if need_db else None, None, None, None)
 
 
@@ -236,7 +245,7 @@ def flash_attn_head_first(q: Tensor, k: Tensor, v: Tensor, freqs: Optional[Tenso
         k = k.to(q.dtype)
     if v.dtype != q.dtype:
         v = v.to(q.dtype)
-    o, _ = flash_fwd_op(q, k, v, freqs, pope_bias, mask, causal, float(scale))
+    o, _, _ = flash_fwd_op(q, k, v, freqs, pope_bias, mask, causal, float(scale))
     return o.to(out_dtype) if o.dtype != out_dtype else o
 
 
@@ -250,7 +259,7 @@ def flash_attn_forward(q, k, v, freqs=None, pope_bias=None, mask=None, causal=Fa
     qh, kh, vh = (t.transpose(1, 2) for t in (q, k, v))
     if exists(freqs) and freqs.ndim == 4:
         freqs = freqs.transpose(1, 2)   # (B, N, H, R) -> (B, H, N, R) view
-    o, lse = flash_fwd_op(qh, kh, vh, freqs, pope_bias, mask, causal, float(scale))
+    o, lse, _ = flash_fwd_op(qh, kh, vh, freqs, pope_bias, mask, causal, float(scale))
     return o.transpose(1, 2), lse
 
 

@@ -47,15 +47,17 @@ def _ws(op, d):
 
 
 def test_workspace_sizes():
+    al = lambda n: (n + 255) // 256 * 256
     d = _desc()
-    table = 256 * 32 * 8                                           # cos/sin table, (Nk, R) float2
-    st, n = _ws(_lib.OP_FLASH_FWD, d)
-    assert st == 0 and n == table + 2 * 8 * 256 * 96 * 2            # + K_hat (E = 96 columns)
-    st, nb = _ws(_lib.OP_FLASH_BWD, d)
-    # + Q_hat, K_hat (E = 96 columns), (lse, delta) pairs
-    assert st == 0 and nb == table + 2 * (2 * 8 * 256 * 96 * 2) + 2 * 8 * 256 * 8
-    d3 = _desc(R=0, Nk=200)                                         # no table; K_hat rows padded to 256
-    assert _ws(_lib.OP_FLASH_FWD, d3) == (0, 2 * 8 * 256 * 64 * 2)
+    # cos/sin(F) (Nk, R) float2 | cos/sin(bias) (Hk, R) float2 | K_hat, Q_hat (E = 96 columns)
+    # | visibility words (B, Nk/64) u64 | kend (B) int32 | (lse, delta) (B, Hq, Nq) float2
+    want = (al(256 * 32 * 8) + al(8 * 32 * 8) + 2 * al(2 * 8 * 256 * 96 * 2) + al(2 * 4 * 8) + al(2 * 4)
+            + al(2 * 8 * 256 * 8))
+    assert _ws(_lib.OP_FLASH_FWD, d) == (0, want)
+    assert _ws(_lib.OP_FLASH_BWD, d) == (0, want)   # one layout: the backward reuses the forward's
+    d3 = _desc(R=0, Nk=200)                          # no tables; K_hat rows padded to 256, E = 64
+    want3 = 2 * al(2 * 8 * 256 * 64 * 2) + al(2 * 4 * 8) + al(2 * 4) + al(2 * 8 * 256 * 8)
+    assert _ws(_lib.OP_FLASH_FWD, d3) == (0, want3)
     ds = _desc(dtype=_lib.POPE_F32, R=64)
     st, n = _ws(_lib.OP_SIM_FWD, ds)
     assert st == 0 and n == 8 * 256 * 64 * 8 + 256 * 64 * 8         # key table per kv head + query table
@@ -110,6 +112,14 @@ def test_flash_rejects_bad_dtype_strides_pointers_workspace():
     assert _flash_fwd(d, k=ctypes.c_void_p(_A.value + 2)) == 1 and "aligned" in _lib.last_error()
     assert _flash_fwd(d, ws=None) == 3 and "workspace" in _lib.last_error()
     assert _flash_fwd(d, wsz=16) == 3 and "workspace" in _lib.last_error()
+
+
+def test_flash_bwd_rejects_unknown_flags():
+    d = _desc()
+    d.flags = 4
+    st = _lib.lib().pope_flash_bwd(ctypes.byref(d), _A, _A, _A, _A, _A, _A, _A, _A, None, _A, _A, _A, None, None,
+                                   _A, 1 << 16, None)
+    assert st == 1 and "flags" in _lib.last_error()
 
 
 def test_sim_and_decode_validation():
