@@ -52,13 +52,24 @@ constexpr int kStages = 3;
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Direct global -> LDS load of 16 bytes per lane: lane l's bytes land at dst + 16 l (dst is
-// wave-uniform).
-__device__ __forceinline__ void load_lds16(const void* src, void* dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void*)dst, 16, 0, 0);
+// Direct global -> LDS load of 16 bytes per lane: lane l's bytes land at LDS byte address
+// lds + 16 l (lds is wave-uniform, passed in M0).  Written as inline assembly so that the
+// compiler does not add its conservative wait for every outstanding LDS load before each LDS
+// read: the kernel waits for its own loads (vmcnt) before the barrier that publishes a stage.
+__device__ __forceinline__ void load_lds16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory");
 }
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// Waits until at most n of this thread's vector memory loads are outstanding.
+#define POPE_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+
+// Instruction-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedDsRead = 0x100;
 
 template <int EP, int DV>
 struct FwdCfg {
@@ -107,11 +118,15 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   }
 
   // ---- key range: causal bound of the block's last query, last visible key of the batch ----
-  int nkeys = min(p.kend[b], Nk);
+  // (the preparation's words and bounds are read-only here: the constant address space lets
+  // the uniform reads go through scalar loads)
+  typedef const __attribute__((address_space(4))) uint64_t cu64;
+  typedef const __attribute__((address_space(4))) int ci32;
+  int nkeys = min(((ci32*)p.kend)[b], Nk);
   if (p.causal) nkeys = min(nkeys, min(qb * kBM + kBM, Nq));
   const int nt = (nkeys + BN - 1) / BN;
   const int npair = (nt + 1) / 2;
-  const uint64_t* mw = p.mwords + (int64_t)b * p.NW;
+  cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
 
   // ---- direct-load plan: unit c = m * 512 + tid of a stage slot ---------------------
   // K_hat units first (tile g, row r, swizzled unit), then V units.  Offsets are relative
@@ -139,16 +154,19 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   auto issue = [&](int pr) {
     char* slot = smem + (pr % kStages) * C::STAGE;
     const int j0 = pr * 2 * BN;
+    const uint16_t* kp = khg + j0 * EP;   // K_hat rows are padded to NkP: no clamp
 #pragma unroll
     for (int m = 0; m < C::LPT; ++m) {
       const int c0 = m * kThreads + wave * 64;   // first unit of this wave's instruction
-      if (C::UNITS % kThreads != 0 && c0 >= C::UNITS) continue;
-      const void* src;
-      if (c0 < C::KUNITS)
-        src = khg + (j0 + ld_row[m]) * EP + ld_col[m];   // K_hat rows are padded to NkP
-      else
-        src = vg + (int64_t)min(j0 + ld_row[m], Nk - 1) * vs2 + ld_col[m];
-      load_lds16(src, slot + c0 * 16);
+      const uint32_t dst = lds_addr(slot + c0 * 16);
+      const uint16_t* vsrc = vg + min(j0 + ld_row[m], Nk - 1) * vs2 + ld_col[m];
+      if ((m + 1) * kThreads <= C::KUNITS) {          // K_hat units for every wave
+        load_lds16(kp + ld_row[m] * EP + ld_col[m], dst);
+      } else if (m * kThreads >= C::KUNITS) {         // V units
+        if (C::UNITS % kThreads == 0 || c0 < C::UNITS) load_lds16(vsrc, dst);
+      } else {                                        // the K / V boundary falls in this load
+        load_lds16(c0 < C::KUNITS ? (const void*)(kp + ld_row[m] * EP + ld_col[m]) : (const void*)vsrc, dst);
+      }
     }
   };
 
@@ -183,14 +201,43 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   float m_ref = 0.f, l_run = 0.f;
   bool m_set = false;
   f32x16 sacc[KB];
-
   auto kh_tile = [&](int pr) -> const uint16_t* {
     return reinterpret_cast<const uint16_t*>(smem + (pr % kStages) * C::STAGE) + grp * C::KTILE;
   };
   auto v_tile = [&](int pr) -> const uint16_t* {
     return reinterpret_cast<const uint16_t*>(smem + (pr % kStages) * C::STAGE) + 2 * C::KTILE + grp * C::VTILE;
   };
-  // S^T - m for the group's tile of pair pr
+  // Visibility of the group's tile of pair pr: true when every key is visible to every row of
+  // the wave (no per-element mask needed).
+  auto tile_full = [&](int pr, uint64_t& mb) -> bool {
+    const int tile = 2 * pr + grp;
+    const int j0 = tile * BN;
+    mb = 0;
+    if (tile < nt) {
+      mb = mw[j0 >> 6];
+      if (BN == 32) mb = (mb >> (j0 & 32)) & 0xffffffffull;
+    }
+    const uint64_t all = BN == 64 ? ~0ull : 0xffffffffull;
+    return mb == all && !(p.causal && j0 + BN - 1 > qw0);
+  };
+  // masked scores -> -inf (cold: diagonal and partially visible tiles)
+  auto apply_mask = [&](int pr, uint64_t mb, f32x16* s) {
+    const int j0 = (2 * pr + grp) * BN;
+    // the lane's keys are 32 kb + 8 (r >> 2) + (r & 3) past 4 hf: compile-time bit positions
+    const uint64_t w = mb >> (4 * hf);
+    const int lim = p.causal ? qi - j0 - 4 * hf : BN;   // causal: key offset <= lim
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr = 32 * kb + 8 * (r >> 2) + (r & 3);
+        const bool ok = ((uint32_t)(w >> kr) & 1u) && kr <= lim;
+        // in place (tied operand), so the scores keep their registers across the branch
+        asm("v_cmp_ne_u32 vcc, 0, %2\n\tv_cndmask_b32 %0, %1, %0, vcc"
+            : "+v"(s[kb][r]) : "v"(-INFINITY), "v"((int)ok) : "vcc");
+      }
+  };
+  // S^T - m for the group's tile of pair pr (the accumulators start from the -m block)
   auto qk = [&](int pr, f32x16* s) {
     const uint16_t* kt = kh_tile(pr);
 #pragma unroll
@@ -201,58 +248,36 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
         s[kb] = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt + 32 * kb * EP + koff[kk])), qreg[kk], s[kb]);
     }
   };
-  // masks of the group's tile of pair pr (cold: diagonal and partially visible tiles)
-  auto mask = [&](int pr, f32x16* s) {
-    const int tile = 2 * pr + grp;
-    const int j0 = tile * BN;
-    uint64_t mb = 0;
-    if (tile < nt) {
-      mb = mw[j0 >> 6];
-      if (BN == 32) mb = (mb >> (j0 & 32)) & 0xffffffffull;
-    }
-    const uint64_t all = BN == 64 ? ~0ull : 0xffffffffull;
-    const bool full = mb == all && !(p.causal && j0 + BN - 1 > qw0);
-    if (!full) {
-      POPE_COLD_PATH();
-      // the lane's keys are 32 kb + 8 (r >> 2) + (r & 3) past 4 hf: compile-time bit positions
-      const uint64_t w = mb >> (4 * hf);
-      const int lim = p.causal ? qi - j0 - 4 * hf : BN;   // causal: key offset <= lim
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kr = 32 * kb + 8 * (r >> 2) + (r & 3);
-          const bool ok = ((uint32_t)(w >> kr) & 1u) && kr <= lim;
-          s[kb][r] = ok ? s[kb][r] : -INFINITY;
-        }
-    }
-  };
-  // row maximum and the lazy reference update (rare, wave-uniform branch)
-  auto rowmax = [&](f32x16* s) {
+  auto rowmax = [&](const f32x16* s) -> float {
     float mt = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
-    mt = half_swap_max(mt);
-    const bool need = mt > -INFINITY && (!m_set || mt > 8.f);
+    return half_swap_max(mt);
+  };
+  // lazy reference update (rare, wave-uniform branch): moves m when a row's tile maximum mt
+  // (relative to m) exceeds 8, or on the row's first visible key
+  auto rescale = [&](float mt, f32x16* s) {
+    const bool need = (mt > -INFINITY) & (!m_set | (mt > 8.f));
     if (__any(need)) {
       POPE_COLD_PATH();
       const float sh = need ? mt : 0.f;
       const float alpha = (need && m_set) ? __builtin_amdgcn_exp2f(-mt) : 1.f;
-      l_run *= alpha;
+      // in-place updates (tied operands): the values keep their registers across the branch
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+        for (int r = 0; r < 16; ++r) asm("v_mul_f32 %0, %0, %1" : "+v"(oacc[db][r]) : "v"(alpha));
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[kb][r] -= sh;
+        for (int r = 0; r < 16; ++r) asm("v_sub_f32 %0, %0, %1" : "+v"(s[kb][r]) : "v"(sh));
+      asm("v_mul_f32 %0, %0, %1" : "+v"(l_run) : "v"(alpha));
       m_ref += sh;
       m_set = m_set || need;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) negm[r] = -m_ref;
+      for (int r = 0; r < 16; ++r) asm("v_mov_b32 %0, %1" : "=v"(negm[r]) : "v"(-m_ref));
     }
   };
   // probabilities (bf16 / fp16 pairs, in B-operand order) and the row sum
@@ -286,36 +311,81 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   };
 
   // ---- main loop ---------------------------------------------------------------------
+  // Iteration t: reference update for tile t; masks of tile t + 1 folded into its initial
+  // accumulators; then the score MFMAs of tile t + 1 interleaved with the exponentials of
+  // tile t, and the P V MFMAs of tile t interleaved with the row maximum of tile t + 1.
   if (npair > 0) {
     issue(0);
     if (npair > 1) {
       issue(1);
-      __builtin_amdgcn_s_waitcnt(0xf70 | (C::LPT & 15) | ((C::LPT >> 4) << 14));   // stage 0 landed
+      if (C::LPT == 3) POPE_WAIT_VMCNT(3);
+      else if (C::LPT == 4) POPE_WAIT_VMCNT(4);
+      else if (C::LPT == 5) POPE_WAIT_VMCNT(5);
+      else if (C::LPT == 6) POPE_WAIT_VMCNT(6);
+      else POPE_WAIT_VMCNT(0);
     } else {
-      __builtin_amdgcn_s_waitcnt(0xf70);
+      POPE_WAIT_VMCNT(0);
     }
     __syncthreads();
+    uint64_t mb0;
+    const bool full0 = tile_full(0, mb0);
     qk(0, sacc);
-    mask(0, sacc);
-    for (int t = 0; t < npair; ++t) {
-      rowmax(sacc);
+    if (!full0) {
+      POPE_COLD_PATH();
+      apply_mask(0, mb0, sacc);
+    }
+    float mt = rowmax(sacc);
+    // one pipelined step: tile t in `cur` (scores - m), tile t + 1 computed into `nxt`
+    auto step = [&](int t, f32x16* cur, f32x16* nxt) {
+      rescale(mt, cur);
       u32x4 pw[2 * KB];
-      const bool more = t + 1 < npair;
-      if (more) {
-        __builtin_amdgcn_s_waitcnt(0xf70);   // this thread's loads of pair t + 1 landed
-        __syncthreads();                     // ... everyone's; and pair t - 1's slot is free
-        if (t + 2 < npair) issue(t + 2);
-        f32x16 snext[KB];
-        qk(t + 1, snext);
-        probs(sacc, pw);
-        pv(t, pw);
-        mask(t + 1, snext);
+      uint64_t mb;
+      const bool full = tile_full(t + 1, mb);
+      POPE_WAIT_VMCNT(0);   // this thread's loads of pair t + 1 landed
+      __syncthreads();      // ... everyone's; and pair t - 1's slot is free
+      if (t + 2 < npair) issue(t + 2);
+      // keep the exponentials of tile t below the barrier, next to the MFMAs they overlap
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) sacc[kb] = snext[kb];
-      } else {
-        probs(sacc, pw);
-        pv(t, pw);
+      for (int kb = 0; kb < KB; ++kb) asm volatile("" : "+v"(cur[kb]));
+      qk(t + 1, nxt);
+      probs(cur, pw);
+#pragma unroll
+      for (int i = 0; i < KB * KS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedValu, (6 * KB * 16 / 2) / (KB * KS), 0);
       }
+      if (!full) {
+        POPE_COLD_PATH();
+        apply_mask(t + 1, mb, nxt);
+      }
+      pv(t, pw);
+      mt = rowmax(nxt);
+#pragma unroll
+      for (int i = 0; i < (BN / 16) * NDB; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(kSchedValu, 2, 1);
+      }
+    };
+    auto last = [&](int t, f32x16* cur) {
+      rescale(mt, cur);
+      u32x4 pw[2 * KB];
+      probs(cur, pw);
+      pv(t, pw);
+    };
+    // unrolled by two so the score buffers alternate instead of being copied
+    f32x16 sb[KB];
+    int t = 0;
+    for (; t + 2 < npair; t += 2) {
+      step(t, sacc, sb);
+      step(t + 1, sb, sacc);
+    }
+    if (t + 1 < npair) {
+      step(t, sacc, sb);
+      last(t + 1, sb);
+    } else {
+      last(t, sacc);
     }
   }
 
