@@ -25,7 +25,7 @@
 // softmax_scale by multiplying with ln 2.
 //
 // Launches (all on the caller's stream, no atomics except dfreqs / dbias):
-//   delta      : (lse * log2 e, rowsum(O * dO)) per query row
+//   delta      : -lse * log2 e and -rowsum(O * dO) per query row
 //   bwd_main   : one launch holding two kinds of jobs, one per workgroup of 4 waves
 //     dK/dV job: 128 keys (32 per wave) of one (batch, kv head); loops over the
 //                query heads of its group and the query tiles that can see its
@@ -38,8 +38,11 @@
 //                triton_pope_flash_attn.py:215).
 //   Causal dK/dV job r and dQ job (blocks - 1 - r) cost the same; the launch
 //   orders the pairs heaviest first, so the triangle's work balances over the
-//   CUs.  Streamed tiles are double-buffered in LDS, the next one fetched into
-//   registers while the current one is computed.
+//   CUs.  Streamed tiles go straight from global memory into a ring of three LDS
+//   slots (global_load_lds_dwordx4), two steps ahead of the step computed.
+//   The row terms enter the MFMAs as initial accumulators: the score product
+//   starts from -lse (so it returns s - lse and P = exp2 of it) and dO V^T from
+//   -delta (so it returns dP - delta).
 //
 // MFMA layouts (v_mfma_f32_32x32x16, result lane = column, registers = rows
 // 8 (r / 4) + 4 half + r % 4): a result read back as an operand has, per 16-wide
@@ -55,10 +58,13 @@ namespace pope {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kSlots = 3;
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
-__device__ __forceinline__ void st16(uint16_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
+
+typedef const __attribute__((address_space(4))) uint64_t cu64;
+typedef const __attribute__((address_space(4))) int ci32;
 
 // Registers [8 g, 8 g + 8) of an MFMA result, packed as an 8-element operand.
 template <typename T>
@@ -69,20 +75,37 @@ __device__ __forceinline__ u32x4 pack8(const f32x16& x, int g) {
   return w;
 }
 
+// Waits until at most n of this thread's vector loads are outstanding (n a compile-time count).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n <= 8, "wait count");
+  if (n == 0) POPE_WAIT_VMCNT(0);
+  else if (n == 1) POPE_WAIT_VMCNT(1);
+  else if (n == 2) POPE_WAIT_VMCNT(2);
+  else if (n == 3) POPE_WAIT_VMCNT(3);
+  else if (n == 4) POPE_WAIT_VMCNT(4);
+  else if (n == 5) POPE_WAIT_VMCNT(5);
+  else if (n == 6) POPE_WAIT_VMCNT(6);
+  else if (n == 7) POPE_WAIT_VMCNT(7);
+  else POPE_WAIT_VMCNT(8);
+}
+
 // ---------------------------------------------------------------------------
-// delta: one thread per (batch * query head, padded query row): (lse * log2 e, rowsum(O * dO))
-// (_bwd_preprocess, triton_pope_flash_attn.py:119-130).  Rows past Nq and rows with every key
-// masked carry lse = +inf, so their P = exp2(s - lse) is 0 without a test.  With `zero_grads`
-// the first threads also clear dfreqs / dbias, which the main kernel accumulates into.
+// delta: 8 lanes per (batch * query head, padded query row), one 8-element chunk of O and dO
+// each (_bwd_preprocess, triton_pope_flash_attn.py:119-130).  Writes -lse * log2 e and
+// -rowsum(O * dO), the initial accumulators of the main kernel's score and dO V^T products;
+// rows past Nq and rows with every key masked get -inf, so their P = exp2(s - inf) is 0.
+// With `zero_grads` the kernel also clears dfreqs / dbias, which the main kernel accumulates
+// into.
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_delta_kernel(FlashBwdParams p) {
   const int D = p.D, NqP = p.NqP;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (p.zero_grads) {
-    if (p.dbias && idx < (int64_t)p.Hb * p.R) p.dbias[(idx / p.R) * p.bias_sh + idx % p.R] = 0.f;
+    if (p.dbias && gid < (int64_t)p.Hb * p.R) p.dbias[(gid / p.R) * p.bias_sh + gid % p.R] = 0.f;
     const int64_t ndf = (int64_t)p.Bt * p.Ht * p.Nk * p.R;
     if (p.dfreqs)
-      for (int64_t x = idx; x < ndf; x += (int64_t)gridDim.x * 256) {
+      for (int64_t x = gid; x < ndf; x += (int64_t)gridDim.x * 256) {
         const int d = (int)(x % p.R);
         int64_t rest = x / p.R;
         const int n = (int)(rest % p.Nk);
@@ -91,50 +114,64 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(FlashBwdParams p) {
         p.dfreqs[(int64_t)bt * p.df_s[0] + (int64_t)ht * p.df_s[1] + (int64_t)n * p.df_s[2] + d] = 0.f;
       }
   }
-  if (idx >= (int64_t)p.B * p.Hq * NqP) return;
+  const int64_t idx = gid >> 3;
+  const int part = (int)(gid & 7);
+  if (idx >= (int64_t)p.B * p.Hq * NqP) return;   // whole groups of 8 lanes leave together
   const int i = (int)(idx % NqP);
   const int bh = (int)(idx / NqP);
   const int b = bh / p.Hq, h = bh % p.Hq;
-  float dl = 0.f, l2 = INFINITY;
+  float dl = 0.f;
   if (i < p.Nq) {
-    const float l = p.lse[(int64_t)bh * p.Nq + i];
-    l2 = l == -INFINITY ? INFINITY : l * kLog2e;
     const uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1] + (int64_t)i * p.o_s[2];
     const uint16_t* drow = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1] + (int64_t)i * p.do_s[2];
-    for (int d0 = 0; d0 < D; d0 += 8) {
+    for (int d0 = 8 * part; d0 < D; d0 += 64) {
       float xo[8], xd[8];
       unpack8<T>(ld16(orow + d0), xo);
       unpack8<T>(ld16(drow + d0), xd);
 #pragma unroll
-      for (int s = 0; s < 8; ++s) dl += xo[s] * xd[s];
+      for (int s = 0; s < 8; ++s) dl = fmaf(xo[s], xd[s], dl);
     }
   }
-  p.ld[idx] = make_float2(l2, dl);
+  dl += __shfl_xor(dl, 1, 64);
+  dl += __shfl_xor(dl, 2, 64);
+  dl += __shfl_xor(dl, 4, 64);
+  if (part == 0) {
+    float nl = -INFINITY;
+    if (i < p.Nq) {
+      const float l = p.lse[(int64_t)bh * p.Nq + i];
+      nl = l == -INFINITY ? -INFINITY : -l * kLog2e;
+    }
+    p.nl[idx] = nl;
+    p.nd[idx] = -dl;
+  }
 }
 
 // ---------------------------------------------------------------------------
 template <int EP, int DV>
 struct BwdCfg {
   static constexpr bool kBig = EP + DV > 160;
-  static constexpr int BMK = kBig ? 32 : 64;   // query tile of a dK/dV job
-  static constexpr int BNQ = kBig ? 32 : 64;   // key tile of a dQ job
+  static constexpr int BM = kBig ? 32 : 64;    // query rows per dK/dV step, keys per dQ step
   static constexpr int MINB = kBig ? 1 : 2;
-  // Q_hat / dO (dK/dV jobs) and K_hat (dQ jobs) are read by rows and transposed: swizzled
-  // strides; V (dQ jobs) only by rows.
-  static constexpr int QH = 8 * lds_units_tr(EP / 8), DO = 8 * lds_units_tr(DV / 8);
-  static constexpr int VR = 8 * lds_units_rows(DV / 8);
-  // dK/dV stage: Q_hat tile, dO tile, lse and delta
-  static constexpr int KV_STAGE = (BMK * QH + BMK * DO) * 2 + BMK * 8;
-  // dQ stage: K_hat tile, V tile
-  static constexpr int Q_STAGE = (BNQ * QH + BNQ * VR) * 2;
-  static constexpr int STAGE = KV_STAGE > Q_STAGE ? KV_STAGE : Q_STAGE;
+  static constexpr int KS = EP / 16, DS = DV / 16, EB = EP / 32, DB = DV / 32;
+  static constexpr int EPU = EP / 8, DVU = DV / 8;
+  static constexpr int XT = BM * EP, YT = BM * DV;            // elements of the two tiles of a slot
+  static constexpr int XU = XT / 8, YU = YT / 8;              // their 16-byte units
+  static constexpr int LU = BM / 2;                           // -lse and -delta rows (dK/dV slot)
+  static constexpr int KV_UNITS = XU + YU + LU, Q_UNITS = XU + YU;
+  static constexpr int SLOT = KV_UNITS * 16;
+  // loads per thread per step, and the count every wave issues (the last load can be partial)
+  static constexpr int KV_LPT = (KV_UNITS + kThreads - 1) / kThreads;
+  static constexpr int Q_LPT = (Q_UNITS + kThreads - 1) / kThreads;
+  static constexpr int KV_LMIN = (KV_UNITS - 192 + kThreads - 1) / kThreads;   // loads of wave 3
+  static constexpr int Q_LMIN = (Q_UNITS - 192 + kThreads - 1) / kThreads;
   static constexpr int EPI = 32 * (EP + 1) * 4;
-  static constexpr int LDS = 2 * STAGE > EPI ? 2 * STAGE : EPI;
+  static constexpr int LDS = kSlots * SLOT > EPI ? kSlots * SLOT : EPI;
+  static_assert(XU % 64 == 0 && YU % 64 == 0, "tile regions must split at wave boundaries");
 };
 
 // dK / dV job.  Lane lr of wave w owns key j0 + 32 w + lr.
-//   S  = Q_hat K_hat^T : A = Q_hat tile rows (LDS), B = the lane's K_hat row (regs)
-//   dP = dO V^T        : A = dO tile rows (LDS),    B = the lane's V row (regs)
+//   S  = Q_hat K_hat^T - lse : A = Q_hat tile rows (LDS), B = the lane's K_hat row (regs)
+//   dP = dO V^T - delta      : A = dO tile rows (LDS),    B = the lane's V row (regs)
 // Both results have lane = key, registers = queries, so P and dS are A operands
 // (lane = key row, k = queries) of
 //   dV     += P^T dO      B = dO tile read transposed
@@ -142,21 +179,20 @@ struct BwdCfg {
 template <typename T, int EP, int DV>
 __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, float* dbias_s, int kb, int bhk) {
   typedef BwdCfg<EP, DV> C;
-  constexpr int BM = C::BMK, KS = EP / 16, DS = DV / 16, EB = EP / 32, DB = DV / 32, QB = BM / 32;
-  constexpr int QH = C::QH, DO = C::DO;
-  constexpr int QCH = BM * (EP / 8), DCH = BM * (DV / 8);
-  constexpr int QLD = (QCH + kThreads - 1) / kThreads, DLD = (DCH + kThreads - 1) / kThreads;
+  constexpr int BM = C::BM, KS = C::KS, DS = C::DS, EB = C::EB, DB = C::DB, QB = BM / 32;
+  constexpr int EPU = C::EPU, DVU = C::DVU, XU = C::XU, YU = C::YU, UNITS = C::KV_UNITS;
   typedef typename T::vec8 vec8;
 
   const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int b = bhk / p.Hk, hk = bhk % p.Hk;
   const int D = p.D, R = p.R, Nq = p.Nq, Nk = p.Nk, NqP = p.NqP;
   const int j0 = kb * 128;
-  const int kj = j0 + 32 * wave + lr;
+  const int kw0 = j0 + 32 * wave;   // first key of this wave
+  const int kj = kw0 + lr;
 
-  const uint8_t* mrow = p.has_mask ? p.mask + (int64_t)b * p.mask_sb : nullptr;
-  const bool kvis = kj < Nk && (!p.has_mask || mrow[kj] != 0);
-  const TrLane dotr = tr_lane<true>(DO, lane), qhtr = tr_lane<true>(QH, lane);
+  cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
+  const uint64_t kword = mw[kj >> 6];   // kj < NkP: a word exists
+  const bool kvis = (kword >> (kj & 63)) & 1ull;
   for (int e = tid; e < EP; e += kThreads) dbias_s[e] = 0.f;
 
   vec8 kreg[KS], vreg[DS];
@@ -183,110 +219,128 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
     for (int r = 0; r < 16; ++r) dka[x][r] = 0.f;
 
   const bool wave_vis = __all(kvis);
-  const float masked = -INFINITY;
+  const bool wave_any = __any(kvis);
   const int any_key = __syncthreads_or(kvis ? 1 : 0);
-  const int nqt = (Nq + BM - 1) / BM;
-  const int qt0 = p.causal ? min(j0 / BM, nqt) : 0;
+  const int nqt = NqP / BM;
+  const int qt0 = p.causal ? j0 / BM : 0;
   const int groups = p.Hq / p.Hk;
   const int per_head = nqt - qt0;
   const int nsteps = any_key ? groups * per_head : 0;
 
-  // staging of one query tile: global -> registers -> LDS.  The fetch cursor (fg, fqt) walks
-  // the group heads and query tiles in step order; pointers are per-job bases plus offsets.
-  u32x4 qpf[QLD], dpf[DLD];
-  float2 ldpf = make_float2(0.f, 0.f);
+  // ---- direct-load plan: unit c = m * 256 + tid of a slot (Q_hat tile | dO tile | -lse | -delta)
   const uint16_t* qh_job = p.qh + (int64_t)(b * p.Hq + hk) * NqP * EP;
   const int64_t qh_hstride = (int64_t)p.Hk * NqP * EP;
   const uint16_t* do_job = p.dout + (int64_t)b * p.do_s[0] + (int64_t)hk * p.do_s[1];
   const int64_t do_hstride = (int64_t)p.Hk * p.do_s[1];
   const int do_rs = (int)p.do_s[2];
-  const float2* ld_job = p.ld + (int64_t)(b * p.Hq + hk) * NqP;
-  const int64_t ld_hstride = (int64_t)p.Hk * NqP;
-  int fg = 0, fqt = qt0;
-  auto fetch = [&]() {
-    const int i0 = fqt * BM;
-    const uint16_t* qh_g = qh_job + fg * qh_hstride + (int64_t)i0 * EP;
-    const uint16_t* do_g = do_job + fg * do_hstride;
-    // Branch-free: chunk counts are whole multiples of the thread count where possible; rows
-    // past Nq clamp to the last row (their P is 0: lse = +inf) and dims past D to the last
-    // chunk (those columns only meet zero V columns, and their dV is never stored).
+  const float* nl_job = p.nl + (int64_t)(b * p.Hq + hk) * NqP;
+  const float* nd_job = p.nd + (int64_t)(b * p.Hq + hk) * NqP;
+  const int64_t nl_hstride = (int64_t)p.Hk * NqP;
+  int ld_a[C::KV_LPT], ld_b[C::KV_LPT];   // per load: row and column (tiles) or row offset (-lse / -delta)
 #pragma unroll
-    for (int m = 0; m < QLD; ++m) {
-      const int c = tid + m * kThreads;
-      if (QCH % kThreads == 0 || c < QCH) qpf[m] = ld16(qh_g + (c / (EP / 8)) * EP + 8 * (c % (EP / 8)));
+  for (int m = 0; m < C::KV_LPT; ++m) {
+    const int c = m * kThreads + tid;
+    if (c < XU) {
+      const int r = c / EPU;
+      ld_a[m] = r;
+      ld_b[m] = 8 * ((c % EPU) ^ tile_swz(EPU, r));
+    } else if (c < XU + YU) {
+      const int r = (c - XU) / DVU;
+      ld_a[m] = r;
+      ld_b[m] = min(8 * (((c - XU) % DVU) ^ tile_swz(DVU, r)), D - 8);
+    } else {
+      const int cl = c - XU - YU;   // 4 rows per unit: -lse rows, then -delta rows
+      ld_a[m] = 4 * (cl % (BM / 4));
+      ld_b[m] = cl < BM / 4 ? 0 : 1;
     }
+  }
+  auto issue = [&](int st) {
+    const int g = st / per_head, i0 = (qt0 + st % per_head) * BM;
+    char* slot = smem + (st % kSlots) * C::SLOT;
+    const uint16_t* qg = qh_job + g * qh_hstride + (int64_t)i0 * EP;
+    const uint16_t* dg = do_job + g * do_hstride;
+    const float* lg = nl_job + g * nl_hstride + i0;
+    const float* ddg = nd_job + g * nl_hstride + i0;
 #pragma unroll
-    for (int m = 0; m < DLD; ++m) {
-      const int c = tid + m * kThreads;
-      if (DCH % kThreads == 0 || c < DCH) {
-        const int row = min(i0 + c / (DV / 8), Nq - 1), d8 = min(8 * (c % (DV / 8)), D - 8);
-        dpf[m] = ld16(do_g + (int64_t)row * do_rs + d8);
+    for (int m = 0; m < C::KV_LPT; ++m) {
+      const int c0 = m * kThreads + wave * 64;
+      const uint32_t dst = lds_addr(slot + c0 * 16);
+      if ((m + 1) * kThreads <= XU) {
+        load_lds16(qg + ld_a[m] * EP + ld_b[m], dst);
+      } else if (m * kThreads >= XU && (m + 1) * kThreads <= XU + YU) {
+        load_lds16(dg + min(i0 + ld_a[m], Nq - 1) * do_rs + ld_b[m], dst);
+      } else {   // boundary loads: per-wave region, partial waves past the slot
+        if (c0 < XU) {
+          load_lds16(qg + ld_a[m] * EP + ld_b[m], dst);
+        } else if (c0 < XU + YU) {
+          load_lds16(dg + min(i0 + ld_a[m], Nq - 1) * do_rs + ld_b[m], dst);
+        } else if (c0 < UNITS) {
+          if (m * kThreads + tid < UNITS) load_lds16((ld_b[m] ? ddg : lg) + ld_a[m], dst);
+        }
       }
     }
-    if (tid < BM) ldpf = ld_job[fg * ld_hstride + i0 + tid];
-    if (++fqt == nqt) {
-      fqt = qt0;
-      ++fg;
-    }
-  };
-  auto stage = [&](int buf) {
-    uint16_t* qh_s = reinterpret_cast<uint16_t*>(smem + buf * C::STAGE);
-    uint16_t* do_s = qh_s + BM * QH;
-    float2* ld_s = reinterpret_cast<float2*>(do_s + BM * DO);
-#pragma unroll
-    for (int m = 0; m < QLD; ++m) {
-      const int c = tid + m * kThreads;
-      const int row = c / (EP / 8);
-      if (QCH % kThreads == 0 || c < QCH) st16(qh_s + row * QH + 8 * lds_swz(row, c % (EP / 8)), qpf[m]);
-    }
-#pragma unroll
-    for (int m = 0; m < DLD; ++m) {
-      const int c = tid + m * kThreads;
-      const int row = c / (DV / 8);
-      if (DCH % kThreads == 0 || c < DCH) st16(do_s + row * DO + 8 * lds_swz(row, c % (DV / 8)), dpf[m]);
-    }
-    if (tid < BM) ld_s[tid] = ldpf;
   };
 
-  if (nsteps > 0) {
-    fetch();
-    stage(0);
-  }
-  __syncthreads();
-  int i0 = qt0 * BM;   // query tile of the current step
+  // ---- LDS operand offsets (elements) ------------------------------------------------
+  int qrow[KS], drow[DS], qtr_lo[EB], qtr_hi[EB], dtr_lo[DB], dtr_hi[DB];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) qrow[kk] = row_offset<EPU>(lane, kk);
+#pragma unroll
+  for (int kk = 0; kk < DS; ++kk) drow[kk] = row_offset<DVU>(lane, kk);
+#pragma unroll
+  for (int eb = 0; eb < EB; ++eb) tr_offsets<EPU>(lane, eb, qtr_lo[eb], qtr_hi[eb]);
+#pragma unroll
+  for (int db = 0; db < DB; ++db) tr_offsets<DVU>(lane, db, dtr_lo[db], dtr_hi[db]);
+
+  if (nsteps > 0) issue(0);
+  if (nsteps > 1) issue(1);
   for (int st = 0; st < nsteps; ++st) {
-    const int buf = st & 1;
-    if (st + 1 < nsteps) fetch();
-    const uint16_t* qh_s = reinterpret_cast<const uint16_t*>(smem + buf * C::STAGE);
-    const uint16_t* do_s = qh_s + BM * QH;
-    const float2* ld_s = reinterpret_cast<const float2*>(do_s + BM * DO);
+    if (st + 1 < nsteps) wait_vmcnt<C::KV_LMIN>();   // this thread's loads of step st landed
+    else wait_vmcnt<0>();
+    __syncthreads();                                // ... everyone's; step st - 1's slot is free
+    if (st + 2 < nsteps) issue(st + 2);
+    const int i0 = (qt0 + st % per_head) * BM;
+    const uint16_t* qh_s = reinterpret_cast<const uint16_t*>(smem + (st % kSlots) * C::SLOT);
+    const uint16_t* do_s = qh_s + C::XT;
+    const float* nl_s = reinterpret_cast<const float*>(do_s + C::YT);
+    const float* nd_s = nl_s + BM;
 #pragma unroll
     for (int qs = 0; qs < QB; ++qs) {
-      f32x16 s = {}, dp = {};
+      // every query of the sub-tile before every key of the wave (causal), or no visible key
+      if ((p.causal && i0 + 32 * qs + 31 < kw0) || !wave_any) continue;
+      f32x16 s, dp;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {   // rows 32 qs + 8 q + 4 hf + (0..3)
+        const f32x4 a = *reinterpret_cast<const f32x4*>(nl_s + 32 * qs + 8 * q + 4 * hf);
+        const f32x4 d = *reinterpret_cast<const f32x4*>(nd_s + 32 * qs + 8 * q + 4 * hf);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          s[4 * q + x] = a[x];
+          dp[4 * q + x] = d[x];
+        }
+      }
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk)
-        s = T::mfma32(as_vec8<vec8>(ld16(qh_s + (32 * qs + lr) * QH + 8 * lds_swz(lr, 2 * kk + hf))), kreg[kk], s);
+        s = T::mfma32(as_vec8<vec8>(ld16(qh_s + 32 * qs * EP + qrow[kk])), kreg[kk], s);
 #pragma unroll
       for (int kk = 0; kk < DS; ++kk)
-        dp = T::mfma32(as_vec8<vec8>(ld16(do_s + (32 * qs + lr) * DO + 8 * lds_swz(lr, 2 * kk + hf))), vreg[kk], dp);
+        dp = T::mfma32(as_vec8<vec8>(ld16(do_s + 32 * qs * DV + drow[kk])), vreg[kk], dp);
       // Partial sub-tile (some key of the wave masked, or on the causal diagonal): masked
-      // scores become -inf so that P = 0.  Rows past Nq and fully
-      // masked rows carry lse = +inf, which gives P = 0 without a test.
-      if (!wave_vis || (p.causal && i0 + 32 * qs < j0 + 32 * wave + 31)) {
+      // scores become -inf so that P = 0.
+      if (!wave_vis || (p.causal && i0 + 32 * qs < kw0 + 31)) {
         POPE_COLD_PATH();
+        const int lim = i0 + 32 * qs + 4 * hf - kj;   // causal: row offset >= -lim
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int qr = 32 * qs + 8 * (r >> 2) + 4 * hf + (r & 3);
-          s[r] = (kvis && (!p.causal || kj <= i0 + qr)) ? s[r] : masked;
+          const int qr = 8 * (r >> 2) + (r & 3);
+          s[r] = (kvis && (!p.causal || qr + lim >= 0)) ? s[r] : -INFINITY;
         }
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int qr = 32 * qs + 8 * (r >> 2) + 4 * hf + (r & 3);
-        const float2 ld = ld_s[qr];
-        const float pv = __builtin_amdgcn_exp2f(s[r] - ld.x);
+        const float pv = __builtin_amdgcn_exp2f(s[r]);
         s[r] = pv;
-        dp[r] = pv * (dp[r] - ld.y);
+        dp[r] = pv * dp[r];
       }
 #pragma unroll
       for (int g2 = 0; g2 < 2; ++g2) {
@@ -295,16 +349,14 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
         const int r0 = 32 * qs + 16 * g2;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
-          dva[db] = T::mfma32(ap, as_vec8<vec8>(lds_operand_tr(do_s, dotr, DO, r0, 32 * db)), dva[db]);
+          dva[db] = T::mfma32(ap, as_vec8<vec8>(lds_tr8(do_s + r0 * DV, dtr_lo[db], dtr_hi[db])), dva[db]);
 #pragma unroll
         for (int eb = 0; eb < EB; ++eb)
-          dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_operand_tr(qh_s, qhtr, QH, r0, 32 * eb)), dka[eb]);
+          dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_tr8(qh_s + r0 * EP, qtr_lo[eb], qtr_hi[eb])), dka[eb]);
       }
     }
-    if (st + 1 < nsteps) stage(buf ^ 1);
-    __syncthreads();
-    i0 = i0 + BM == nqt * BM ? qt0 * BM : i0 + BM;
   }
+  __syncthreads();   // every wave is done with the slots
 
   // ---- dV: lane = d column, registers = the wave's keys -----------------------
   {
@@ -363,17 +415,15 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
 }
 
 // dQ job.  Lane lr of wave w owns query i0 + 32 w + lr.
-//   S^T  = K_hat Q_hat^T : A = K_hat tile rows (LDS), B = the lane's Q_hat row (regs)
-//   dP^T = V dO^T        : A = V tile rows (LDS),     B = the lane's dO row (regs)
+//   S^T  = K_hat Q_hat^T - lse : A = K_hat tile rows (LDS), B = the lane's Q_hat row (regs)
+//   dP^T = V dO^T - delta      : A = V tile rows (LDS),     B = the lane's dO row (regs)
 // Results: lane = query, registers = keys; dS^T is the B operand of
 //   dQ_hat^T += K_hat^T dS^T   A = K_hat tile read transposed.
 template <typename T, int EP, int DV>
-__device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint64_t* mbits_s, int qb, int bh) {
+__device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int qb, int bh) {
   typedef BwdCfg<EP, DV> C;
-  constexpr int BN = C::BNQ, KS = EP / 16, DS = DV / 16, EB = EP / 32, NB = BN / 32;
-  constexpr int KH = C::QH, VR = C::VR;
-  constexpr int KCH = BN * (EP / 8), VCH = BN * (DV / 8);
-  constexpr int KLD = (KCH + kThreads - 1) / kThreads, VLD = (VCH + kThreads - 1) / kThreads;
+  constexpr int BN = C::BM, KS = C::KS, DS = C::DS, EB = C::EB, NB = BN / 32;
+  constexpr int EPU = C::EPU, DVU = C::DVU, XU = C::XU, UNITS = C::Q_UNITS;
   typedef typename T::vec8 vec8;
 
   const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lr = lane & 31, hf = lane >> 5;
@@ -381,9 +431,8 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
   const int bhk = b * p.Hk + hk;
   const int D = p.D, R = p.R, Nq = p.Nq, Nk = p.Nk, NkP = p.NkP;
   const int q_off = Nk - Nq;
-  const int qi = qb * 128 + 32 * wave + lr;
-  const bool qvalid = qi < Nq;
-  const TrLane khtr = tr_lane<true>(KH, lane);
+  const int qw0 = qb * 128 + 32 * wave;
+  const int qi = qw0 + lr;
 
   vec8 qreg[KS], doreg[DS];
   {
@@ -395,12 +444,19 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
 #pragma unroll
     for (int kk = 0; kk < DS; ++kk) {
       const int d0 = 16 * kk + 8 * hf;
-      doreg[kk] = as_vec8<vec8>((qvalid && d0 < D) ? ld16(dr + d0) : zero4());
+      doreg[kk] = as_vec8<vec8>((qi < Nq && d0 < D) ? ld16(dr + d0) : zero4());
     }
   }
-  const float masked = -INFINITY;
-  const float2 ld = p.ld[(int64_t)bh * p.NqP + qi];   // rows past Nq: lse = +inf
-  const float lse2 = ld.x, dl = ld.y;
+  // initial accumulators: -lse and -delta of the lane's query in every register
+  f32x16 nlc, ndc;
+  {
+    const float a = p.nl[(int64_t)bh * p.NqP + qi], d = p.nd[(int64_t)bh * p.NqP + qi];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      nlc[r] = a;
+      ndc[r] = d;
+    }
+  }
 
   f32x16 dqa[EB];
 #pragma unroll
@@ -408,108 +464,104 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, uint
 #pragma unroll
     for (int r = 0; r < 16; ++r) dqa[x][r] = 0.f;
 
-  int nt = (Nk + BN - 1) / BN;
-  if (p.causal) {
-    const int last_q = min(qb * 128 + 128, Nq) - 1;
-    nt = last_q < 0 ? 0 : min(nt, last_q / BN + 1);
-  }
+  cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
+  int nkeys = min(((ci32*)p.kend)[b], Nk);
+  if (p.causal) nkeys = min(nkeys, min(qb * 128 + 128, Nq));
+  const int nt = (nkeys + BN - 1) / BN;
+
+  // ---- direct-load plan: unit c = m * 256 + tid of a slot (K_hat tile | V tile) --------
   const uint16_t* kh_g = p.kh + (int64_t)bhk * NkP * EP;
   const uint16_t* v_g = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
-  const uint8_t* mrow = p.has_mask ? p.mask + (int64_t)b * p.mask_sb : nullptr;
-
-  u32x4 kpf[KLD], vpf[VLD];
-  uint64_t mpf = 0;
-  auto fetch = [&](int kt) {
-    const int j0 = kt * BN;
-    // Branch-free as in the dK/dV job: keys past Nk clamp to the last row (masked, P = 0) and
-    // dims past D to the last chunk (those columns only meet zero dO columns).
+  const int vs2 = (int)p.v_s[2];
+  int ld_r[C::Q_LPT], ld_c[C::Q_LPT];
 #pragma unroll
-    for (int m = 0; m < KLD; ++m) {
-      const int c = tid + m * kThreads;
-      if (KCH % kThreads == 0 || c < KCH) kpf[m] = ld16(kh_g + (int64_t)(j0 + c / (EP / 8)) * EP + 8 * (c % (EP / 8)));
+  for (int m = 0; m < C::Q_LPT; ++m) {
+    const int c = m * kThreads + tid;
+    if (c < XU) {
+      const int r = c / EPU;
+      ld_r[m] = r;
+      ld_c[m] = 8 * ((c % EPU) ^ tile_swz(EPU, r));
+    } else {
+      const int r = (c - XU) / DVU;
+      ld_r[m] = r;
+      ld_c[m] = min(8 * (((c - XU) % DVU) ^ tile_swz(DVU, r)), D - 8);
     }
+  }
+  auto issue = [&](int kt) {
+    const int j0 = kt * BN;
+    char* slot = smem + (kt % kSlots) * C::SLOT;
+    const uint16_t* kg = kh_g + j0 * EP;   // K_hat rows are padded to NkP
 #pragma unroll
-    for (int m = 0; m < VLD; ++m) {
-      const int c = tid + m * kThreads;
-      if (VCH % kThreads == 0 || c < VCH) {
-        const int row = min(j0 + c / (DV / 8), Nk - 1), d8 = min(8 * (c % (DV / 8)), D - 8);
-        vpf[m] = ld16(v_g + (int64_t)row * p.v_s[2] + d8);
+    for (int m = 0; m < C::Q_LPT; ++m) {
+      const int c0 = m * kThreads + wave * 64;
+      const uint32_t dst = lds_addr(slot + c0 * 16);
+      const uint16_t* vsrc = v_g + min(j0 + ld_r[m], Nk - 1) * vs2 + ld_c[m];
+      if ((m + 1) * kThreads <= XU) {
+        load_lds16(kg + ld_r[m] * EP + ld_c[m], dst);
+      } else if (m * kThreads >= XU) {
+        if (UNITS % kThreads == 0 || c0 < UNITS) load_lds16(vsrc, dst);
+      } else {
+        load_lds16(c0 < XU ? (const void*)(kg + ld_r[m] * EP + ld_c[m]) : (const void*)vsrc, dst);
       }
     }
-    if (wave == 0) {   // bit j: key j0 + j visible
-      const int key = j0 + lane;
-      mpf = __ballot(lane < BN && key < Nk && (!p.has_mask || mrow[key] != 0));
-    }
-  };
-  auto stage = [&](int buf) {
-    uint16_t* kh_s = reinterpret_cast<uint16_t*>(smem + buf * C::STAGE);
-    uint16_t* v_s = kh_s + BN * KH;
-#pragma unroll
-    for (int m = 0; m < KLD; ++m) {
-      const int c = tid + m * kThreads;
-      const int row = c / (EP / 8);
-      if (KCH % kThreads == 0 || c < KCH) st16(kh_s + row * KH + 8 * lds_swz(row, c % (EP / 8)), kpf[m]);
-    }
-#pragma unroll
-    for (int m = 0; m < VLD; ++m) {
-      const int c = tid + m * kThreads;
-      if (VCH % kThreads == 0 || c < VCH) st16(v_s + (c / (DV / 8)) * VR + 8 * (c % (DV / 8)), vpf[m]);
-    }
-    if (tid == 0) mbits_s[buf] = mpf;
   };
 
-  if (nt > 0) {
-    fetch(0);
-    stage(0);
-  }
-  __syncthreads();
+  int krow[KS], vrow[DS], ktr_lo[EB], ktr_hi[EB];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) krow[kk] = row_offset<EPU>(lane, kk);
+#pragma unroll
+  for (int kk = 0; kk < DS; ++kk) vrow[kk] = row_offset<DVU>(lane, kk);
+#pragma unroll
+  for (int eb = 0; eb < EB; ++eb) tr_offsets<EPU>(lane, eb, ktr_lo[eb], ktr_hi[eb]);
+
+  if (nt > 0) issue(0);
+  if (nt > 1) issue(1);
   for (int kt = 0; kt < nt; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nt) fetch(kt + 1);
+    if (kt + 1 < nt) wait_vmcnt<C::Q_LMIN>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    if (kt + 2 < nt) issue(kt + 2);
     const int j0 = kt * BN;
-    const uint16_t* kh_s = reinterpret_cast<const uint16_t*>(smem + buf * C::STAGE);
-    const uint16_t* v_s = kh_s + BN * KH;
-    const uint64_t mraw = mbits_s[buf];
-    const uint64_t mb = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)mraw) |
-                        ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(mraw >> 32)) << 32);
-    const uint64_t all_bits = BN == 64 ? ~0ull : ((1ull << BN) - 1);
+    const uint16_t* kh_s = reinterpret_cast<const uint16_t*>(smem + (kt % kSlots) * C::SLOT);
+    const uint16_t* v_s = kh_s + C::XT;
+    uint64_t mb = mw[j0 >> 6];
+    if (BN == 32) mb = (mb >> (j0 & 32)) & 0xffffffffull;
+    const uint64_t all_bits = BN == 64 ? ~0ull : 0xffffffffull;
     // every key visible and (causal) every key at or before the wave's first query
-    const bool full = mb == all_bits && !(p.causal && j0 + BN - 1 > qb * 128 + 32 * wave);
-    if (mb == 0) {   // every key of this tile masked
-      if (kt + 1 < nt) stage(buf ^ 1);
-      __syncthreads();
-      continue;
-    }
+    const bool full = mb == all_bits && !(p.causal && j0 + BN - 1 > qw0);
+    if (mb == 0 || (p.causal && j0 > qw0 + 31)) continue;   // nothing visible to this wave
 #pragma unroll
     for (int ks = 0; ks < NB; ++ks) {
-      f32x16 s = {}, dp = {};
+      f32x16 s = nlc, dp = ndc;
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk)
-        s = T::mfma32(as_vec8<vec8>(ld16(kh_s + (32 * ks + lr) * KH + 8 * lds_swz(lr, 2 * kk + hf))), qreg[kk], s);
+        s = T::mfma32(as_vec8<vec8>(ld16(kh_s + 32 * ks * EP + krow[kk])), qreg[kk], s);
 #pragma unroll
       for (int kk = 0; kk < DS; ++kk)
-        dp = T::mfma32(as_vec8<vec8>(ld16(v_s + (32 * ks + lr) * VR + 16 * kk + 8 * hf)), doreg[kk], dp);
+        dp = T::mfma32(as_vec8<vec8>(ld16(v_s + 32 * ks * DV + vrow[kk])), doreg[kk], dp);
       if (!full) {   // masked scores -> -inf: P = 0
         POPE_COLD_PATH();
+        const uint64_t w = mb >> (32 * ks + 4 * hf);
+        const int lim = p.causal ? qi - j0 - 32 * ks - 4 * hf : 64;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int kr = 32 * ks + 8 * (r >> 2) + 4 * hf + (r & 3);
-          s[r] = (((mb >> kr) & 1ull) && (!p.causal || j0 + kr <= qi)) ? s[r] : masked;
+          const int kr = 8 * (r >> 2) + (r & 3);
+          s[r] = (((uint32_t)(w >> kr) & 1u) && kr <= lim) ? s[r] : -INFINITY;
         }
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dp[r] = __builtin_amdgcn_exp2f(s[r] - lse2) * (dp[r] - dl);
+      for (int r = 0; r < 16; ++r) dp[r] = __builtin_amdgcn_exp2f(s[r]) * dp[r];
 #pragma unroll
       for (int g2 = 0; g2 < 2; ++g2) {
         const vec8 bds = as_vec8<vec8>(pack8<T>(dp, g2));
+        const uint16_t* kr0 = kh_s + (32 * ks + 16 * g2) * EP;
 #pragma unroll
         for (int eb = 0; eb < EB; ++eb)
-          dqa[eb] = T::mfma32(as_vec8<vec8>(lds_operand_tr(kh_s, khtr, KH, 32 * ks + 16 * g2, 32 * eb)), bds, dqa[eb]);
+          dqa[eb] = T::mfma32(as_vec8<vec8>(lds_tr8(kr0, ktr_lo[eb], ktr_hi[eb])), bds, dqa[eb]);
       }
     }
-    if (kt + 1 < nt) stage(buf ^ 1);
-    __syncthreads();
   }
+  __syncthreads();   // every wave is done with the slots
 
   // ---- dQ: query-side chain rule, one wave's 32 queries at a time through LDS ----
   constexpr int BS = EP + 1;
@@ -554,7 +606,6 @@ template <typename T, int EP, int DV>
 __global__ __launch_bounds__(kThreads, (BwdCfg<EP, DV>::MINB)) void bwd_main_kernel(FlashBwdParams p) {
   __shared__ __attribute__((aligned(16))) char smem[BwdCfg<EP, DV>::LDS];
   __shared__ float dbias_s[EP];
-  __shared__ uint64_t mbits_s[2];
   const int nqb = p.NqP / 128;
   const int id = blockIdx.x;
   int kind, blk, head;   // kind 0 = dK/dV job (head = b * Hk + hk), 1 = dQ job (head = b * Hq + h)
@@ -581,14 +632,14 @@ __global__ __launch_bounds__(kThreads, (BwdCfg<EP, DV>::MINB)) void bwd_main_ker
   if (kind == 0)
     dkdv_job<T, EP, DV>(p, smem, dbias_s, blk, head);
   else
-    dq_job<T, EP, DV>(p, smem, mbits_s, blk, head);
+    dq_job<T, EP, DV>(p, smem, blk, head);
 }
 
 template <typename T, int EP, int DV>
 hipError_t launch_t(const FlashBwdParams& p0, hipStream_t s) {
   FlashBwdParams p = p0;
   const int64_t nrows = (int64_t)p.B * p.Hq * p.NqP;
-  hipError_t e = launch_named("flash_bwd_delta", bwd_delta_kernel<T>, dim3((unsigned)((nrows + 255) / 256)),
+  hipError_t e = launch_named("flash_bwd_delta", bwd_delta_kernel<T>, dim3((unsigned)((8 * nrows + 255) / 256)),
                               dim3(256), s, p);
   if (e != hipSuccess) return e;
   const int nkb = p.NkP / 128, nqb = p.NqP / 128;

@@ -52,25 +52,6 @@ constexpr int kStages = 3;
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-// Direct global -> LDS load of 16 bytes per lane: lane l's bytes land at LDS byte address
-// lds + 16 l (lds is wave-uniform, passed in M0).  Written as inline assembly so that the
-// compiler does not add its conservative wait for every outstanding LDS load before each LDS
-// read: the kernel waits for its own loads (vmcnt) before the barrier that publishes a stage.
-__device__ __forceinline__ void load_lds16(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory");
-}
-
-// LDS byte address of a pointer into a __shared__ array.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
-}
-
-// Waits until at most n of this thread's vector memory loads are outstanding.
-#define POPE_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
-
-// Instruction-group masks of __builtin_amdgcn_sched_group_barrier.
-constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedDsRead = 0x100;
-
 template <int EP, int DV>
 struct FwdCfg {
   static constexpr int BN = (EP + DV <= 192 && DV <= 64) ? 64 : 32;   // keys per tile

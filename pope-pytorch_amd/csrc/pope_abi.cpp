@@ -107,7 +107,7 @@ int check_ws(size_t need, void* ws, size_t have) {
 //   cos/sin(F) (Bt, Ht, Nk, R) float2 | cos/sin(bias) (Hb, R) float2
 //   | K_hat (B, Hk, NkP, EP) | Q_hat (B, Hq, NqP, EP)      16-bit elements
 //   | key visibility words (B, NW) u64 | last visible key + 1 (B) int32
-//   | (lse * log2 e, delta) (B, Hq, NqP) float2            backward only
+//   | -lse * log2 e, -delta (B, Hq, NqP) fp32 each           backward only
 // with EP = round_up(D + R, 32), DV = round_up(D, 32), NqP / NkP = round_up(N, 128),
 // NW = NkP / 64.
 void copy3(int64_t* dst, const int64_t* src);
@@ -426,7 +426,11 @@ int pope_flash_bwd(const pope_desc* d, const void* dout, const void* q, const vo
   p.dbias = dbias;
   p.qh = reinterpret_cast<const uint16_t*>(ws + L.qh);
   p.kh = reinterpret_cast<const uint16_t*>(ws + L.kh);
-  p.ld = reinterpret_cast<float2*>(ws + L.ld);
+  p.nl = reinterpret_cast<float*>(ws + L.ld);
+  p.nd = p.nl + (size_t)d->B * d->Hq * L.NqP;
+  p.mwords = reinterpret_cast<const uint64_t*>(ws + L.mwords);
+  p.kend = reinterpret_cast<const int*>(ws + L.kend);
+  p.NW = L.NW;
   p.B = d->B; p.Hq = d->Hq; p.Hk = d->Hk; p.Nq = d->Nq; p.Nk = d->Nk; p.D = d->D; p.R = d->R;
   p.E = d->D + d->R;
   p.EP = L.EP;

@@ -177,6 +177,55 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
+// Direct global -> LDS load of 16 bytes per lane: lane l's bytes land at LDS byte address
+// lds + 16 l (lds is wave-uniform, passed in M0).  Written as inline assembly so that the
+// compiler does not add its conservative wait for every outstanding LDS load before each LDS
+// read: the kernel waits for its own loads (vmcnt) before the barrier that publishes a stage.
+__device__ __forceinline__ void load_lds16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory");
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// Waits until at most n of this thread's vector memory loads are outstanding.
+#define POPE_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+
+// Instruction-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedDsRead = 0x100;
+
+// Element offsets, inside a row-major tile of U 16-byte units per row stored with tile_swz, of
+// the two 4-element chunks a lane reads for an 8-element MFMA operand taken transposed
+// (lds_read_tr16): rows R0 + 4 h + j / 4 and R0 + 8 + 4 h + j / 4, columns n0 + 8 u + 4 (j & 1)
+// with j = lane % 16, h = lane / 32, u = 2 (lane / 16 % 2) + (j / 2 % 2), relative to R0 = 0 and
+// the 32-column block n0 = 32 nb.  The operand's k order (rows) is the register order of a
+// 32x32 MFMA result read back as an operand: [4 h, 4 h + 4) then [8 + 4 h, 12 + 4 h).
+template <int U>
+__device__ __forceinline__ void tr_offsets(int lane, int nb, int& lo, int& hi) {
+  const int j = lane & 15, gi = lane >> 4;
+  const int u = 2 * (gi & 1) + ((j >> 1) & 1), sub = 4 * (j & 1);
+  const int rlo = 4 * (lane >> 5) + (j >> 2), rhi = rlo + 8;
+  lo = rlo * 8 * U + 8 * ((4 * nb + u) ^ tile_swz(U, rlo)) + sub;
+  hi = rhi * 8 * U + 8 * ((4 * nb + u) ^ tile_swz(U, rhi)) + sub;
+}
+
+// Element offset of the 8-element operand chunk a lane reads by rows: row lane % 32, unit
+// 2 kk + lane / 32 of a tile of U units per row stored with tile_swz.
+template <int U>
+__device__ __forceinline__ int row_offset(int lane, int kk) {
+  const int lr = lane & 31;
+  return lr * 8 * U + 8 * ((2 * kk + (lane >> 5)) ^ tile_swz(U, lr));
+}
+
+// 8-element operand from the two transposed chunks at lo and hi.
+__device__ __forceinline__ u32x4 lds_tr8(const uint16_t* base, int lo, int hi) {
+  const u32x2 a = lds_read_tr16(base + lo);
+  const u32x2 b = lds_read_tr16(base + hi);
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+
 // 8-element operand of a 32x32x16 MFMA taken from a row-major LDS tile X
 // (row stride ld elements) transposed: lane l gets column n0 + l % 32 and the
 // rows [R0 + 4 h, R0 + 4 h + 4) followed by [R0 + 8 + 4 h, R0 + 12 + 4 h),

@@ -81,8 +81,10 @@ struct FlashBwdParams {
   // workspace (FlashPrep): expanded rows, zero past Nq / Nk and past E
   const uint16_t* qh;        // (B, Hq, NqP, EP)  Q_hat * softmax_scale * log2(e)
   const uint16_t* kh;        // (B, Hk, NkP, EP)  K_hat
-  float2* ld;                // (B, Hq, NqP)      (lse * log2(e), rowsum(O * dO)); rows past Nq and
-                             //                   rows with every key masked carry lse = +inf
+  float* nl; float* nd;      // (B, Hq, NqP)      -lse * log2(e) and -rowsum(O * dO); rows past Nq and
+                             //                   rows with every key masked carry -inf in nl
+  const uint64_t* mwords; const int* kend;   // key visibility (FlashPrep)
+  int NW;
   int B, Hq, Hk, Nq, Nk, D, R, E, EP, DV, NqP, NkP, causal, has_mask;
   int Bt, Ht, Hb;            // extents of the cos/sin table and of the bias rows
   int zero_grads;            // clear dfreqs / dbias before accumulating
