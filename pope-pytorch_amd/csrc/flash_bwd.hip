@@ -234,63 +234,58 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
   const int64_t do_hstride = (int64_t)p.Hk * p.do_s[1];
   const int do_rs = (int)p.do_s[2];
   const float* nl_job = p.nl + (int64_t)(b * p.Hq + hk) * NqP;
-  const float* nd_job = p.nd + (int64_t)(b * p.Hq + hk) * NqP;
   const int64_t nl_hstride = (int64_t)p.Hk * NqP;
-  int ld_a[C::KV_LPT], ld_b[C::KV_LPT];   // per load: row and column (tiles) or row offset (-lse / -delta)
+  // one offset per load: Q_hat element offset in the tile; dO element offset of (row, column)
+  // relative to the tile's first row (rows past Nq clamp to the last chunk of the last row:
+  // those rows only meet P = 0); -lse / -delta offset from the tile's first -lse row (the -delta array
+  // follows the -lse array in the workspace)
+  const int64_t nd_off = p.nd - p.nl;
+  int ld_o[C::KV_LPT];
 #pragma unroll
   for (int m = 0; m < C::KV_LPT; ++m) {
     const int c = m * kThreads + tid;
     if (c < XU) {
       const int r = c / EPU;
-      ld_a[m] = r;
-      ld_b[m] = 8 * ((c % EPU) ^ tile_swz(EPU, r));
+      ld_o[m] = r * EP + 8 * ((c % EPU) ^ tile_swz(EPU, r));
     } else if (c < XU + YU) {
       const int r = (c - XU) / DVU;
-      ld_a[m] = r;
-      ld_b[m] = min(8 * (((c - XU) % DVU) ^ tile_swz(DVU, r)), D - 8);
+      ld_o[m] = r * do_rs + min(8 * (((c - XU) % DVU) ^ tile_swz(DVU, r)), D - 8);
     } else {
       const int cl = c - XU - YU;   // 4 rows per unit: -lse rows, then -delta rows
-      ld_a[m] = 4 * (cl % (BM / 4));
-      ld_b[m] = cl < BM / 4 ? 0 : 1;
+      ld_o[m] = 4 * (cl % (BM / 4)) + (cl < BM / 4 ? 0 : (int)nd_off);
     }
   }
+  const int do_last = (Nq - 1) * do_rs + D - 8;   // start of the last chunk of the last row
   auto issue = [&](int st) {
     const int g = st / per_head, i0 = (qt0 + st % per_head) * BM;
     char* slot = smem + (st % kSlots) * C::SLOT;
     const uint16_t* qg = qh_job + g * qh_hstride + (int64_t)i0 * EP;
     const uint16_t* dg = do_job + g * do_hstride;
     const float* lg = nl_job + g * nl_hstride + i0;
-    const float* ddg = nd_job + g * nl_hstride + i0;
+    const int drow0 = i0 * do_rs;
 #pragma unroll
     for (int m = 0; m < C::KV_LPT; ++m) {
       const int c0 = m * kThreads + wave * 64;
       const uint32_t dst = lds_addr(slot + c0 * 16);
       if ((m + 1) * kThreads <= XU) {
-        load_lds16(qg + ld_a[m] * EP + ld_b[m], dst);
+        load_lds16(qg + ld_o[m], dst);
       } else if (m * kThreads >= XU && (m + 1) * kThreads <= XU + YU) {
-        load_lds16(dg + min(i0 + ld_a[m], Nq - 1) * do_rs + ld_b[m], dst);
+        load_lds16(dg + min(drow0 + ld_o[m], do_last), dst);
       } else {   // boundary loads: per-wave region, partial waves past the slot
         if (c0 < XU) {
-          load_lds16(qg + ld_a[m] * EP + ld_b[m], dst);
+          load_lds16(qg + ld_o[m], dst);
         } else if (c0 < XU + YU) {
-          load_lds16(dg + min(i0 + ld_a[m], Nq - 1) * do_rs + ld_b[m], dst);
+          load_lds16(dg + min(drow0 + ld_o[m], do_last), dst);
         } else if (c0 < UNITS) {
-          if (m * kThreads + tid < UNITS) load_lds16((ld_b[m] ? ddg : lg) + ld_a[m], dst);
+          if (m * kThreads + tid < UNITS) load_lds16(lg + ld_o[m], dst);
         }
       }
     }
   };
 
   // ---- LDS operand offsets (elements) ------------------------------------------------
-  int qrow[KS], drow[DS], qtr_lo[EB], qtr_hi[EB], dtr_lo[DB], dtr_hi[DB];
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) qrow[kk] = row_offset<EPU>(lane, kk);
-#pragma unroll
-  for (int kk = 0; kk < DS; ++kk) drow[kk] = row_offset<DVU>(lane, kk);
-#pragma unroll
-  for (int eb = 0; eb < EB; ++eb) tr_offsets<EPU>(lane, eb, qtr_lo[eb], qtr_hi[eb]);
-#pragma unroll
-  for (int db = 0; db < DB; ++db) tr_offsets<DVU>(lane, db, dtr_lo[db], dtr_hi[db]);
+  const TileOffsets<EPU> qo(lane);
+  const TileOffsets<DVU> doo(lane);
 
   if (nsteps > 0) issue(0);
   if (nsteps > 1) issue(1);
@@ -321,10 +316,10 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
       }
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk)
-        s = T::mfma32(as_vec8<vec8>(ld16(qh_s + 32 * qs * EP + qrow[kk])), kreg[kk], s);
+        s = T::mfma32(as_vec8<vec8>(ld16(qh_s + 32 * qs * EP + qo.row_at(kk))), kreg[kk], s);
 #pragma unroll
       for (int kk = 0; kk < DS; ++kk)
-        dp = T::mfma32(as_vec8<vec8>(ld16(do_s + 32 * qs * DV + drow[kk])), vreg[kk], dp);
+        dp = T::mfma32(as_vec8<vec8>(ld16(do_s + 32 * qs * DV + doo.row_at(kk))), vreg[kk], dp);
       // Partial sub-tile (some key of the wave masked, or on the causal diagonal): masked
       // scores become -inf so that P = 0.
       if (!wave_vis || (p.causal && i0 + 32 * qs < kw0 + 31)) {
@@ -349,10 +344,10 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
         const int r0 = 32 * qs + 16 * g2;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
-          dva[db] = T::mfma32(ap, as_vec8<vec8>(lds_tr8(do_s + r0 * DV, dtr_lo[db], dtr_hi[db])), dva[db]);
+          dva[db] = T::mfma32(ap, as_vec8<vec8>(lds_tr8(do_s + r0 * DV, doo.lo_at(db), doo.hi_at(db))), dva[db]);
 #pragma unroll
         for (int eb = 0; eb < EB; ++eb)
-          dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_tr8(qh_s + r0 * EP, qtr_lo[eb], qtr_hi[eb])), dka[eb]);
+          dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_tr8(qh_s + r0 * EP, qo.lo_at(eb), qo.hi_at(eb))), dka[eb]);
       }
     }
   }
@@ -473,46 +468,43 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
   const uint16_t* kh_g = p.kh + (int64_t)bhk * NkP * EP;
   const uint16_t* v_g = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
   const int vs2 = (int)p.v_s[2];
-  int ld_r[C::Q_LPT], ld_c[C::Q_LPT];
+  // one offset per load: K_hat element offset in the tile; V element offset of (row, column)
+  // relative to the tile's first row (rows past Nk clamp to the last chunk of the last row: P = 0 there)
+  int ld_o[C::Q_LPT];
 #pragma unroll
   for (int m = 0; m < C::Q_LPT; ++m) {
     const int c = m * kThreads + tid;
     if (c < XU) {
       const int r = c / EPU;
-      ld_r[m] = r;
-      ld_c[m] = 8 * ((c % EPU) ^ tile_swz(EPU, r));
+      ld_o[m] = r * EP + 8 * ((c % EPU) ^ tile_swz(EPU, r));
     } else {
       const int r = (c - XU) / DVU;
-      ld_r[m] = r;
-      ld_c[m] = min(8 * (((c - XU) % DVU) ^ tile_swz(DVU, r)), D - 8);
+      ld_o[m] = r * vs2 + min(8 * (((c - XU) % DVU) ^ tile_swz(DVU, r)), D - 8);
     }
   }
+  const int v_last = (Nk - 1) * vs2 + D - 8;   // start of the last chunk of the last row
   auto issue = [&](int kt) {
     const int j0 = kt * BN;
     char* slot = smem + (kt % kSlots) * C::SLOT;
     const uint16_t* kg = kh_g + j0 * EP;   // K_hat rows are padded to NkP
+    const int vrow0 = j0 * vs2;
 #pragma unroll
     for (int m = 0; m < C::Q_LPT; ++m) {
       const int c0 = m * kThreads + wave * 64;
       const uint32_t dst = lds_addr(slot + c0 * 16);
-      const uint16_t* vsrc = v_g + min(j0 + ld_r[m], Nk - 1) * vs2 + ld_c[m];
+      const uint16_t* vsrc = v_g + min(vrow0 + ld_o[m], v_last);
       if ((m + 1) * kThreads <= XU) {
-        load_lds16(kg + ld_r[m] * EP + ld_c[m], dst);
+        load_lds16(kg + ld_o[m], dst);
       } else if (m * kThreads >= XU) {
         if (UNITS % kThreads == 0 || c0 < UNITS) load_lds16(vsrc, dst);
       } else {
-        load_lds16(c0 < XU ? (const void*)(kg + ld_r[m] * EP + ld_c[m]) : (const void*)vsrc, dst);
+        load_lds16(c0 < XU ? (const void*)(kg + ld_o[m]) : (const void*)vsrc, dst);
       }
     }
   };
 
-  int krow[KS], vrow[DS], ktr_lo[EB], ktr_hi[EB];
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) krow[kk] = row_offset<EPU>(lane, kk);
-#pragma unroll
-  for (int kk = 0; kk < DS; ++kk) vrow[kk] = row_offset<DVU>(lane, kk);
-#pragma unroll
-  for (int eb = 0; eb < EB; ++eb) tr_offsets<EPU>(lane, eb, ktr_lo[eb], ktr_hi[eb]);
+  const TileOffsets<EPU> ko(lane);
+  const TileOffsets<DVU> vo(lane);
 
   if (nt > 0) issue(0);
   if (nt > 1) issue(1);
@@ -535,10 +527,10 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
       f32x16 s = nlc, dp = ndc;
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk)
-        s = T::mfma32(as_vec8<vec8>(ld16(kh_s + 32 * ks * EP + krow[kk])), qreg[kk], s);
+        s = T::mfma32(as_vec8<vec8>(ld16(kh_s + 32 * ks * EP + ko.row_at(kk))), qreg[kk], s);
 #pragma unroll
       for (int kk = 0; kk < DS; ++kk)
-        dp = T::mfma32(as_vec8<vec8>(ld16(v_s + 32 * ks * DV + vrow[kk])), doreg[kk], dp);
+        dp = T::mfma32(as_vec8<vec8>(ld16(v_s + 32 * ks * DV + vo.row_at(kk))), doreg[kk], dp);
       if (!full) {   // masked scores -> -inf: P = 0
         POPE_COLD_PATH();
         const uint64_t w = mb >> (32 * ks + 4 * hf);
@@ -557,7 +549,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
         const uint16_t* kr0 = kh_s + (32 * ks + 16 * g2) * EP;
 #pragma unroll
         for (int eb = 0; eb < EB; ++eb)
-          dqa[eb] = T::mfma32(as_vec8<vec8>(lds_tr8(kr0, ktr_lo[eb], ktr_hi[eb])), bds, dqa[eb]);
+          dqa[eb] = T::mfma32(as_vec8<vec8>(lds_tr8(kr0, ko.lo_at(eb), ko.hi_at(eb))), bds, dqa[eb]);
       }
     }
   }

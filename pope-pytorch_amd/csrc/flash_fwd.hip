@@ -115,60 +115,48 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   const uint16_t* khg = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;
   const uint16_t* vg = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
   const int vs2 = (int)p.v_s[2];
-  int ld_row[C::LPT], ld_col[C::LPT];
+  // one offset per load: K_hat element offset relative to the pair's first row; V element
+  // offset of (row, column) relative to the pair's first row (rows past Nk clamp to the last
+  // chunk of the last row: their P is 0; columns past D repeat the last chunk and are never stored)
+  int ld_o[C::LPT];
 #pragma unroll
   for (int m = 0; m < C::LPT; ++m) {
     const int c = m * kThreads + tid;
     if (c < C::KUNITS) {
       const int g = c / (BN * C::EPU), rem = c % (BN * C::EPU);
       const int r = rem / C::EPU, u = (rem % C::EPU) ^ tile_swz(C::EPU, r);
-      ld_row[m] = g * BN + r;
-      ld_col[m] = 8 * u;
+      ld_o[m] = (g * BN + r) * EP + 8 * u;
     } else {
       const int cv = c - C::KUNITS;
       const int g = cv / (BN * C::DVU), rem = cv % (BN * C::DVU);
       const int r = rem / C::DVU, u = (rem % C::DVU) ^ tile_swz(C::DVU, r);
-      ld_row[m] = g * BN + r;
-      ld_col[m] = min(8 * u, D - 8);   // columns past D repeat the last chunk (never stored)
+      ld_o[m] = (g * BN + r) * vs2 + min(8 * u, D - 8);
     }
   }
+  const int v_last = (Nk - 1) * vs2 + D - 8;   // start of the last chunk of the last row
   auto issue = [&](int pr) {
     char* slot = smem + (pr % kStages) * C::STAGE;
     const int j0 = pr * 2 * BN;
     const uint16_t* kp = khg + j0 * EP;   // K_hat rows are padded to NkP: no clamp
+    const int vrow0 = j0 * vs2;
 #pragma unroll
     for (int m = 0; m < C::LPT; ++m) {
       const int c0 = m * kThreads + wave * 64;   // first unit of this wave's instruction
       const uint32_t dst = lds_addr(slot + c0 * 16);
-      const uint16_t* vsrc = vg + min(j0 + ld_row[m], Nk - 1) * vs2 + ld_col[m];
+      const uint16_t* vsrc = vg + min(vrow0 + ld_o[m], v_last);
       if ((m + 1) * kThreads <= C::KUNITS) {          // K_hat units for every wave
-        load_lds16(kp + ld_row[m] * EP + ld_col[m], dst);
+        load_lds16(kp + ld_o[m], dst);
       } else if (m * kThreads >= C::KUNITS) {         // V units
         if (C::UNITS % kThreads == 0 || c0 < C::UNITS) load_lds16(vsrc, dst);
       } else {                                        // the K / V boundary falls in this load
-        load_lds16(c0 < C::KUNITS ? (const void*)(kp + ld_row[m] * EP + ld_col[m]) : (const void*)vsrc, dst);
+        load_lds16(c0 < C::KUNITS ? (const void*)(kp + ld_o[m]) : (const void*)vsrc, dst);
       }
     }
   };
 
-  // ---- LDS operand addressing -------------------------------------------------------
-  // K_hat A operand: row 32 kb + lr, unit 2 kk + hf of tile grp.
-  int koff[KS];
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) koff[kk] = lr * EP + 8 * ((2 * kk + hf) ^ tile_swz(C::EPU, lr));
-  // V^T A operand (transpose read): rows R0 + 4 h + j / 4 and R0 + 8 + 4 h + j / 4, columns
-  // n0 + 8 u + 4 (j & 1) with u = 2 (gi & 1) + ((j >> 1) & 1) inside the 4-unit group at n0.
-  int voff_lo[NDB], voff_hi[NDB];
-  {
-    const int j = lane & 15, gi = lane >> 4;
-    const int u = 2 * (gi & 1) + ((j >> 1) & 1), sub = 4 * (j & 1);
-    const int rlo = 4 * hf + (j >> 2), rhi = rlo + 8;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      voff_lo[db] = rlo * DV + 8 * ((4 * db + u) ^ tile_swz(C::DVU, rlo)) + sub;
-      voff_hi[db] = rhi * DV + 8 * ((4 * db + u) ^ tile_swz(C::DVU, rhi)) + sub;
-    }
-  }
+  // K_hat A operand: row 32 kb + lr, unit 2 kk + hf of tile grp; V^T A operand: transpose reads
+  const TileOffsets<C::EPU> ko(lane);
+  const TileOffsets<C::DVU> vo(lane);
 
   // ---- state -----------------------------------------------------------------------------
   f32x16 oacc[NDB];
@@ -223,10 +211,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
     const uint16_t* kt = kh_tile(pr);
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-      s[kb] = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt + 32 * kb * EP + koff[0])), qreg[0], negm);
+      s[kb] = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt + 32 * kb * EP + ko.row_at(0))), qreg[0], negm);
 #pragma unroll
       for (int kk = 1; kk < KS; ++kk)
-        s[kb] = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt + 32 * kb * EP + koff[kk])), qreg[kk], s[kb]);
+        s[kb] = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt + 32 * kb * EP + ko.row_at(kk))), qreg[kk], s[kb]);
     }
   };
   auto rowmax = [&](const f32x16* s) -> float {
@@ -284,9 +272,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
       const vec8 pb = as_vec8<vec8>(pw[g16]);
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const u32x2 lo = lds_read_tr16(vt + 16 * g16 * DV + voff_lo[db]);
-        const u32x2 hi = lds_read_tr16(vt + 16 * g16 * DV + voff_hi[db]);
-        oacc[db] = T::mfma32(as_vec8<vec8>(u32x4{lo[0], lo[1], hi[0], hi[1]}), pb, oacc[db]);
+        oacc[db] = T::mfma32(as_vec8<vec8>(lds_tr8(vt + 16 * g16 * DV, vo.lo_at(db), vo.hi_at(db))), pb, oacc[db]);
       }
     }
   };

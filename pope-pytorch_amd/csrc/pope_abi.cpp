@@ -141,6 +141,16 @@ FlashLayout flash_layout(const pope_desc& d) {
 
 size_t flash_ws(const pope_desc& d, int) { return flash_layout(d).total; }
 
+// The flash kernels address the rows of v and do inside one (batch, head) with 32-bit element
+// offsets, up to one tile past the padded length.
+int check_row_span(const char* name, int rows_padded, int64_t row_stride) {
+  const int64_t span = ((int64_t)rows_padded + 128) * row_stride;
+  if (span >= ((int64_t)1 << 31))
+    return fail(POPE_ERR_UNSUPPORTED, "%s rows span %lld elements per (batch, head); the kernels index them "
+                "with 32-bit offsets", name, (long long)span);
+  return POPE_OK;
+}
+
 // Launches the shared preparation of the flash forward and backward into the workspace.
 hipError_t flash_prepare(const pope_desc& d, const FlashLayout& L, const void* q, const void* k,
                          const float* freqs, const float* bias, const uint8_t* mask, char* ws, hipStream_t s) {
@@ -356,9 +366,7 @@ int pope_flash_fwd(const pope_desc* d, const void* q, const void* k, const void*
   if (rc) return rc;
   const FlashLayout L = flash_layout(*d);
   if ((rc = check_ws(L.total, workspace, workspace_bytes))) return rc;
-  if ((int64_t)d->Nk * d->v_s[2] >= ((int64_t)1 << 31))
-    return fail(POPE_ERR_UNSUPPORTED, "v rows span %lld elements per (batch, head); the kernels index them "
-                "with 32-bit offsets", (long long)((int64_t)d->Nk * d->v_s[2]));
+  if ((rc = check_row_span("v", L.NkP, d->v_s[2]))) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   hipError_t e = flash_prepare(*d, L, q, k, freqs, bias, mask, ws, s);
@@ -402,6 +410,7 @@ int pope_flash_bwd(const pope_desc* d, const void* dout, const void* q, const vo
     return fail(POPE_ERR_INVALID, "unknown flags 0x%x", (unsigned)d->flags);
   const FlashLayout L = flash_layout(*d);
   if ((rc = check_ws(L.total, workspace, workspace_bytes))) return rc;
+  if ((rc = check_row_span("v", L.NkP, d->v_s[2])) || (rc = check_row_span("do", L.NqP, d->do_s[2]))) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   if (!(d->flags & POPE_FLAG_PREPARED)) {

@@ -196,28 +196,42 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Instruction-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedDsRead = 0x100;
 
-// Element offsets, inside a row-major tile of U 16-byte units per row stored with tile_swz, of
-// the two 4-element chunks a lane reads for an 8-element MFMA operand taken transposed
-// (lds_read_tr16): rows R0 + 4 h + j / 4 and R0 + 8 + 4 h + j / 4, columns n0 + 8 u + 4 (j & 1)
-// with j = lane % 16, h = lane / 32, u = 2 (lane / 16 % 2) + (j / 2 % 2), relative to R0 = 0 and
-// the 32-column block n0 = 32 nb.  The operand's k order (rows) is the register order of a
-// 32x32 MFMA result read back as an operand: [4 h, 4 h + 4) then [8 + 4 h, 12 + 4 h).
-template <int U>
-__device__ __forceinline__ void tr_offsets(int lane, int nb, int& lo, int& hi) {
-  const int j = lane & 15, gi = lane >> 4;
-  const int u = 2 * (gi & 1) + ((j >> 1) & 1), sub = 4 * (j & 1);
-  const int rlo = 4 * (lane >> 5) + (j >> 2), rhi = rlo + 8;
-  lo = rlo * 8 * U + 8 * ((4 * nb + u) ^ tile_swz(U, rlo)) + sub;
-  hi = rhi * 8 * U + 8 * ((4 * nb + u) ^ tile_swz(U, rhi)) + sub;
-}
+// Number of distinct low-bit patterns tile_swz can flip: swizzle values stay below 4 (U % 16 in
+// {4, 12}), 8 (U % 16 == 8) or 16 (U % 16 == 0).
+__host__ __device__ constexpr int swz_bits(int U) { return U % 16 == 0 ? 4 : U % 8 == 0 ? 3 : 2; }
 
-// Element offset of the 8-element operand chunk a lane reads by rows: row lane % 32, unit
-// 2 kk + lane / 32 of a tile of U units per row stored with tile_swz.
+// Operand offsets (elements) of the MFMA reads of a row-major tile of U 16-byte units per row
+// stored with tile_swz.  The swizzle only flips the low swz_bits(U) bits of a unit index, so
+// the lane-dependent part repeats with a short period and a few base registers serve every
+// k step / column block:
+//   row read   lane % 32 reads row lane % 32, unit 2 kk + lane / 32        (ds_read_b128)
+//   transpose  rows R0 + 4 h + j / 4 and R0 + 8 + 4 h + j / 4, columns 32 nb + 8 u + 4 (j & 1),
+//              j = lane % 16, h = lane / 32, u = 2 (lane / 16 % 2) + (j / 2 % 2)
+//              (two lds_read_tr16 chunks; the k order is the register order of a 32x32 MFMA
+//              result read back as an operand: [4 h, 4 h + 4) then [8 + 4 h, 12 + 4 h))
 template <int U>
-__device__ __forceinline__ int row_offset(int lane, int kk) {
-  const int lr = lane & 31;
-  return lr * 8 * U + 8 * ((2 * kk + (lane >> 5)) ^ tile_swz(U, lr));
-}
+struct TileOffsets {
+  static constexpr int RP = 1 << (swz_bits(U) - 1);   // period of the row-read offset in kk
+  static constexpr int TP = 1 << (swz_bits(U) - 2);   // period of the transpose offset in nb
+  int row[RP], lo[TP], hi[TP];
+  __device__ __forceinline__ explicit TileOffsets(int lane) {
+    const int lr = lane & 31, hf = lane >> 5;
+#pragma unroll
+    for (int k = 0; k < RP; ++k) row[k] = lr * 8 * U + 8 * ((2 * k + hf) ^ tile_swz(U, lr));
+    const int j = lane & 15, gi = lane >> 4;
+    const int u = 2 * (gi & 1) + ((j >> 1) & 1), sub = 4 * (j & 1);
+    const int rlo = 4 * hf + (j >> 2), rhi = rlo + 8;
+#pragma unroll
+    for (int nb = 0; nb < TP; ++nb) {
+      lo[nb] = rlo * 8 * U + 8 * ((4 * nb + u) ^ tile_swz(U, rlo)) + sub;
+      hi[nb] = rhi * 8 * U + 8 * ((4 * nb + u) ^ tile_swz(U, rhi)) + sub;
+    }
+  }
+  // row read of k step kk (compile-time kk: the base index and the added constant fold)
+  __device__ __forceinline__ int row_at(int kk) const { return row[kk % RP] + 16 * (kk - kk % RP); }
+  __device__ __forceinline__ int lo_at(int nb) const { return lo[nb % TP] + 32 * (nb - nb % TP); }
+  __device__ __forceinline__ int hi_at(int nb) const { return hi[nb % TP] + 32 * (nb - nb % TP); }
+};
 
 // 8-element operand from the two transposed chunks at lo and hi.
 __device__ __forceinline__ u32x4 lds_tr8(const uint16_t* base, int lo, int hi) {
