@@ -50,6 +50,8 @@
 // other operand of such a product is read from a row-major LDS tile with
 // ds_read_b64_tr_b16 in the same row order (lds_operand_tr), so no transposed
 // copy of any tile is ever stored.
+#include <type_traits>
+
 #include "pope_common.hpp"
 #include "pope_kernels.hpp"
 
@@ -65,6 +67,19 @@ __device__ __forceinline__ u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
 
 typedef const __attribute__((address_space(4))) uint64_t cu64;
 typedef const __attribute__((address_space(4))) int ci32;
+
+// Calls f(std::integral_constant<int, n>) for the runtime n in [0, N]: register arrays indexed
+// by n stay statically indexed.
+template <int N, typename F>
+__device__ __forceinline__ void with_const(int n, F&& f) {
+  if constexpr (N >= 0) {
+    if (n == N) {
+      f(std::integral_constant<int, N>{});
+      return;
+    }
+    with_const<N - 1>(n, f);
+  }
+}
 
 // Registers [8 g, 8 g + 8) of an MFMA result, packed as an 8-element operand.
 template <typename T>
@@ -207,6 +222,7 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
       vreg[kk] = as_vec8<vec8>((kj < Nk && d0 < D) ? ld16(vr + d0) : zero4());
     }
   }
+  settle_vector_loads();
 
   f32x16 dva[DB], dka[EB];
 #pragma unroll
@@ -367,40 +383,92 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
     }
   }
 
-  // ---- dK: key-side chain rule, one wave's 32 keys at a time through LDS -------
-  constexpr int BS = EP + 1;
-  float* ebuf = reinterpret_cast<float*>(smem);
+  // ---- dK: key-side chain rule ---------------------------------------------------
+  // dka lane lr of block eb holds column e = 32 eb + lr of dK_hat for the wave's 16 keys
+  // 8 (r >> 2) + 4 hf + (r & 3).  With R a multiple of 32 the cos column of dim d < R (e = d)
+  // and its sin column (e = R + d) sit in the same lane, blocks eb and eb + R / 32, and a
+  // pass-through dim d >= R (e = R + d) in block (R + d) / 32: the chain rule runs on the
+  // registers, with every load of the lane issued before the arithmetic.
   const uint16_t* kb_ptr = p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1];
   uint16_t* dkb = p.dk + (int64_t)b * p.dk_s[0] + (int64_t)hk * p.dk_s[1];
   const float2* tb = R ? p.table + (int64_t)b * p.t_sb + (int64_t)hk * p.t_sh : nullptr;
   float* dfb = p.dfreqs ? p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)hk * p.df_s[1] : nullptr;
-  for (int w = 0; w < 4; ++w) {
-    __syncthreads();
-    if (wave == w) {
+  if (R % 32 == 0) {
+    auto key_of = [&](int r) { return kw0 + 8 * (r >> 2) + 4 * hf + (r & 3); };
+    with_const<EP / 64>(R / 32, [&](auto rbc) {   // rotated blocks: R / 32 <= EP / 64
+    constexpr int RB = decltype(rbc)::value;
 #pragma unroll
-      for (int eb = 0; eb < EB; ++eb)
+    for (int rb = 0; rb < RB; ++rb) {
+      const int d = 32 * rb + lr;
+      float x[16];
+      float2 cs[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ebuf[(8 * (r >> 2) + 4 * hf + (r & 3)) * BS + 32 * eb + lr] = dka[eb][r];
-    }
-    __syncthreads();
-    for (int it = tid; it < 32 * D; it += kThreads) {
-      const int kr = it / D, d = it - kr * D;
-      const int key = j0 + 32 * w + kr;
-      if (key >= Nk) continue;
-      const float* row = ebuf + kr * BS;
-      float g;
-      if (d < R) {
-        const float x = T::to_float(kb_ptr[(int64_t)key * p.k_s[2] + d]);
-        const float2 cs = tb[(int64_t)key * R + d];
-        const float uc = row[d] * kLn2, us = row[R + d] * kLn2;
-        g = sigmoid_f(x) * (cs.x * uc + cs.y * us);
-        const float dpsi = softplus_f(x) * (cs.x * us - cs.y * uc);
-        if (dfb) atomicAdd(dfb + (int64_t)key * p.df_s[2] + d, dpsi);
-        if (p.dbias) atomicAdd(&dbias_s[d], dpsi);
-      } else {
-        g = row[R + d] * kLn2;
+      for (int r = 0; r < 16; ++r) {
+        const int key = min(key_of(r), Nk - 1);
+        x[r] = T::to_float(kb_ptr[(int64_t)key * p.k_s[2] + d]);
+        cs[r] = tb[(int64_t)key * R + d];
       }
-      dkb[(int64_t)key * p.dk_s[2] + d] = T::bits(g);
+      float dsum = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float uc = dka[rb][r] * kLn2, us = dka[rb + RB][r] * kLn2;
+        const float g = sigmoid_f(x[r]) * (cs[r].x * uc + cs[r].y * us);
+        const float dpsi = softplus_f(x[r]) * (cs[r].x * us - cs[r].y * uc);
+        const int key = key_of(r);
+        if (key < Nk) {
+          dkb[(int64_t)key * p.dk_s[2] + d] = T::bits(g);
+          if (dfb) atomicAdd(dfb + (int64_t)key * p.df_s[2] + d, dpsi);
+          dsum += dpsi;
+        }
+      }
+      if (p.dbias) {
+        dsum += wave_shfl_xor(dsum, 32);
+        if (hf == 0) atomicAdd(&dbias_s[d], dsum);
+      }
+    }
+#pragma unroll
+    for (int eb = 2 * RB; eb < EB; ++eb) {   // pass-through dims
+      const int d = 32 * eb + lr - R;
+      if (d >= D) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = key_of(r);
+        if (key < Nk) dkb[(int64_t)key * p.dk_s[2] + d] = T::bits(dka[eb][r] * kLn2);
+      }
+    }
+    });
+  } else {
+    // general rotate dim: one wave's 32 keys at a time through LDS
+    constexpr int BS = EP + 1;
+    float* ebuf = reinterpret_cast<float*>(smem);
+    for (int w = 0; w < 4; ++w) {
+      __syncthreads();
+      if (wave == w) {
+  #pragma unroll
+        for (int eb = 0; eb < EB; ++eb)
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) ebuf[(8 * (r >> 2) + 4 * hf + (r & 3)) * BS + 32 * eb + lr] = dka[eb][r];
+      }
+      __syncthreads();
+      for (int it = tid; it < 32 * D; it += kThreads) {
+        const int kr = it / D, d = it - kr * D;
+        const int key = j0 + 32 * w + kr;
+        if (key >= Nk) continue;
+        const float* row = ebuf + kr * BS;
+        float g;
+        if (d < R) {
+          const float x = T::to_float(kb_ptr[(int64_t)key * p.k_s[2] + d]);
+          const float2 cs = tb[(int64_t)key * R + d];
+          const float uc = row[d] * kLn2, us = row[R + d] * kLn2;
+          g = sigmoid_f(x) * (cs.x * uc + cs.y * us);
+          const float dpsi = softplus_f(x) * (cs.x * us - cs.y * uc);
+          if (dfb) atomicAdd(dfb + (int64_t)key * p.df_s[2] + d, dpsi);
+          if (p.dbias) atomicAdd(&dbias_s[d], dpsi);
+        } else {
+          g = row[R + d] * kLn2;
+        }
+        dkb[(int64_t)key * p.dk_s[2] + d] = T::bits(g);
+      }
     }
   }
   if (p.dbias) {
@@ -452,6 +520,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
       ndc[r] = d;
     }
   }
+  settle_vector_loads();
 
   f32x16 dqa[EB];
 #pragma unroll
@@ -555,41 +624,105 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
   }
   __syncthreads();   // every wave is done with the slots
 
-  // ---- dQ: query-side chain rule, one wave's 32 queries at a time through LDS ----
-  constexpr int BS = EP + 1;
-  float* ebuf = reinterpret_cast<float*>(smem);
+  // ---- dQ: query-side chain rule --------------------------------------------------
+  // dqa lane (query qi, hf) of block eb holds rows e = 32 eb + 8 (r >> 2) + 4 hf + (r & 3) of
+  // dQ_hat^T: with R a multiple of 32, dim d < R has its cos row (e = d) and sin row (e = R + d)
+  // in blocks eb and eb + R / 32 at the same register, and pass-through dims d >= R (e = R + d)
+  // fill the later blocks.  Each register group of 4 covers 4 consecutive dims.
   const uint16_t* qb_ptr = p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1];
   uint16_t* dqb = p.dq + (int64_t)b * p.dq_s[0] + (int64_t)h * p.dq_s[1];
   const float2* tq = R ? p.table + (int64_t)b * p.t_sb + (int64_t)h * p.t_sh : nullptr;
   const float2* bq = R ? p.btab + (p.Hb > 1 ? hk : 0) * R : nullptr;
   float* dfb = p.dfreqs ? p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)h * p.df_s[1] : nullptr;
-  for (int w = 0; w < 4; ++w) {
-    __syncthreads();
-    if (wave == w) {
+  if (R % 32 == 0) {
+    if (qi < Nq) {
+      uint16_t* dqrow = dqb + (int64_t)qi * p.dq_s[2];
+      with_const<EP / 64>(R / 32, [&](auto rbc) {   // rotated blocks: R / 32 <= EP / 64
+      constexpr int RB = decltype(rbc)::value;
 #pragma unroll
-      for (int eb = 0; eb < EB; ++eb)
+      for (int rb = 0; rb < RB; ++rb) {
+        float x[16];
+        float2 tf[16], tbv[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ebuf[lr * BS + 32 * eb + 8 * (r >> 2) + 4 * hf + (r & 3)] = dqa[eb][r];
-    }
-    __syncthreads();
-    for (int it = tid; it < 32 * D; it += kThreads) {
-      const int qr = it / D, d = it - qr * D;
-      const int i = qb * 128 + 32 * w + qr;
-      if (i >= Nq) continue;
-      const float* row = ebuf + qr * BS;
-      float g;
-      if (d < R) {
-        const float x = T::to_float(qb_ptr[(int64_t)i * p.q_s[2] + d]);
-        // cos / sin(F[q_off + i] - bias) from the tables of F and of the bias
-        const float2 tf = tq[(int64_t)(q_off + i) * R + d], tb = bq[d];
-        const float cs = fmaf(tf.x, tb.x, tf.y * tb.y), sn = fmaf(tf.y, tb.x, -tf.x * tb.y);
-        const float uc = row[d] * p.scale, us = row[R + d] * p.scale;
-        g = sigmoid_f(x) * (cs * uc + sn * us);
-        if (dfb) atomicAdd(dfb + (int64_t)(q_off + i) * p.df_s[2] + d, softplus_f(x) * (cs * us - sn * uc));
-      } else {
-        g = row[R + d] * p.scale;
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = 32 * rb + 8 * g + 4 * hf;
+          const u32x2 raw = *reinterpret_cast<const u32x2*>(qb_ptr + (int64_t)qi * p.q_s[2] + d0);
+          x[4 * g] = T::to_float((uint16_t)u16lo(raw[0]));
+          x[4 * g + 1] = T::to_float((uint16_t)u16hi(raw[0]));
+          x[4 * g + 2] = T::to_float((uint16_t)u16lo(raw[1]));
+          x[4 * g + 3] = T::to_float((uint16_t)u16hi(raw[1]));
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            tf[4 * g + c] = tq[(int64_t)(q_off + qi) * R + d0 + c];
+            tbv[4 * g + c] = bq[d0 + c];
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = 32 * rb + 8 * g + 4 * hf;
+          float out[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int r = 4 * g + c;
+            // cos / sin(F[q_off + i] - bias) from the tables of F and of the bias
+            const float cs = fmaf(tf[r].x, tbv[r].x, tf[r].y * tbv[r].y);
+            const float sn = fmaf(tf[r].y, tbv[r].x, -tf[r].x * tbv[r].y);
+            const float uc = dqa[rb][r] * p.scale, us = dqa[rb + RB][r] * p.scale;
+            out[c] = sigmoid_f(x[r]) * (cs * uc + sn * us);
+            if (dfb) atomicAdd(dfb + (int64_t)(q_off + qi) * p.df_s[2] + d0 + c, softplus_f(x[r]) * (cs * us - sn * uc));
+          }
+          u32x2 w;
+          w[0] = T::pack2(out[0], out[1]);
+          w[1] = T::pack2(out[2], out[3]);
+          *reinterpret_cast<u32x2*>(dqrow + d0) = w;
+        }
       }
-      dqb[(int64_t)i * p.dq_s[2] + d] = T::bits(g);
+#pragma unroll
+      for (int eb = 2 * RB; eb < EB; ++eb) {   // pass-through dims
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = 32 * eb + 8 * g + 4 * hf - R;
+          if (d0 >= D) continue;
+          u32x2 w;
+          w[0] = T::pack2(dqa[eb][4 * g] * p.scale, dqa[eb][4 * g + 1] * p.scale);
+          w[1] = T::pack2(dqa[eb][4 * g + 2] * p.scale, dqa[eb][4 * g + 3] * p.scale);
+          *reinterpret_cast<u32x2*>(dqrow + d0) = w;
+        }
+      }
+      });
+    }
+  } else {
+    // general rotate dim: one wave's 32 queries at a time through LDS
+    constexpr int BS = EP + 1;
+    float* ebuf = reinterpret_cast<float*>(smem);
+    for (int w = 0; w < 4; ++w) {
+      __syncthreads();
+      if (wave == w) {
+  #pragma unroll
+        for (int eb = 0; eb < EB; ++eb)
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) ebuf[lr * BS + 32 * eb + 8 * (r >> 2) + 4 * hf + (r & 3)] = dqa[eb][r];
+      }
+      __syncthreads();
+      for (int it = tid; it < 32 * D; it += kThreads) {
+        const int qr = it / D, d = it - qr * D;
+        const int i = qb * 128 + 32 * w + qr;
+        if (i >= Nq) continue;
+        const float* row = ebuf + qr * BS;
+        float g;
+        if (d < R) {
+          const float x = T::to_float(qb_ptr[(int64_t)i * p.q_s[2] + d]);
+          // cos / sin(F[q_off + i] - bias) from the tables of F and of the bias
+          const float2 tf = tq[(int64_t)(q_off + i) * R + d], tb = bq[d];
+          const float cs = fmaf(tf.x, tb.x, tf.y * tb.y), sn = fmaf(tf.y, tb.x, -tf.x * tb.y);
+          const float uc = row[d] * p.scale, us = row[R + d] * p.scale;
+          g = sigmoid_f(x) * (cs * uc + sn * us);
+          if (dfb) atomicAdd(dfb + (int64_t)(q_off + i) * p.df_s[2] + d, softplus_f(x) * (cs * us - sn * uc));
+        } else {
+          g = row[R + d] * p.scale;
+        }
+        dqb[(int64_t)i * p.dq_s[2] + d] = T::bits(g);
+      }
     }
   }
 }

@@ -97,6 +97,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) qreg[kk] = as_vec8<vec8>(ld16(qrow + 16 * kk + 8 * hf));
   }
+  settle_vector_loads();
 
   // ---- key range: causal bound of the block's last query, last visible key of the batch ----
   // (the preparation's words and bounds are read-only here: the constant address space lets

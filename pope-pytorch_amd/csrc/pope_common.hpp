@@ -193,6 +193,11 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Waits until at most n of this thread's vector memory loads are outstanding.
 #define POPE_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
 
+// Waits for every outstanding vector memory load, as an instruction the compiler's own wait
+// insertion accounts for: registers loaded before it count as ready afterwards, so no later
+// use of them (inside a loop that also has direct-to-LDS loads in flight) adds a vmcnt(0).
+__device__ __forceinline__ void settle_vector_loads() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
 // Instruction-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedDsRead = 0x100;
 
