@@ -59,7 +59,6 @@ namespace pope {
 
 namespace {
 
-constexpr int kThreads = 256;
 constexpr int kSlots = 3;
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
@@ -93,7 +92,7 @@ __device__ __forceinline__ u32x4 pack8(const f32x16& x, int g) {
 // Waits until at most n of this thread's vector loads are outstanding (n a compile-time count).
 template <int n>
 __device__ __forceinline__ void wait_vmcnt() {
-  static_assert(n >= 0 && n <= 8, "wait count");
+  static_assert(n >= 0 && n <= 15, "wait count");
   if (n == 0) POPE_WAIT_VMCNT(0);
   else if (n == 1) POPE_WAIT_VMCNT(1);
   else if (n == 2) POPE_WAIT_VMCNT(2);
@@ -102,7 +101,14 @@ __device__ __forceinline__ void wait_vmcnt() {
   else if (n == 5) POPE_WAIT_VMCNT(5);
   else if (n == 6) POPE_WAIT_VMCNT(6);
   else if (n == 7) POPE_WAIT_VMCNT(7);
-  else POPE_WAIT_VMCNT(8);
+  else if (n == 8) POPE_WAIT_VMCNT(8);
+  else if (n == 9) POPE_WAIT_VMCNT(9);
+  else if (n == 10) POPE_WAIT_VMCNT(10);
+  else if (n == 11) POPE_WAIT_VMCNT(11);
+  else if (n == 12) POPE_WAIT_VMCNT(12);
+  else if (n == 13) POPE_WAIT_VMCNT(13);
+  else if (n == 14) POPE_WAIT_VMCNT(14);
+  else if (n == 15) POPE_WAIT_VMCNT(15);
 }
 
 // ---------------------------------------------------------------------------
@@ -164,9 +170,14 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(FlashBwdParams p) {
 // ---------------------------------------------------------------------------
 template <int EP, int DV>
 struct BwdCfg {
+  // Small rows: 8 waves (256 keys per dK/dV job, 256 queries per dQ job) and 128-row steps, one
+  // workgroup per CU (two waves per SIMD).  Wide rows need up to 512 registers per lane: 4 waves,
+  // one per SIMD, 64-row steps.
   static constexpr bool kBig = EP + DV > 160;
-  static constexpr int BM = kBig ? 32 : 64;    // query rows per dK/dV step, keys per dQ step
-  static constexpr int MINB = kBig ? 1 : 2;
+  static constexpr int NW = kBig ? 4 : 8;                    // waves per workgroup
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int JOB = 32 * NW;                        // keys (dK/dV) or queries (dQ) per job
+  static constexpr int BM = kBig ? 64 : 128;                 // query rows per dK/dV step, keys per dQ step
   static constexpr int KS = EP / 16, DS = DV / 16, EB = EP / 32, DB = DV / 32;
   static constexpr int EPU = EP / 8, DVU = DV / 8;
   static constexpr int XT = BM * EP, YT = BM * DV;            // elements of the two tiles of a slot
@@ -175,13 +186,14 @@ struct BwdCfg {
   static constexpr int KV_UNITS = XU + YU + LU, Q_UNITS = XU + YU;
   static constexpr int SLOT = KV_UNITS * 16;
   // loads per thread per step, and the count every wave issues (the last load can be partial)
-  static constexpr int KV_LPT = (KV_UNITS + kThreads - 1) / kThreads;
-  static constexpr int Q_LPT = (Q_UNITS + kThreads - 1) / kThreads;
-  static constexpr int KV_LMIN = (KV_UNITS - 192 + kThreads - 1) / kThreads;   // loads of wave 3
-  static constexpr int Q_LMIN = (Q_UNITS - 192 + kThreads - 1) / kThreads;
+  static constexpr int KV_LPT = (KV_UNITS + THREADS - 1) / THREADS;
+  static constexpr int Q_LPT = (Q_UNITS + THREADS - 1) / THREADS;
+  static constexpr int KV_LMIN = (KV_UNITS - (THREADS - 64) + THREADS - 1) / THREADS;   // loads of the last wave
+  static constexpr int Q_LMIN = (Q_UNITS - (THREADS - 64) + THREADS - 1) / THREADS;
   static constexpr int EPI = 32 * (EP + 1) * 4;
   static constexpr int LDS = kSlots * SLOT > EPI ? kSlots * SLOT : EPI;
   static_assert(XU % 64 == 0 && YU % 64 == 0, "tile regions must split at wave boundaries");
+  static_assert(LDS <= 160 * 1024, "LDS budget");
 };
 
 // dK / dV job.  Lane lr of wave w owns key j0 + 32 w + lr.
@@ -195,13 +207,14 @@ template <typename T, int EP, int DV>
 __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, float* dbias_s, int kb, int bhk) {
   typedef BwdCfg<EP, DV> C;
   constexpr int BM = C::BM, KS = C::KS, DS = C::DS, EB = C::EB, DB = C::DB, QB = BM / 32;
+  constexpr int kThreads = C::THREADS;
   constexpr int EPU = C::EPU, DVU = C::DVU, XU = C::XU, YU = C::YU, UNITS = C::KV_UNITS;
   typedef typename T::vec8 vec8;
 
   const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int b = bhk / p.Hk, hk = bhk % p.Hk;
   const int D = p.D, R = p.R, Nq = p.Nq, Nk = p.Nk, NqP = p.NqP;
-  const int j0 = kb * 128;
+  const int j0 = kb * C::JOB;
   const int kw0 = j0 + 32 * wave;   // first key of this wave
   const int kj = kw0 + lr;
 
@@ -441,7 +454,7 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
     // general rotate dim: one wave's 32 keys at a time through LDS
     constexpr int BS = EP + 1;
     float* ebuf = reinterpret_cast<float*>(smem);
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < C::NW; ++w) {
       __syncthreads();
       if (wave == w) {
   #pragma unroll
@@ -473,7 +486,7 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
   }
   if (p.dbias) {
     __syncthreads();
-    for (int d = tid; d < R; d += kThreads) atomicAdd(p.dbias + (int64_t)hk * p.bias_sh + d, dbias_s[d]);
+    for (int d = tid; d < R; d += C::THREADS) atomicAdd(p.dbias + (int64_t)hk * p.bias_sh + d, dbias_s[d]);
   }
 }
 
@@ -486,6 +499,7 @@ template <typename T, int EP, int DV>
 __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int qb, int bh) {
   typedef BwdCfg<EP, DV> C;
   constexpr int BN = C::BM, KS = C::KS, DS = C::DS, EB = C::EB, NB = BN / 32;
+  constexpr int kThreads = C::THREADS;
   constexpr int EPU = C::EPU, DVU = C::DVU, XU = C::XU, UNITS = C::Q_UNITS;
   typedef typename T::vec8 vec8;
 
@@ -494,7 +508,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
   const int bhk = b * p.Hk + hk;
   const int D = p.D, R = p.R, Nq = p.Nq, Nk = p.Nk, NkP = p.NkP;
   const int q_off = Nk - Nq;
-  const int qw0 = qb * 128 + 32 * wave;
+  const int qw0 = qb * C::JOB + 32 * wave;
   const int qi = qw0 + lr;
 
   vec8 qreg[KS], doreg[DS];
@@ -530,7 +544,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
 
   cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
   int nkeys = min(((ci32*)p.kend)[b], Nk);
-  if (p.causal) nkeys = min(nkeys, min(qb * 128 + 128, Nq));
+  if (p.causal) nkeys = min(nkeys, min(qb * C::JOB + C::JOB, Nq));
   const int nt = (nkeys + BN - 1) / BN;
 
   // ---- direct-load plan: unit c = m * 256 + tid of a slot (K_hat tile | V tile) --------
@@ -585,14 +599,14 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
     const int j0 = kt * BN;
     const uint16_t* kh_s = reinterpret_cast<const uint16_t*>(smem + (kt % kSlots) * C::SLOT);
     const uint16_t* v_s = kh_s + C::XT;
-    uint64_t mb = mw[j0 >> 6];
-    if (BN == 32) mb = (mb >> (j0 & 32)) & 0xffffffffull;
-    const uint64_t all_bits = BN == 64 ? ~0ull : 0xffffffffull;
-    // every key visible and (causal) every key at or before the wave's first query
-    const bool full = mb == all_bits && !(p.causal && j0 + BN - 1 > qw0);
-    if (mb == 0 || (p.causal && j0 > qw0 + 31)) continue;   // nothing visible to this wave
 #pragma unroll
     for (int ks = 0; ks < NB; ++ks) {
+      const int k0 = j0 + 32 * ks;   // first key of the sub-tile
+      const uint32_t mb = (uint32_t)(mw[k0 >> 6] >> (k0 & 32));
+      // nothing visible to this wave: every key masked, or (causal) after the wave's last query
+      if (mb == 0 || (p.causal && k0 > qw0 + 31)) continue;
+      // every key visible and (causal) at or before the wave's first query
+      const bool full = mb == 0xffffffffu && !(p.causal && k0 + 31 > qw0);
       f32x16 s = nlc, dp = ndc;
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk)
@@ -602,12 +616,12 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
         dp = T::mfma32(as_vec8<vec8>(ld16(v_s + 32 * ks * DV + vo.row_at(kk))), doreg[kk], dp);
       if (!full) {   // masked scores -> -inf: P = 0
         POPE_COLD_PATH();
-        const uint64_t w = mb >> (32 * ks + 4 * hf);
-        const int lim = p.causal ? qi - j0 - 32 * ks - 4 * hf : 64;
+        const uint32_t w = mb >> (4 * hf);
+        const int lim = p.causal ? qi - k0 - 4 * hf : 64;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kr = 8 * (r >> 2) + (r & 3);
-          s[r] = (((uint32_t)(w >> kr) & 1u) && kr <= lim) ? s[r] : -INFINITY;
+          s[r] = (((w >> kr) & 1u) && kr <= lim) ? s[r] : -INFINITY;
         }
       }
 #pragma unroll
@@ -695,7 +709,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
     // general rotate dim: one wave's 32 queries at a time through LDS
     constexpr int BS = EP + 1;
     float* ebuf = reinterpret_cast<float*>(smem);
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < C::NW; ++w) {
       __syncthreads();
       if (wave == w) {
   #pragma unroll
@@ -706,7 +720,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
       __syncthreads();
       for (int it = tid; it < 32 * D; it += kThreads) {
         const int qr = it / D, d = it - qr * D;
-        const int i = qb * 128 + 32 * w + qr;
+        const int i = qb * C::JOB + 32 * w + qr;
         if (i >= Nq) continue;
         const float* row = ebuf + qr * BS;
         float g;
@@ -728,10 +742,10 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
 }
 
 template <typename T, int EP, int DV>
-__global__ __launch_bounds__(kThreads, (BwdCfg<EP, DV>::MINB)) void bwd_main_kernel(FlashBwdParams p) {
+__global__ __launch_bounds__((BwdCfg<EP, DV>::THREADS), 1) void bwd_main_kernel(FlashBwdParams p) {
   __shared__ __attribute__((aligned(16))) char smem[BwdCfg<EP, DV>::LDS];
   __shared__ float dbias_s[EP];
-  const int nqb = p.NqP / 128;
+  const int nqb = p.NqP / BwdCfg<EP, DV>::JOB;
   const int id = blockIdx.x;
   int kind, blk, head;   // kind 0 = dK/dV job (head = b * Hk + hk), 1 = dQ job (head = b * Hq + h)
   if (p.interleave) {
@@ -767,11 +781,12 @@ hipError_t launch_t(const FlashBwdParams& p0, hipStream_t s) {
   hipError_t e = launch_named("flash_bwd_delta", bwd_delta_kernel<T>, dim3((unsigned)((8 * nrows + 255) / 256)),
                               dim3(256), s, p);
   if (e != hipSuccess) return e;
-  const int nkb = p.NkP / 128, nqb = p.NqP / 128;
+  typedef BwdCfg<EP, DV> C;
+  const int nkb = p.NkP / C::JOB, nqb = p.NqP / C::JOB;
   p.n_kv_jobs = nkb * p.B * p.Hk;
   p.interleave = p.causal && p.Hq == p.Hk && nkb == nqb && p.Nq == p.Nk;
   const int jobs = p.n_kv_jobs + nqb * p.B * p.Hq;
-  return launch_named("flash_bwd", bwd_main_kernel<T, EP, DV>, dim3(jobs), dim3(kThreads), s, p);
+  return launch_named("flash_bwd", bwd_main_kernel<T, EP, DV>, dim3(jobs), dim3(C::THREADS), s, p);
 }
 
 template <typename T>

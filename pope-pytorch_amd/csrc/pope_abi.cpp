@@ -108,8 +108,8 @@ int check_ws(size_t need, void* ws, size_t have) {
 //   | K_hat (B, Hk, NkP, EP) | Q_hat (B, Hq, NqP, EP)      16-bit elements
 //   | key visibility words (B, NW) u64 | last visible key + 1 (B) int32
 //   | -lse * log2 e, -delta (B, Hq, NqP) fp32 each           backward only
-// with EP = round_up(D + R, 32), DV = round_up(D, 32), NqP / NkP = round_up(N, 128),
-// NW = NkP / 64.
+// with EP = round_up(D + R, 32), DV = round_up(D, 32), NqP / NkP = round_up(N, 256) (the backward's
+// jobs cover 256 rows), NW = NkP / 64.
 void copy3(int64_t* dst, const int64_t* src);
 
 struct FlashLayout {
@@ -121,8 +121,8 @@ FlashLayout flash_layout(const pope_desc& d) {
   FlashLayout L;
   L.EP = round_up(d.D + d.R, 32);
   L.DV = round_up(d.D, 32);
-  L.NqP = round_up(d.Nq, 128);
-  L.NkP = round_up(d.Nk, 128);
+  L.NqP = round_up(d.Nq, 256);
+  L.NkP = round_up(d.Nk, 256);
   L.NW = L.NkP / 64;
   L.Bt = d.f_s[0] != 0 ? d.B : 1;
   L.Ht = d.f_s[1] != 0 ? d.Hq : 1;
@@ -144,7 +144,7 @@ size_t flash_ws(const pope_desc& d, int) { return flash_layout(d).total; }
 // The flash kernels address the rows of v and do inside one (batch, head) with 32-bit element
 // offsets, up to one tile past the padded length.
 int check_row_span(const char* name, int rows_padded, int64_t row_stride) {
-  const int64_t span = ((int64_t)rows_padded + 128) * row_stride;
+  const int64_t span = ((int64_t)rows_padded + 256) * row_stride;
   if (span >= ((int64_t)1 << 31))
     return fail(POPE_ERR_UNSUPPORTED, "%s rows span %lld elements per (batch, head); the kernels index them "
                 "with 32-bit offsets", name, (long long)span);
@@ -383,7 +383,7 @@ int pope_flash_fwd(const pope_desc* d, const void* q, const void* k, const void*
   p.B = d->B; p.Hq = d->Hq; p.Hk = d->Hk; p.Nq = d->Nq; p.Nk = d->Nk; p.D = d->D;
   p.EP = L.EP; p.DV = L.DV; p.NqP = L.NqP; p.NkP = L.NkP; p.NW = L.NW;
   p.causal = d->causal != 0;
-  p.nqb = L.NqP / 128;
+  p.nqb = (d->Nq + 127) / 128;
   copy3(p.v_s, d->v_s);
   copy3(p.o_s, d->o_s);
   e = pope::launch_flash_fwd(p, d->dtype, s);
