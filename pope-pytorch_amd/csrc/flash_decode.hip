@@ -50,6 +50,57 @@ __device__ __forceinline__ float2 half2f(uint32_t w) {
   return make_float2((float)v[0], (float)v[1]);
 }
 
+// Sum over aligned groups of LPK lanes (LPK = 4, 8 or 16) with DPP lane moves (VALU, no LDS
+// round trip): xor 1 and xor 2 by quad permutes, then the half-row mirror (lane i <-> 7 - i in
+// each 8-lane half) joins the two quads, and a row mirror (i <-> 15 - i) the two halves.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+template <int LPK>
+__device__ __forceinline__ float group_sum(float x) {
+  x += dpp_move<0xB1>(x);                    // quad_perm [1, 0, 3, 2]
+  x += dpp_move<0x4E>(x);                    // quad_perm [2, 3, 0, 1]
+  if (LPK >= 8) x += dpp_move<0x141>(x);     // row_half_mirror
+  if (LPK >= 16) x += dpp_move<0x140>(x);    // row_mirror
+  return x;
+}
+
+// Setup: the fp16 (cos, sin) table of F[bt, n, d] for n < Nk, and each (batch, head)'s query
+// weights (scale * log2 e folded in): rotated dims (a cos(F_q - b), a sin(F_q - b)) with
+// a = softplus(q) and F_q = F[Nk - 1]; pass-through dims (q, 0).
+template <typename T>
+__global__ __launch_bounds__(256) void decode_setup_kernel(DecodeParams p, int tab_blocks, int64_t n_tab) {
+  if ((int)blockIdx.x < tab_blocks) {
+    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < n_tab; idx += (int64_t)tab_blocks * 256) {
+      const int d = (int)(idx % p.R);
+      const int64_t rest = idx / p.R;
+      const int n = (int)(rest % p.Nk), bt = (int)(rest / p.Nk);
+      float sn, cs;
+      sincos_acc(p.freqs[(int64_t)bt * p.f_s[0] + (int64_t)n * p.f_s[2] + d], &sn, &cs);
+      const f16x2 v = {(_Float16)cs, (_Float16)sn};
+      p.table[idx] = __builtin_bit_cast(uint32_t, v);
+    }
+    return;
+  }
+  const int idx = ((int)blockIdx.x - tab_blocks) * 256 + threadIdx.x;
+  if (idx >= p.B * p.Hq * p.D) return;
+  const int d = idx % p.D, bh = idx / p.D;
+  const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
+  const float qv = T::to_float(p.q[(int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + d]);
+  float2 w;
+  if (d < p.R) {
+    float sn, cs;
+    sincos_acc(p.freqs[(int64_t)b * p.f_s[0] + (int64_t)(p.Nk - 1) * p.f_s[2] + d] - p.bias[(int64_t)hk * p.bias_sh + d],
+               &sn, &cs);
+    const float a = softplus_f(qv) * p.scale_log2;
+    w = make_float2(a * cs, a * sn);
+  } else {
+    w = make_float2(qv * p.scale_log2, 0.f);
+  }
+  p.qw[idx] = w;
+}
+
 // Thread layout: t = c + LPK * (hl + HG * kp): c = 8-dim chunk of the head dim, hl =
 // head within the pass, kp = key parity (the thread streams keys kp, kp + KP, ...).
 template <typename T, int LPK, int RMAX>
@@ -119,24 +170,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
     float wa[8], wb[8];
     f16x2 wab[8];
     {
-      const uint16_t* qrow = p.q + (int64_t)b * p.q_s[0] + (int64_t)hs * p.q_s[1];
-      float x[8];
-      unpack8<T>(cact ? ld16(qrow + d0) : u32x4{0u, 0u, 0u, 0u}, x);
-      const float* frow = R ? p.freqs + (int64_t)b * p.f_s[0] + (int64_t)(Nk - 1) * p.f_s[2] : nullptr;
-      const float* brow = R ? p.bias + (int64_t)hk * p.bias_sh : nullptr;
+      const float2* qwr = p.qw + ((int64_t)b * p.Hq + hs) * D + min(d0, D - 8);
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const int d = d0 + s;
-        if (rot) {
-          float sn, cs;
-          sincos_acc(frow[d] - brow[d], &sn, &cs);
-          const float a = softplus_f(x[s]);
-          wa[s] = a * cs * p.scale_log2;
-          wb[s] = a * sn * p.scale_log2;
-        } else {
-          wa[s] = cact ? x[s] * p.scale_log2 : 0.f;
-          wb[s] = 0.f;
-        }
+        const float2 w = cact ? qwr[s] : make_float2(0.f, 0.f);
+        wa[s] = w.x;
+        wb[s] = w.y;
         wab[s] = f16x2{(_Float16)wa[s], (_Float16)wb[s]};
       }
     }
@@ -176,8 +215,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
 #pragma unroll
           for (int q = 0; q < 8; ++q) part += wa[q] * x[q];
         }
-#pragma unroll
-        for (int m = 1; m < LPK; m <<= 1) part += __shfl_xor(part, m, 64);
+        part = group_sum<LPK>(part);
         if (c == 0 && jl < kSplit) s_lds[hl][jl] = vis_s[jl] ? part : -INFINITY;
       }
     };
@@ -190,6 +228,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
         score(bufB, bt + 1);
       }
     }
+    // the first V batch is in flight while the heads' maxima are reduced
+    if (nbh > 0) fetch(bufA, vbase, p.v_s[2], 0);
     __syncthreads();
 
     // ---- each head's max over the split (LPK * KP threads per head) -----------------
@@ -222,7 +262,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
         lsum += pv;
       }
     };
-    if (nbh > 0) fetch(bufA, vbase, p.v_s[2], 0);
     for (int bt = 0; bt < nbh; bt += 2) {
       if (bt + 1 < nbh) fetch(bufB, vbase, p.v_s[2], bt + 1);
       accumulate(bufA, bt);
@@ -327,8 +366,14 @@ hipError_t launch_t(const DecodeParams& p, hipStream_t s) {
   int HG = kThreads / LPK < kMaxHG ? kThreads / LPK : kMaxHG;
   if (p.Hq < HG) HG = p.Hq;
   const int KP = (kThreads / LPK) / HG;
-  hipError_t e = launch_named("flash_decode_split", decode_split_kernel<T, LPK, RMAX>, dim3(p.B * p.splits),
-                              dim3(kThreads), s, p, HG, KP);
+  const int64_t n_tab = p.R > 0 ? (int64_t)(p.t_sb != 0 ? p.B : 1) * p.Nk * p.R : 0;
+  const int tab_blocks = (int)((n_tab + 1023) / 1024);   // 4 entries per thread
+  const int qw_blocks = (p.B * p.Hq * p.D + 255) / 256;
+  hipError_t e = launch_named("flash_decode_setup", decode_setup_kernel<T>, dim3(tab_blocks + qw_blocks), dim3(256),
+                              s, p, tab_blocks, n_tab);
+  if (e != hipSuccess) return e;
+  e = launch_named("flash_decode_split", decode_split_kernel<T, LPK, RMAX>, dim3(p.B * p.splits),
+                   dim3(kThreads), s, p, HG, KP);
   if (e != hipSuccess) return e;
   return launch_named("flash_decode_combine", decode_combine_kernel<T>, dim3(p.B * p.Hq), dim3(256), s, p);
 }

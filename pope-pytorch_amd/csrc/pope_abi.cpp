@@ -203,8 +203,9 @@ size_t sim_ws(const pope_desc& d, int op) {
   return n;
 }
 
-// Decode workspace: [table | partial O (rows, splits, D) | partial (m, l) (rows, splits, 2)],
-// one split per pope::decode_split_keys() keys.
+// Decode workspace: [fp16 cos/sin table | partial O (rows, splits, D) | partial (m, l)
+// (rows, splits, 2) | query weights (rows, D) float2], one split per pope::decode_split_keys()
+// keys.
 int decode_splits(const pope_desc& d) {
   const int per = pope::decode_split_keys();
   return (d.Nk + per - 1) / per;
@@ -219,7 +220,7 @@ size_t decode_ws(const pope_desc& d) {
   const int splits = decode_splits(d);
   const size_t rows = (size_t)d.B * d.Hq * d.Nq;
   return decode_table_bytes(d) + align_up(rows * splits * d.D * sizeof(float)) +
-         align_up(rows * splits * 2 * sizeof(float));
+         align_up(rows * splits * 2 * sizeof(float)) + align_up(rows * d.D * sizeof(float2));
 }
 
 hipError_t build_table(const pope_desc& d, const float* freqs, const float* bias, int Bt, int Ht,
@@ -484,10 +485,7 @@ int pope_flash_decode(const pope_desc* d, const void* q, const void* k, const vo
   const size_t tb = decode_table_bytes(*d);
   float* part_o = reinterpret_cast<float*>(ws + tb);
   float* part_ml = reinterpret_cast<float*>(ws + tb + align_up(rows * splits * d->D * sizeof(float)));
-  if (d->R > 0) {
-    hipError_t e = build_table(*d, freqs, nullptr, g.Bt, g.Ht, nullptr, s, table);
-    if (e != hipSuccess) return hip_fail(e, "phase table launch");
-  }
+  float2* qw = reinterpret_cast<float2*>(reinterpret_cast<char*>(part_ml) + align_up(rows * splits * 2 * sizeof(float)));
   pope::DecodeParams p;
   std::memset(&p, 0, sizeof p);
   p.q = static_cast<const uint16_t*>(q);
@@ -497,6 +495,7 @@ int pope_flash_decode(const pope_desc* d, const void* q, const void* k, const vo
   p.bias = d->R > 0 ? bias : nullptr;
   p.mask = mask;
   p.table = d->R > 0 ? table : nullptr;
+  p.qw = qw;
   p.o = static_cast<uint16_t*>(o);
   p.lse = lse;
   p.part_o = part_o;

@@ -113,7 +113,8 @@ hipError_t launch_sim_bwd_ws(const SimParams& p, float* U, float* W, hipStream_t
 struct DecodeParams {
   const uint16_t* q; const uint16_t* k; const uint16_t* v;
   const float* freqs; const float* bias; const uint8_t* mask;
-  const uint32_t* table;     // fp16 (cos, sin) of F[b, h, n, d] for n < Nk, packed per 32-bit word
+  uint32_t* table;           // fp16 (cos, sin) of F[bt, n, d] for n < Nk, packed per 32-bit word
+  float2* qw;                // (B, Hq, D) query weights, written by the decode setup kernel
   uint16_t* o; float* lse;
   float* part_o; float* part_ml;   // split-K partials (B*Hq*Nq, splits, D) and (.., splits, 2)
   int B, Hq, Hk, Nq, Nk, D, R, causal, has_mask, splits, keys_per_split;
