@@ -15,12 +15,19 @@ the bias gradient, as the reference's fused backward does.
 
 Prints ONE JSON line.  ``value`` is TFLOP/s with the FA accounting of the
 metric: 3.5 * 4 * B * H * N^2 * D / 2 flops per causal fwd+bwd step.
+``secondary`` carries the two other GPU configs of the path, measured in the
+same run on their own inputs: C5 decode (one query row against a 32k KV cache,
+HBM GB/s of the valid K/V rows) and C2 fused similarity fwd+bwd in fp32.
+``--workload decode`` / ``--workload sim`` run only that config (used to
+profile one workload at a time); the default ``train`` runs all three.
 ``roofline`` covers the kernel with the largest share of the step time, timed
-by the library's own per-kernel hipEvents (recorded on the stream each kernel
-runs on) over a second pass of the same steps (the events stay out of the
-timed pass).  ``cpu_baseline`` times the CPU oracle (the
-restatement of the reference's PyTorch path) fwd+bwd on a bounded sample of the
-same workload on this host's cores.
+by the library's own per-kernel hipEvents over a second pass of the same steps
+(each launch's dispatch stamps its start and end into an event pair on the
+stream it runs on; the events stay out of the timed pass).  Its ``traffic`` is
+the HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+summary (profiles/flash_c3_traffic.md), calibrated against a copy kernel.
+``cpu_baseline`` times the CPU oracle (the restatement of the reference's
+PyTorch path) fwd+bwd on the whole workload on this host's cores.
 """
 from __future__ import annotations
 
@@ -43,6 +50,21 @@ SEED = 1003
 MAX_PAD = 512
 
 
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "flash_c3_traffic.md")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary (lines
+    ``traffic: <kernel> <bytes>``), or None when it holds no figure for that kernel."""
+    import re
+    try:
+        text = open(TRAFFIC_SUMMARY).read()
+    except OSError:
+        return None
+    m = re.search(rf"^traffic: {re.escape(kernel)} (\d+)$", text, re.M)
+    return int(m.group(1)) if m else None
+
+
 def fa_flops(kind: str) -> float:
     """Algorithmic flops of one launch (FA accounting, causal = half the N^2 pairs, head dim D).
 
@@ -55,6 +77,14 @@ def fa_flops(kind: str) -> float:
 
 
 STEP_FLOPS = 3.5 * 4 * B * H * N * N * D / 2
+
+
+# C5 decode: q (8,16,1,64), K/V (8,16,32768,64) bf16, PoPE(64, heads=16), valid lengths U{4096..32768}
+DEC_B, DEC_H, DEC_N, DEC_D, DEC_SEED = 8, 16, 32768, 64, 1005
+# C2 fused similarity: q, k (2,8,2048,64) fp32, PoPE(64, heads=8), dS N(0,1)
+SIM_B, SIM_H, SIM_N, SIM_D, SIM_SEED = 2, 8, 2048, 64, 1002
+PEAK_HBM_GBS = 8000.0
+PEAK_FP32_TFLOPS = 157.3
 
 
 def make_inputs(device):
@@ -117,9 +147,119 @@ def gpu_bench(steps: int, warmup: int):
     return elapsed, kernels, pads
 
 
-def cpu_baseline(min_seconds: float = 10.0, max_reps: int = 5):
-    """The CPU oracle fwd+bwd on one (batch, head) slice x 2 heads of the workload, fp32 after the
-    bf16 cast (the reference's PyTorch path promotes after softplus, pope.py:60,69-70)."""
+def _kernel_us(kernels, names):
+    return {n: round(kernels[n][1] / kernels[n][0] * 1e3, 2) for n in names if n in kernels}
+
+
+def decode_bench(steps: int, warmup: int):
+    """C5: flash_attn_with_pope at Nq = 1 (the decode kernels).  GB/s counts the valid K and V rows
+    once (sum_b L_b * H * D * 2 bytes * 2) -- the algorithmic bytes; masked rows are never read."""
+    import torch
+
+    import pope_amd
+    from pope_amd import _lib
+
+    g = torch.Generator().manual_seed(DEC_SEED)
+    dev = torch.device("cuda:0")
+    q = torch.randn(DEC_B, DEC_H, 1, DEC_D, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(DEC_B, DEC_H, DEC_N, DEC_D, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(DEC_B, DEC_H, DEC_N, DEC_D, generator=g).to(torch.bfloat16).to(dev)
+    lens = torch.randint(4096, DEC_N + 1, (DEC_B,), generator=g)
+    mask = (torch.arange(DEC_N)[None, :] < lens[:, None]).to(dev)
+    freqs, bias = pope_amd.PoPE(DEC_D, heads=DEC_H).to(dev)(DEC_N)
+    run = lambda: pope_amd.flash_attn_with_pope(q, k, v, pos_emb=(freqs, bias), mask=mask)
+    with torch.no_grad():
+        for _ in range(warmup):
+            run()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            run()
+        torch.cuda.synchronize()
+        el = (time.perf_counter() - t0) / steps
+        _lib.profile_reset()
+        _lib.profile_enable(True)
+        for _ in range(steps):
+            run()
+        torch.cuda.synchronize()
+        _lib.profile_enable(False)
+    ks = _lib.profile_read()
+    valid = int(lens.sum()) * DEC_H * DEC_D * 2 * 2
+    split = ks["flash_decode_split"]
+    split_s = split[1] / split[0] * 1e-3
+    kern_s = sum(c_t[1] / c_t[0] for c_t in ks.values()) * 1e-3
+    return {
+        "workload": "C5 decode: q (8,16,1,64) vs K/V (8,16,32768,64) bf16, PoPE(64, heads=16), "
+                    "key-padding mask with valid lengths U{4096..32768}",
+        "valid_lengths": [int(x) for x in lens], "algorithmic_bytes": valid,
+        "us_per_call": round(el * 1e6, 2), "GBps": round(valid / el / 1e9, 1),
+        "GBps_kernels": round(valid / kern_s / 1e9, 1),
+        "roofline": {"bound": "hbm", "kernel": "flash_decode_split",
+                     "achieved": round(valid / split_s / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(valid / split_s / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": measured_traffic("flash_decode_split"),
+                     "avg_launch_us": round(split_s * 1e6, 2)},
+        "frac_of_hbm_peak": round(valid / el / 1e9 / PEAK_HBM_GBS, 4),
+        "kernels_us": _kernel_us(ks, sorted(ks)),
+    }
+
+
+def sim_bench(steps: int, warmup: int):
+    """C2: compute_attn_similarity fwd+bwd in fp32 (sim, dq, dk, dbias).  Flops: fwd 2*B*H*N^2*(D+R),
+    bwd twice that; bytes: sim write + dS read + q, k read + dq, dk write + freqs."""
+    import torch
+
+    import pope_amd
+    from pope_amd import _lib
+
+    B_, H_, N_, D_ = SIM_B, SIM_H, SIM_N, SIM_D
+    g = torch.Generator().manual_seed(SIM_SEED)
+    dev = torch.device("cuda:0")
+    q = torch.randn(B_, H_, N_, D_, generator=g).to(dev).requires_grad_(True)
+    k = torch.randn(B_, H_, N_, D_, generator=g).to(dev).requires_grad_(True)
+    ds = torch.randn(B_, H_, N_, N_, generator=g).to(dev)
+    pope = pope_amd.PoPE(D_, heads=H_).to(dev)
+
+    def step():
+        q.grad = k.grad = None
+        pope.bias.grad = None
+        sim = pope_amd.compute_attn_similarity(q, k, pope(N_))
+        sim.backward(ds)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    el = (time.perf_counter() - t0) / steps
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_enable(False)
+    ks = _lib.profile_read()
+    R_ = D_
+    flops = 3 * 2 * B_ * H_ * N_ * N_ * (D_ + R_)
+    nbytes = 2 * 4 * B_ * H_ * N_ * N_ + 2 * 4 * 2 * B_ * H_ * N_ * D_ + 4 * N_ * R_
+    t_min = max(flops / (PEAK_FP32_TFLOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9))
+    return {
+        "workload": "C2 fused similarity fwd+bwd: q, k (2,8,2048,64) fp32, PoPE(64, heads=8), dS N(0,1)",
+        "us_per_step": round(el * 1e6, 2), "TFLOPs": round(flops / el / 1e12, 2),
+        "GBps": round(nbytes / el / 1e9, 1), "algorithmic_flops": flops, "algorithmic_bytes": nbytes,
+        "frac_of_roofline": round(t_min / el, 4),
+        "roofline_bound": "fp32" if flops / (PEAK_FP32_TFLOPS * 1e12) > nbytes / (PEAK_HBM_GBS * 1e9) else "hbm",
+        "kernels_us": _kernel_us(ks, sorted(ks)),
+    }
+
+
+def cpu_baseline(min_seconds: float = 10.0, max_reps: int = 10):
+    """The CPU oracle fwd+bwd over the whole C3 workload (every batch and head, two heads per
+    call), fp32 after the bf16 cast (the reference's PyTorch path promotes after softplus,
+    pope.py:60,69-70).  Repeated until about ``min_seconds`` of CPU work; the median pass is
+    reported."""
     import torch
 
     from oracle import pope_oracle as orc
@@ -129,16 +269,15 @@ def cpu_baseline(min_seconds: float = 10.0, max_reps: int = 5):
     torch.set_num_threads(threads)
     q, k, v, do, mask, _ = make_inputs("cpu")
     hs = 2
-    up = lambda t: t[:1, :hs].float().clone().requires_grad_(True)
     freqs = orc.pope_freqs(N, orc.inv_freqs(R))
     bias = torch.zeros(hs, R, requires_grad=True)
-    m1 = mask[:1]
-    flops = 3.5 * 4 * 1 * hs * N * N * D / 2
 
     def one():
-        qq, kk, vv = up(q), up(k), up(v)
-        o = orc.flash_nonfused(qq, kk, vv, freqs, bias, mask=m1, causal=True)
-        o.backward(do[:1, :hs].float())
+        for b in range(B):
+            for h0 in range(0, H, hs):
+                up = lambda t: t[b:b + 1, h0:h0 + hs].float().clone().requires_grad_(True)
+                o = orc.flash_nonfused(up(q), up(k), up(v), freqs, bias, mask=mask[b:b + 1], causal=True)
+                o.backward(do[b:b + 1, h0:h0 + hs].float())
 
     one()   # warm-up
     times = []
@@ -150,13 +289,13 @@ def cpu_baseline(min_seconds: float = 10.0, max_reps: int = 5):
     times.sort()
     med = times[len(times) // 2]
     return {
-        "value": round(flops / med / 1e12, 6),
+        "value": round(STEP_FLOPS / med / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"oracle fwd+bwd (torch fp32, CPU) on batch 0, heads 0-{hs - 1} of the workload "
-                  f"(1x{hs}x{N}x{D}, causal, mask); median of {len(times)} runs "
-                  f"= {med * 1e3:.1f} ms; FA flop accounting as the GPU value",
+        "sample": f"the whole workload: oracle fwd+bwd (torch fp32, CPU) over B={B} x H={H} heads, "
+                  f"N={N}, D={D}, causal, mask, two heads per call; median of {len(times)} passes "
+                  f"= {med * 1e3:.1f} ms per step; FA flop accounting as the GPU value",
     }
 
 
@@ -166,11 +305,20 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=("train", "decode", "sim"), default="train",
+                    help="train (default): the C3 headline line with C5 and C2 as secondary; "
+                         "decode / sim: only that config's measurement")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {a.gpus} is not supported "
               "(the path shards over (batch x head); see the multi-GPU design notes)", file=sys.stderr)
         sys.exit(2)
+
+    if a.workload != "train":
+        fn = decode_bench if a.workload == "decode" else sim_bench
+        print(json.dumps({"workload": a.workload, "steps": a.steps, "warmup": a.warmup,
+                          **fn(a.steps, a.warmup)}), flush=True)
+        return
 
     elapsed, kernels, pads = gpu_bench(a.steps, a.warmup)
     ms = elapsed / a.steps * 1e3
@@ -184,7 +332,7 @@ def main():
     achieved = fa_flops(dom) / avg_s / 1e12
     roofline = {
         "bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-        "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+        "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(dom),
         "avg_launch_us": round(avg_s * 1e6, 2),
     }
     breakdown = {n: {"launches": c, "avg_us": round(t / c * 1e3, 2)} for n, (c, t, _, _) in sorted(kernels.items())}
@@ -200,6 +348,7 @@ def main():
         "frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
         "roofline": roofline,
         "kernels": breakdown,
+        "secondary": {"decode_c5": decode_bench(a.steps, a.warmup), "sim_c2": sim_bench(a.steps, a.warmup)},
     }
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()

@@ -156,8 +156,9 @@ int pope_flash_decode(const pope_desc* desc, const void* q, const void* k, const
 /*
  * Per-kernel timing.  No counterpart in the reference (its tests print only
  * parity diffs, tests/test_flash_attn.py:61,109).  While enabled, every kernel
- * launch of the library is bracketed by a pair of hipEvents recorded on the
- * stream the kernel runs on.  pope_profile_read waits for the recorded events
+ * launch of the library carries a pair of hipEvents that its dispatch stamps with
+ * the kernel's own start and end (hipExtLaunchKernel), on the stream the kernel
+ * runs on.  pope_profile_read waits for the recorded events
  * and writes one line per kernel name, "name count total_ms min_ms max_ms",
  * cumulative since the last pope_profile_reset.  Used by bench.py to time the
  * dominant kernel on its own stream.

@@ -26,16 +26,18 @@
 //
 // Launches (all on the caller's stream, no atomics except dfreqs / dbias):
 //   delta      : -lse * log2 e and -rowsum(O * dO) per query row
-//   bwd_main   : one launch holding two kinds of jobs, one per workgroup of 4 waves
-//     dK/dV job: 128 keys (32 per wave) of one (batch, kv head); loops over the
-//                query heads of its group and the query tiles that can see its
-//                keys (tiles before the causal diagonal are skipped); the
-//                epilogue applies the key-side chain rule and sums dbias.
-//     dQ job   : 128 queries (32 per wave); loops over the key tiles up to the
-//                causal diagonal; the epilogue applies the query-side chain
-//                rule.  dQ needs no atomics, so dq is deterministic (the
-//                reference accumulates it with atomics in the input dtype,
-//                triton_pope_flash_attn.py:215).
+//   bwd_main   : one launch holding two kinds of jobs, one per workgroup
+//     dK/dV job: 32 keys per wave (256 keys in 8 waves when D + R and D are small,
+//                128 in 4 waves otherwise) of one (batch, kv head); loops over the
+//                query heads of its group and the query steps (128 or 64 rows)
+//                that can see its keys (steps before the causal diagonal are
+//                skipped); the epilogue applies the key-side chain rule and sums
+//                dbias.
+//     dQ job   : 32 queries per wave, the same job sizes; loops over the key
+//                steps up to the causal diagonal; the epilogue applies the
+//                query-side chain rule.  dQ needs no atomics, so dq is
+//                deterministic (the reference accumulates it with atomics in the
+//                input dtype, triton_pope_flash_attn.py:215).
 //   Causal dK/dV job r and dQ job (blocks - 1 - r) cost the same; the launch
 //   orders the pairs heaviest first, so the triangle's work balances over the
 //   CUs.  Streamed tiles go straight from global memory into a ring of three LDS

@@ -8,6 +8,8 @@
 //
 // The path is bound by HBM: every valid key costs 2 * D * 2 bytes of K and V
 // and a handful of flops.  Work decomposition:
+//   decode_setup : the fp16 cos / sin(F_j) table of the keys and each (batch,
+//                  head)'s query weights (below), once per call;
 //   decode_split : one workgroup (4 waves) per (batch, split of kSplit keys),
 //                  covering every query head of the batch.  A split whose keys
 //                  are all masked exits after reading its mask bytes.  The split's

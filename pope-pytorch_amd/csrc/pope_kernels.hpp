@@ -1,25 +1,34 @@
 // Kernel parameter blocks and launchers shared between the kernels and the C ABI.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace pope {
 
-// Per-kernel timing (profile.cpp).  prof_begin returns -1 when profiling is off.
-int prof_begin(const char* name, hipStream_t s);
-void prof_end(int token, hipStream_t s);
+// Per-kernel timing (profile.cpp).  prof_begin returns -1 when profiling is off, else a token
+// and the event pair the launch records its own start / end timestamps into.
+int prof_begin(const char* name, hipEvent_t* start, hipEvent_t* stop);
+void prof_cancel(int token);
 void prof_enable(int on);
 int prof_read(char* buf, size_t n);
 void prof_reset();
 
-// Launches `kernel`, bracketed by profiling events when profiling is on.
+// Launches `kernel`; when profiling is on, the dispatch itself records its start and end
+// timestamps into a pair of events (hipExtLaunchKernel), so the elapsed time is the kernel's
+// execution alone, as a kernel trace reports it.
 template <typename... KArgs, typename... Args>
 hipError_t launch_named(const char* name, void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t s,
                         Args... args) {
-  const int t = prof_begin(name, s);
-  hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  const int t = prof_begin(name, &ev0, &ev1);
+  if (t < 0) {
+    hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
+    return hipGetLastError();
+  }
+  hipExtLaunchKernelGGL(kernel, grid, block, 0, s, ev0, ev1, 0u, args...);
   const hipError_t e = hipGetLastError();
-  prof_end(t, s);
+  if (e != hipSuccess) prof_cancel(t);
   return e;
 }
 

@@ -1,5 +1,5 @@
-// Opt-in per-kernel timing: when enabled, every kernel launch of the library is
-// bracketed by a pair of hipEvents recorded on the stream it is launched on.
+// Opt-in per-kernel timing: when enabled, every kernel launch of the library carries a pair of
+// hipEvents that its dispatch stamps with the kernel's own start and end times.
 // Reading the totals waits for the recorded events, folds their elapsed times
 // into per-kernel statistics and returns the event pairs to a pool.
 #include <hip/hip_runtime.h>
@@ -20,6 +20,7 @@ namespace {
 struct Pending {
   const char* name;
   hipEvent_t a, b;
+  bool live;
 };
 
 struct Stat {
@@ -36,30 +37,30 @@ constexpr size_t kMaxPending = 1 << 16;
 
 }  // namespace
 
-int prof_begin(const char* name, hipStream_t s) {
+int prof_begin(const char* name, hipEvent_t* start, hipEvent_t* stop) {
   if (!g_on.load(std::memory_order_relaxed)) return -1;
   std::lock_guard<std::mutex> lk(g_mu);
   if (g_pending.size() >= kMaxPending) return -1;
-  Pending p{name, nullptr, nullptr};
+  Pending p{name, nullptr, nullptr, true};
   if (!g_pool.empty()) {
     p.a = g_pool.back().first;
     p.b = g_pool.back().second;
     g_pool.pop_back();
-  } else if (hipEventCreate(&p.a) != hipSuccess || hipEventCreate(&p.b) != hipSuccess) {
+  } else if (hipEventCreate(&p.a) != hipSuccess) {
     return -1;
-  }
-  if (hipEventRecord(p.a, s) != hipSuccess) {
-    g_pool.emplace_back(p.a, p.b);
+  } else if (hipEventCreate(&p.b) != hipSuccess) {
+    (void)hipEventDestroy(p.a);
     return -1;
   }
   g_pending.push_back(p);
+  *start = p.a;
+  *stop = p.b;
   return (int)g_pending.size() - 1;
 }
 
-void prof_end(int token, hipStream_t s) {
-  if (token < 0) return;
+void prof_cancel(int token) {
   std::lock_guard<std::mutex> lk(g_mu);
-  if ((size_t)token < g_pending.size()) (void)hipEventRecord(g_pending[token].b, s);
+  if (token >= 0 && (size_t)token < g_pending.size()) g_pending[token].live = false;
 }
 
 void prof_enable(int on) { g_on.store(on ? 1 : 0); }
@@ -71,6 +72,10 @@ int prof_read(char* buf, size_t n) {
   int rc = 0;
   for (const Pending& p : g_pending) {
     float ms = 0.f;
+    if (!p.live) {
+      g_pool.emplace_back(p.a, p.b);
+      continue;
+    }
     if (hipEventSynchronize(p.b) != hipSuccess || hipEventElapsedTime(&ms, p.a, p.b) != hipSuccess) {
       rc = 1;
     } else {

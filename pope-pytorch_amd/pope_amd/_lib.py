@@ -139,7 +139,7 @@ def workspace(op: int, desc: PopeDesc, device) -> torch.Tensor | None:
 
 
 def profile_enable(on: bool = True) -> None:
-    """Bracket every kernel launch of the library with hipEvents on its stream."""
+    """Time every kernel launch of the library with an event pair its dispatch stamps."""
     check(lib().pope_profile_enable(1 if on else 0), "profile enable")
 
 
