@@ -326,10 +326,11 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
     __syncthreads();                                // ... everyone's; step st - 1's slot is free
     if (st + 2 < nsteps) issue(st + 2);
     const int i0 = (qt0 + st % per_head) * BM;
-    const uint16_t* qh_s = reinterpret_cast<const uint16_t*>(smem + (st % kSlots) * C::SLOT);
-    const uint16_t* do_s = qh_s + C::XT;
-    const float* nl_s = reinterpret_cast<const float*>(do_s + C::YT);
-    const float* nd_s = nl_s + BM;
+    // byte addresses in the step's slot: Q_hat tile | dO tile | -lse rows | -delta rows
+    const uint32_t sb = lds_addr(smem + (st % kSlots) * C::SLOT);
+    const TileAddr<EPU> qa(qo, sb);
+    const TileAddr<DVU> da(doo, sb + 2 * C::XT);
+    const uint32_t nla = opaque_u32(sb + 2 * (C::XT + C::YT) + 16 * hf);
 #pragma unroll
     for (int qs = 0; qs < QB; ++qs) {
       // every query of the sub-tile before every key of the wave (causal), or no visible key
@@ -337,8 +338,8 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
       f32x16 s, dp;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {   // rows 32 qs + 8 q + 4 hf + (0..3)
-        const f32x4 a = *reinterpret_cast<const f32x4*>(nl_s + 32 * qs + 8 * q + 4 * hf);
-        const f32x4 d = *reinterpret_cast<const f32x4*>(nd_s + 32 * qs + 8 * q + 4 * hf);
+        const f32x4 a = lds_read_f4_at(nla + 4 * (32 * qs + 8 * q));
+        const f32x4 d = lds_read_f4_at(nla + 4 * (BM + 32 * qs + 8 * q));
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
           s[4 * q + x] = a[x];
@@ -347,10 +348,10 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
       }
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk)
-        s = T::mfma32(as_vec8<vec8>(ld16(qh_s + 32 * qs * EP + qo.row_at(kk))), kreg[kk], s);
+        s = T::mfma32(as_vec8<vec8>(lds_read16_at(qa.row_at(kk) + 2 * 32 * qs * EP)), kreg[kk], s);
 #pragma unroll
       for (int kk = 0; kk < DS; ++kk)
-        dp = T::mfma32(as_vec8<vec8>(ld16(do_s + 32 * qs * DV + doo.row_at(kk))), vreg[kk], dp);
+        dp = T::mfma32(as_vec8<vec8>(lds_read16_at(da.row_at(kk) + 2 * 32 * qs * DV)), vreg[kk], dp);
       // Partial sub-tile (some key of the wave masked, or on the causal diagonal): masked
       // scores become -inf so that P = 0.
       if (!wave_vis || (p.causal && i0 + 32 * qs < kw0 + 31)) {
@@ -375,10 +376,12 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
         const int r0 = 32 * qs + 16 * g2;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
-          dva[db] = T::mfma32(ap, as_vec8<vec8>(lds_tr8(do_s + r0 * DV, doo.lo_at(db), doo.hi_at(db))), dva[db]);
+          dva[db] = T::mfma32(ap, as_vec8<vec8>(lds_tr8_at(da.lo_at(db) + 2 * r0 * DV, da.hi_at(db) + 2 * r0 * DV)),
+                              dva[db]);
 #pragma unroll
         for (int eb = 0; eb < EB; ++eb)
-          dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_tr8(qh_s + r0 * EP, qo.lo_at(eb), qo.hi_at(eb))), dka[eb]);
+          dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_tr8_at(qa.lo_at(eb) + 2 * r0 * EP, qa.hi_at(eb) + 2 * r0 * EP)),
+                              dka[eb]);
       }
     }
   }
@@ -599,8 +602,9 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
     __syncthreads();
     if (kt + 2 < nt) issue(kt + 2);
     const int j0 = kt * BN;
-    const uint16_t* kh_s = reinterpret_cast<const uint16_t*>(smem + (kt % kSlots) * C::SLOT);
-    const uint16_t* v_s = kh_s + C::XT;
+    const uint32_t sb = lds_addr(smem + (kt % kSlots) * C::SLOT);   // K_hat tile | V tile
+    const TileAddr<EPU> ka(ko, sb);
+    const TileAddr<DVU> va(vo, sb + 2 * C::XT);
 #pragma unroll
     for (int ks = 0; ks < NB; ++ks) {
       const int k0 = j0 + 32 * ks;   // first key of the sub-tile
@@ -612,10 +616,10 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
       f32x16 s = nlc, dp = ndc;
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk)
-        s = T::mfma32(as_vec8<vec8>(ld16(kh_s + 32 * ks * EP + ko.row_at(kk))), qreg[kk], s);
+        s = T::mfma32(as_vec8<vec8>(lds_read16_at(ka.row_at(kk) + 2 * 32 * ks * EP)), qreg[kk], s);
 #pragma unroll
       for (int kk = 0; kk < DS; ++kk)
-        dp = T::mfma32(as_vec8<vec8>(ld16(v_s + 32 * ks * DV + vo.row_at(kk))), doreg[kk], dp);
+        dp = T::mfma32(as_vec8<vec8>(lds_read16_at(va.row_at(kk) + 2 * 32 * ks * DV)), doreg[kk], dp);
       if (!full) {   // masked scores -> -inf: P = 0
         POPE_COLD_PATH();
         const uint32_t w = mb >> (4 * hf);
@@ -631,10 +635,10 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
 #pragma unroll
       for (int g2 = 0; g2 < 2; ++g2) {
         const vec8 bds = as_vec8<vec8>(pack8<T>(dp, g2));
-        const uint16_t* kr0 = kh_s + (32 * ks + 16 * g2) * EP;
+        const uint32_t r0 = 2 * (32 * ks + 16 * g2) * EP;
 #pragma unroll
         for (int eb = 0; eb < EB; ++eb)
-          dqa[eb] = T::mfma32(as_vec8<vec8>(lds_tr8(kr0, ko.lo_at(eb), ko.hi_at(eb))), bds, dqa[eb]);
+          dqa[eb] = T::mfma32(as_vec8<vec8>(lds_tr8_at(ka.lo_at(eb) + r0, ka.hi_at(eb) + r0)), bds, dqa[eb]);
       }
     }
   }

@@ -267,13 +267,21 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   };
   // O^T += V^T P^T over the tile's 16-key groups
   auto pv = [&](int pr, const u32x4* pw) {
-    const uint16_t* vt = v_tile(pr);
+    // one address register per (db, row run); the 16-key groups are immediate offsets
+    const uint32_t vb = lds_addr(v_tile(pr));
+    uint32_t alo[NDB], ahi[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      alo[db] = opaque_u32(vb + 2 * vo.lo_at(db));
+      ahi[db] = opaque_u32(vb + 2 * vo.hi_at(db));
+    }
 #pragma unroll
     for (int g16 = 0; g16 < BN / 16; ++g16) {
       const vec8 pb = as_vec8<vec8>(pw[g16]);
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        oacc[db] = T::mfma32(as_vec8<vec8>(lds_tr8(vt + 16 * g16 * DV, vo.lo_at(db), vo.hi_at(db))), pb, oacc[db]);
+        const uint32_t off = 2 * 16 * g16 * DV;
+        oacc[db] = T::mfma32(as_vec8<vec8>(lds_tr8_at(alo[db] + off, ahi[db] + off)), pb, oacc[db]);
       }
     }
   };

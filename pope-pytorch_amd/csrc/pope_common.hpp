@@ -177,6 +177,26 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
+// The same read at an LDS byte address.  With `a` made opaque (opaque_u32) once per tile, the
+// constant part of every read's address folds into the instruction's offset field instead of
+// costing an address register and one or two VALU instructions per read.
+__device__ __forceinline__ u32x2 lds_read_tr16_at(uint32_t a) {
+  typedef v4i16 __attribute__((address_space(3))) * lds_v4i16_ptr;
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(size_t)a);
+  return __builtin_bit_cast(u32x2, r);
+}
+__device__ __forceinline__ u32x4 lds_tr8_at(uint32_t lo, uint32_t hi) {
+  const u32x2 a = lds_read_tr16_at(lo);
+  const u32x2 b = lds_read_tr16_at(hi);
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+
+// A value the compiler may not re-derive or re-associate (it stays the one register it is).
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // Direct global -> LDS load of 16 bytes per lane: lane l's bytes land at LDS byte address
 // lds + 16 l (lds is wave-uniform, passed in M0).  Written as inline assembly so that the
 // compiler does not add its conservative wait for every outstanding LDS load before each LDS
@@ -237,6 +257,38 @@ struct TileOffsets {
   __device__ __forceinline__ int lo_at(int nb) const { return lo[nb % TP] + 32 * (nb - nb % TP); }
   __device__ __forceinline__ int hi_at(int nb) const { return hi[nb % TP] + 32 * (nb - nb % TP); }
 };
+
+// The periodic bases of TileOffsets made absolute LDS byte addresses of one tile (a stage slot
+// changes every step) and opaque: each operand read is then one base register plus an immediate
+// offset (k step, column block and the caller's row block), with one VALU add per base per tile
+// instead of one or two per read.
+template <int U>
+struct TileAddr {
+  static constexpr int RP = TileOffsets<U>::RP, TP = TileOffsets<U>::TP;
+  uint32_t row[RP], lo[TP], hi[TP];
+  __device__ __forceinline__ TileAddr(const TileOffsets<U>& o, uint32_t tile) {
+#pragma unroll
+    for (int k = 0; k < RP; ++k) row[k] = opaque_u32(tile + 2 * o.row[k]);
+#pragma unroll
+    for (int k = 0; k < TP; ++k) {
+      lo[k] = opaque_u32(tile + 2 * o.lo[k]);
+      hi[k] = opaque_u32(tile + 2 * o.hi[k]);
+    }
+  }
+  __device__ __forceinline__ uint32_t row_at(int kk) const { return row[kk % RP] + 2 * 16 * (kk - kk % RP); }
+  __device__ __forceinline__ uint32_t lo_at(int nb) const { return lo[nb % TP] + 2 * 32 * (nb - nb % TP); }
+  __device__ __forceinline__ uint32_t hi_at(int nb) const { return hi[nb % TP] + 2 * 32 * (nb - nb % TP); }
+};
+
+// 16-byte LDS reads at a byte address.
+__device__ __forceinline__ u32x4 lds_read16_at(uint32_t a) {
+  typedef const u32x4 __attribute__((address_space(3))) * lds_u32x4_ptr;
+  return *(lds_u32x4_ptr)(size_t)a;
+}
+__device__ __forceinline__ f32x4 lds_read_f4_at(uint32_t a) {
+  typedef const f32x4 __attribute__((address_space(3))) * lds_f32x4_ptr;
+  return *(lds_f32x4_ptr)(size_t)a;
+}
 
 // 8-element operand from the two transposed chunks at lo and hi.
 __device__ __forceinline__ u32x4 lds_tr8(const uint16_t* base, int lo, int hi) {
