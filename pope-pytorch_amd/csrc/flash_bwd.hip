@@ -346,12 +346,19 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
           dp[4 * q + x] = d[x];
         }
       }
+      // every operand read of the two products issued before the first product, so one LDS
+      // latency is exposed per sub-tile instead of one per product
+      u32x4 fq[KS], fd[DS];
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk)
-        s = T::mfma32(as_vec8<vec8>(lds_read16_at(qa.row_at(kk) + 2 * 32 * qs * EP)), kreg[kk], s);
+      for (int kk = 0; kk < KS; ++kk) fq[kk] = lds_read16_at(qa.row_at(kk) + 2 * 32 * qs * EP);
 #pragma unroll
-      for (int kk = 0; kk < DS; ++kk)
-        dp = T::mfma32(as_vec8<vec8>(lds_read16_at(da.row_at(kk) + 2 * 32 * qs * DV)), vreg[kk], dp);
+      for (int kk = 0; kk < DS; ++kk) fd[kk] = lds_read16_at(da.row_at(kk) + 2 * 32 * qs * DV);
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) s = T::mfma32(as_vec8<vec8>(fq[kk]), kreg[kk], s);
+#pragma unroll
+      for (int kk = 0; kk < DS; ++kk) dp = T::mfma32(as_vec8<vec8>(fd[kk]), vreg[kk], dp);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8 + KS + DS, 0);   // with the 8 row-term reads
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, KS + DS, 0);
       // Partial sub-tile (some key of the wave masked, or on the causal diagonal): masked
       // scores become -inf so that P = 0.
       if (!wave_vis || (p.causal && i0 + 32 * qs < kw0 + 31)) {
@@ -614,12 +621,27 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
       // every key visible and (causal) at or before the wave's first query
       const bool full = mb == 0xffffffffu && !(p.causal && k0 + 31 > qw0);
       f32x16 s = nlc, dp = ndc;
+      u32x4 fk[KS], fv[DS];   // operand reads first (one exposed LDS latency per sub-tile)
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk)
-        s = T::mfma32(as_vec8<vec8>(lds_read16_at(ka.row_at(kk) + 2 * 32 * ks * EP)), qreg[kk], s);
+      for (int kk = 0; kk < KS; ++kk) fk[kk] = lds_read16_at(ka.row_at(kk) + 2 * 32 * ks * EP);
 #pragma unroll
-      for (int kk = 0; kk < DS; ++kk)
-        dp = T::mfma32(as_vec8<vec8>(lds_read16_at(va.row_at(kk) + 2 * 32 * ks * DV)), doreg[kk], dp);
+      for (int kk = 0; kk < DS; ++kk) fv[kk] = lds_read16_at(va.row_at(kk) + 2 * 32 * ks * DV);
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) s = T::mfma32(as_vec8<vec8>(fk[kk]), qreg[kk], s);
+#pragma unroll
+      for (int kk = 0; kk < DS; ++kk) dp = T::mfma32(as_vec8<vec8>(fv[kk]), doreg[kk], dp);
+      // the transposed K_hat operands of dQ, read while the products and the exponentials run
+      u32x4 ft[2][EB];
+#pragma unroll
+      for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+        for (int eb = 0; eb < EB; ++eb) {
+          const uint32_t r0 = 2 * (32 * ks + 16 * g2) * EP;
+          ft[g2][eb] = lds_tr8_at(ka.lo_at(eb) + r0, ka.hi_at(eb) + r0);
+        }
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, KS + DS, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, KS + DS, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4 * EB, 0);
       if (!full) {   // masked scores -> -inf: P = 0
         POPE_COLD_PATH();
         const uint32_t w = mb >> (4 * hf);
@@ -635,10 +657,8 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
 #pragma unroll
       for (int g2 = 0; g2 < 2; ++g2) {
         const vec8 bds = as_vec8<vec8>(pack8<T>(dp, g2));
-        const uint32_t r0 = 2 * (32 * ks + 16 * g2) * EP;
 #pragma unroll
-        for (int eb = 0; eb < EB; ++eb)
-          dqa[eb] = T::mfma32(as_vec8<vec8>(lds_tr8_at(ka.lo_at(eb) + r0, ka.hi_at(eb) + r0)), bds, dqa[eb]);
+        for (int eb = 0; eb < EB; ++eb) dqa[eb] = T::mfma32(as_vec8<vec8>(ft[g2][eb]), bds, dqa[eb]);
       }
     }
   }
