@@ -556,7 +556,9 @@ int pope_sim_bwd(const pope_desc* d, const void* dsim, const void* q, const void
   hipError_t e = sim_setup(*d, q, k, freqs, bias, ws, s, &p);
   if (e != hipSuccess) return hip_fail(e, "phase table launch");
   p.dsim = static_cast<const float*>(dsim);
-  p.g_vec = aligned16(dsim) && d->sim_s[0] % 4 == 0 && d->sim_s[1] % 4 == 0 && d->sim_s[2] % 4 == 0;
+  // 4-wide loads of dsim rows, addressed with 32-bit offsets within one (batch, head)
+  p.g_vec = aligned16(dsim) && d->sim_s[0] % 4 == 0 && d->sim_s[1] % 4 == 0 && d->sim_s[2] % 4 == 0 &&
+            (int64_t)d->Nq * d->sim_s[2] < ((int64_t)1 << 31);
   p.dq = static_cast<float*>(dq);
   p.dk = static_cast<float*>(dk);
   p.dfreqs = dfreqs;

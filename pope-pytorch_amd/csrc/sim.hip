@@ -186,6 +186,25 @@ __global__ __launch_bounds__(kThreads, 2) void sim_bwd_u_kernel(SimParams p, flo
       }
     }
     __syncthreads();
+    if (p.g_vec && j0 + kBJ <= Nk) {
+      // every key of the block in range: the lane's 8 loads issued before the products (rows
+      // past Nq read the last row and are never stored)
+      float4 gr[8];
+#pragma unroll
+      for (int t4 = 0; t4 < 8; ++t4) gr[t4] = *reinterpret_cast<const float4*>(grow + j0 + 32 * hf + 4 * t4);
+#pragma unroll
+      for (int t4 = 0; t4 < 8; ++t4) {
+        const float gv[4] = {gr[t4].x, gr[t4].y, gr[t4].z, gr[t4].w};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int jr = 32 * hf + 4 * t4 + s;
+#pragma unroll
+          for (int y = 0; y < 4; ++y)
+            acc[y] = __builtin_amdgcn_mfma_f32_32x32x2f32(gv[s], kt[jr * kKtRow + 32 * y + lr], acc[y], 0, 0, 0);
+        }
+      }
+      continue;
+    }
 #pragma unroll
     for (int t4 = 0; t4 < 8; ++t4) {
       float4 g4 = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -223,9 +242,11 @@ __global__ __launch_bounds__(kThreads, 2) void sim_bwd_u_kernel(SimParams p, flo
 }
 
 // Backward pass B:  W[b,hk,j,e] = sum_{h in group(hk)} sum_i G[b,h,i,j] Q_hat[b,h,i,e]
-// one workgroup = 128 keys x 128 expanded columns; 4 waves of 32 keys; the
-// A operand (lane <-> key j, k-slot <-> query i0 + 32*hf + t) is read from HBM
-// with coalesced 32-lane rows.
+// one workgroup = 128 keys x 128 expanded columns; wave w owns the 32 columns 32 w .. 32 w + 31
+// for all 128 keys.  Each lane loads four consecutive keys of a G row at once (16 bytes,
+// coalesced over the row): component s of lane l is key 4 l + s, so the four components feed
+// four MFMA row blocks whose rows are the keys 4 l + s -- no transposition of G is needed.
+// The B operand (Q_hat row i, column e) comes from the transformed tile in LDS.
 constexpr int kBI = 64;
 
 __global__ __launch_bounds__(kThreads, 2) void sim_bwd_w_kernel(SimParams p, float* W, int njb, int nec) {
@@ -235,7 +256,10 @@ __global__ __launch_bounds__(kThreads, 2) void sim_bwd_w_kernel(SimParams p, flo
   const int ec = id % nec, jb = (id / nec) % njb, bhk = id / (nec * njb);
   const int b = bhk / p.Hk, hk = bhk % p.Hk;
   const int R = p.R, E = p.E, Nq = p.Nq, Nk = p.Nk, q_off = Nk - Nq;
-  const int j = jb * 128 + wave * 32 + lr;
+  const int j4 = jb * 128 + 4 * lr;   // the lane's four keys
+  const bool vec = p.g_vec && j4 + 3 < Nk;
+  // every key of the workgroup in range and 16-byte rows: branch-free batched loads
+  const bool fast = p.g_vec && jb * 128 + 127 < Nk;
   const int e_base = ec * 128;
   const int groups = p.Hq / p.Hk;
 
@@ -267,27 +291,63 @@ __global__ __launch_bounds__(kThreads, 2) void sim_bwd_w_kernel(SimParams p, flo
         }
       }
       __syncthreads();
+      if (fast) {
+        // 16 rows of G per batch, all loads issued before the products (rows past Nq read the
+        // last row; their Q_hat rows are zero).  Row offsets fit 32 bits per (batch, head).
+        const float* g0 = gb + j4;
+        const int rs = (int)p.sim_s[2];
+#pragma unroll
+        for (int tc = 0; tc < 32; tc += 16) {
+          float4 gr[16];
+#pragma unroll
+          for (int u = 0; u < 16; ++u)
+            gr[u] = *reinterpret_cast<const float4*>(g0 + (uint32_t)(min(i0 + 32 * hf + tc + u, Nq - 1) * rs));
+#pragma unroll
+          for (int u = 0; u < 16; ++u) {
+            const float bq = qt[(32 * hf + tc + u) * kKtRow + 32 * wave + lr];
+            acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(gr[u].x, bq, acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(gr[u].y, bq, acc[1], 0, 0, 0);
+            acc[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(gr[u].z, bq, acc[2], 0, 0, 0);
+            acc[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(gr[u].w, bq, acc[3], 0, 0, 0);
+          }
+        }
+        continue;
+      }
 #pragma unroll 8
       for (int t = 0; t < 32; ++t) {
-        const int ii = i0 + 32 * hf + t;
-        const float gv = (ii < Nq && j < Nk) ? gb[(int64_t)ii * p.sim_s[2] + j] : 0.f;
-        const int ir = 32 * hf + t;
-#pragma unroll
-        for (int y = 0; y < 4; ++y)
-          acc[y] = __builtin_amdgcn_mfma_f32_32x32x2f32(gv, qt[ir * kKtRow + 32 * y + lr], acc[y], 0, 0, 0);
+        const int ii = i0 + 32 * hf + t;   // k-slot (t, hf)
+        float4 g4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (ii < Nq) {
+          const float* grow = gb + (int64_t)ii * p.sim_s[2];
+          if (vec) {
+            g4 = *reinterpret_cast<const float4*>(grow + j4);
+          } else {
+            g4.x = j4 < Nk ? grow[j4] : 0.f;
+            g4.y = j4 + 1 < Nk ? grow[j4 + 1] : 0.f;
+            g4.z = j4 + 2 < Nk ? grow[j4 + 2] : 0.f;
+            g4.w = j4 + 3 < Nk ? grow[j4 + 3] : 0.f;
+          }
+        }
+        const float bq = qt[(32 * hf + t) * kKtRow + 32 * wave + lr];
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(g4.x, bq, acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(g4.y, bq, acc[1], 0, 0, 0);
+        acc[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(g4.z, bq, acc[2], 0, 0, 0);
+        acc[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(g4.w, bq, acc[3], 0, 0, 0);
       }
     }
   }
-  float* wb = W + ((int64_t)b * p.Hk + hk) * Nk * p.EP;
+  // result lane <-> column e, register r <-> row 8 (r / 4) + 4 hf + r % 4 of block s, i.e. key
+  // 4 row + s
+  const int e = e_base + 32 * wave + lr;
+  if (e < p.EP) {
+    float* wb = W + ((int64_t)b * p.Hk + hk) * Nk * p.EP;
 #pragma unroll
-  for (int y = 0; y < 4; ++y) {
-    const int e = e_base + 32 * y + lr;
-    if (e >= p.EP) continue;
+    for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int jj = jb * 128 + wave * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-      if (jj < Nk) wb[(int64_t)jj * p.EP + e] = acc[y][r];
-    }
+      for (int r = 0; r < 16; ++r) {
+        const int jj = jb * 128 + 4 * (8 * (r >> 2) + 4 * hf + (r & 3)) + s4;
+        if (jj < Nk) wb[(int64_t)jj * p.EP + e] = acc[s4][r];
+      }
   }
 }
 
