@@ -17,9 +17,10 @@ Prints ONE JSON line.  ``value`` is TFLOP/s with the FA accounting of the
 metric: 3.5 * 4 * B * H * N^2 * D / 2 flops per causal fwd+bwd step.
 ``secondary`` carries the two other GPU configs of the path, measured in the
 same run on their own inputs: C5 decode (one query row against a 32k KV cache,
-HBM GB/s of the valid K/V rows) and C2 fused similarity fwd+bwd in fp32.
-``--workload decode`` / ``--workload sim`` run only that config (used to
-profile one workload at a time); the default ``train`` runs all three.
+HBM GB/s of the valid K/V rows), C2 fused similarity fwd+bwd in fp32 and C4
+axial flash attention fwd+bwd (D = 96, non-causal).  ``--workload decode`` /
+``sim`` / ``axial`` run only that config (used to profile one workload at a
+time); the default ``train`` runs all four.
 ``roofline`` covers the kernel with the largest share of the step time, timed
 by the library's own per-kernel hipEvents over a second pass of the same steps
 (each launch's dispatch stamps its start and end into an event pair on the
@@ -83,6 +84,7 @@ STEP_FLOPS = 3.5 * 4 * B * H * N * N * D / 2
 DEC_B, DEC_H, DEC_N, DEC_D, DEC_SEED = 8, 16, 32768, 64, 1005
 # C2 fused similarity: q, k (2,8,2048,64) fp32, PoPE(64, heads=8), dS N(0,1)
 SIM_B, SIM_H, SIM_N, SIM_D, SIM_SEED = 2, 8, 2048, 64, 1002
+AX_SEED = 1004
 PEAK_HBM_GBS = 8000.0
 PEAK_FP32_TFLOPS = 157.3
 
@@ -255,6 +257,55 @@ def sim_bench(steps: int, warmup: int):
     }
 
 
+def axial_bench(steps: int, warmup: int):
+    """C4: flash_attn_with_pope fwd+bwd in bf16, non-causal, no mask, AxialPoPE(96, heads=8,
+    axial_dims=(32, 32, 32)) on an (8, 16, 16) grid (N = 2048), B = 4, H = 8, D = 96.  FA flop
+    accounting: 3.5 * 4 * B * H * N^2 * D per step (non-causal)."""
+    import torch
+
+    import pope_amd
+    from pope_amd import _lib
+
+    B_, H_, D_, grid = 4, 8, 96, (8, 16, 16)
+    N_ = grid[0] * grid[1] * grid[2]
+    g = torch.Generator().manual_seed(AX_SEED)
+    dev = torch.device("cuda:0")
+    q, k, v, do = (torch.randn(B_, H_, N_, D_, generator=g).to(torch.bfloat16).to(dev) for _ in range(4))
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    freqs, bias = pope_amd.AxialPoPE(D_, heads=H_, axial_dims=(32, 32, 32)).to(dev)(grid)
+    bias = bias.detach().requires_grad_(True)
+
+    def step():
+        q.grad = k.grad = v.grad = bias.grad = None
+        o = pope_amd.flash_attn_with_pope(q, k, v, pos_emb=(freqs, bias))
+        o.backward(do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    el = (time.perf_counter() - t0) / steps
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_enable(False)
+    ks = _lib.profile_read()
+    flops = 3.5 * 4 * B_ * H_ * N_ * N_ * D_
+    return {
+        "workload": "C4 axial flash attention fwd+bwd: q, k, v (4,8,2048,96) bf16, AxialPoPE(96, heads=8, "
+                    "axial_dims=(32,32,32)) on an (8,16,16) grid, non-causal, no mask",
+        "ms_per_step": round(el * 1e3, 4), "TFLOPs": round(flops / el / 1e12, 2),
+        "frac_of_peak": round(flops / el / 1e12 / PEAK_BF16_TFLOPS, 4), "algorithmic_flops": flops,
+        "kernels_us": _kernel_us(ks, sorted(ks)),
+    }
+
+
 def cpu_baseline(min_seconds: float = 10.0, max_reps: int = 10):
     """The CPU oracle fwd+bwd over the whole C3 workload (every batch and head, two heads per
     call), fp32 after the bf16 cast (the reference's PyTorch path promotes after softplus,
@@ -305,9 +356,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("train", "decode", "sim"), default="train",
-                    help="train (default): the C3 headline line with C5 and C2 as secondary; "
-                         "decode / sim: only that config's measurement")
+    ap.add_argument("--workload", choices=("train", "decode", "sim", "axial"), default="train",
+                    help="train (default): the C3 headline line with C5, C2 and C4 as secondary; "
+                         "decode / sim / axial: only that config's measurement")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {a.gpus} is not supported "
@@ -315,7 +366,7 @@ def main():
         sys.exit(2)
 
     if a.workload != "train":
-        fn = decode_bench if a.workload == "decode" else sim_bench
+        fn = {"decode": decode_bench, "sim": sim_bench, "axial": axial_bench}[a.workload]
         print(json.dumps({"workload": a.workload, "steps": a.steps, "warmup": a.warmup,
                           **fn(a.steps, a.warmup)}), flush=True)
         return
@@ -348,7 +399,8 @@ def main():
         "frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
         "roofline": roofline,
         "kernels": breakdown,
-        "secondary": {"decode_c5": decode_bench(a.steps, a.warmup), "sim_c2": sim_bench(a.steps, a.warmup)},
+        "secondary": {"decode_c5": decode_bench(a.steps, a.warmup), "sim_c2": sim_bench(a.steps, a.warmup),
+                      "axial_c4": axial_bench(a.steps, a.warmup)},
     }
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
