@@ -45,7 +45,7 @@ enum pope_status {
 enum pope_op { POPE_OP_SIM_FWD = 0, POPE_OP_SIM_BWD = 1, POPE_OP_FLASH_FWD = 2,
                POPE_OP_FLASH_BWD = 3, POPE_OP_FLASH_DECODE = 4 };
 
-/* pope_desc.flags (flash backward only; 0 everywhere else). */
+/* pope_desc.flags (flash backward: PREPARED, ZERO_GRADS; similarity: SPLIT_BF16; 0 elsewhere). */
 enum pope_flags {
   /* The workspace holds the preparation (expanded K/Q rows, phase tables, key visibility)
    * written by a pope_flash_fwd call with the same descriptor, q, k, freqs, bias and mask,
@@ -54,7 +54,12 @@ enum pope_flags {
   POPE_FLAG_PREPARED = 1,
   /* dfreqs / dbias are overwritten (cleared by the library before it accumulates into them)
    * instead of accumulated into. */
-  POPE_FLAG_ZERO_GRADS = 2
+  POPE_FLAG_ZERO_GRADS = 2,
+  /* Similarity forward / backward: the products run on bf16 MFMA with every fp32 operand split
+   * into hi + lo bf16 halves (three products per pair, 16 significant operand bits, fp32
+   * accumulation) -- the counterpart of the reference's default allow_tf32=True (TF32 keeps 10
+   * bits, triton_pope.py:63,145,224).  Without it the products are true fp32 MFMA. */
+  POPE_FLAG_SPLIT_BF16 = 4
 };
 
 /*

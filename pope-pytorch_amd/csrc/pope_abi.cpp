@@ -193,6 +193,8 @@ size_t sim_table_q(const pope_desc& d) {
   const int Hqt = d.f_s[1] != 0 ? d.Hq : 1;
   return d.R > 0 ? align_up((size_t)Bt * Hqt * d.Nk * d.R * sizeof(float2)) : 0;
 }
+// Similarity workspace: [key table | query table | (backward) U | W | (split) Q_hat hi | lo |
+// K_hat hi | lo planes, rows padded to 128].
 size_t sim_ws(const pope_desc& d, int op) {
   const int EP = round_up(d.D + d.R, 32);
   size_t n = sim_table_k(d) + sim_table_q(d);
@@ -200,7 +202,39 @@ size_t sim_ws(const pope_desc& d, int op) {
     n += align_up((size_t)d.B * d.Hq * d.Nq * EP * sizeof(float));
     n += align_up((size_t)d.B * d.Hk * d.Nk * EP * sizeof(float));
   }
+  if (d.flags & POPE_FLAG_SPLIT_BF16) {
+    n += 2 * align_up((size_t)d.B * d.Hq * round_up(d.Nq, 128) * EP * sizeof(uint16_t));
+    n += 2 * align_up((size_t)d.B * d.Hk * round_up(d.Nk, 128) * EP * sizeof(uint16_t));
+    if (op == POPE_OP_SIM_BWD) {   // second partial sums of U and W
+      n += align_up((size_t)d.B * d.Hq * d.Nq * EP * sizeof(float));
+      n += align_up((size_t)d.B * d.Hk * d.Nk * EP * sizeof(float));
+    }
+  }
   return n;
+}
+
+// The split planes at the end of the similarity workspace.
+pope::SimSplit sim_split_planes(const pope_desc& d, char* ws, int op) {
+  const int EP = round_up(d.D + d.R, 32);
+  pope::SimSplit sp;
+  sp.NqP = round_up(d.Nq, 128);
+  sp.NkP = round_up(d.Nk, 128);
+  size_t off = sim_table_k(d) + sim_table_q(d);
+  if (op == POPE_OP_SIM_BWD)
+    off += align_up((size_t)d.B * d.Hq * d.Nq * EP * sizeof(float)) + align_up((size_t)d.B * d.Hk * d.Nk * EP * sizeof(float));
+  const size_t qb = align_up((size_t)d.B * d.Hq * sp.NqP * EP * sizeof(uint16_t));
+  const size_t kb = align_up((size_t)d.B * d.Hk * sp.NkP * EP * sizeof(uint16_t));
+  sp.qh = reinterpret_cast<uint16_t*>(ws + off);
+  sp.ql = reinterpret_cast<uint16_t*>(ws + off + qb);
+  sp.kh = reinterpret_cast<uint16_t*>(ws + off + 2 * qb);
+  sp.kl = reinterpret_cast<uint16_t*>(ws + off + 2 * qb + kb);
+  sp.U2 = sp.W2 = nullptr;
+  if (op == POPE_OP_SIM_BWD) {
+    const size_t o2 = off + 2 * qb + 2 * kb;
+    sp.U2 = reinterpret_cast<float*>(ws + o2);
+    sp.W2 = reinterpret_cast<float*>(ws + o2 + align_up((size_t)d.B * d.Hq * d.Nq * EP * sizeof(float)));
+  }
+  return sp;
 }
 
 // Decode workspace: [fp16 cos/sin table | partial O (rows, splits, D) | partial (m, l)
@@ -272,6 +306,7 @@ int check_sim_common(const pope_desc* d, const void* q, const void* k, const flo
   int rc = check_desc(d);
   if (rc) return rc;
   if (d->dtype != POPE_F32) return fail(POPE_ERR_UNSUPPORTED, "similarity kernels take fp32 (dtype %d)", d->dtype);
+  if (d->flags & ~POPE_FLAG_SPLIT_BF16) return fail(POPE_ERR_INVALID, "unknown flags 0x%x", (unsigned)d->flags);
   if (d->D > 256) return fail(POPE_ERR_UNSUPPORTED, "similarity covers head dim <= 256 (got %d)", d->D);
   if (!q || !k) return fail(POPE_ERR_INVALID, "q, k must be non-NULL");
   if (!aligned16(q) || !aligned16(k)) return fail(POPE_ERR_INVALID, "q, k must be 16-byte aligned");
@@ -531,7 +566,10 @@ int pope_sim_fwd(const pope_desc* d, const void* q, const void* k, const float* 
   hipError_t e = sim_setup(*d, q, k, freqs, bias, static_cast<char*>(workspace), s, &p);
   if (e != hipSuccess) return hip_fail(e, "phase table launch");
   p.sim = static_cast<float*>(sim);
-  e = pope::launch_sim_fwd(p, s);
+  if (d->flags & POPE_FLAG_SPLIT_BF16)
+    e = pope::launch_sim_split_fwd(p, sim_split_planes(*d, static_cast<char*>(workspace), POPE_OP_SIM_FWD), s);
+  else
+    e = pope::launch_sim_fwd(p, s);
   if (e != hipSuccess) return hip_fail(e, "similarity forward launch");
   return POPE_OK;
 }
@@ -569,7 +607,10 @@ int pope_sim_bwd(const pope_desc* d, const void* dsim, const void* q, const void
   const size_t off_u = sim_table_k(*d) + sim_table_q(*d);
   float* U = reinterpret_cast<float*>(ws + off_u);
   float* W = reinterpret_cast<float*>(ws + off_u + align_up((size_t)d->B * d->Hq * d->Nq * p.EP * sizeof(float)));
-  e = pope::launch_sim_bwd_ws(p, U, W, s);
+  if (d->flags & POPE_FLAG_SPLIT_BF16)
+    e = pope::launch_sim_split_bwd(p, sim_split_planes(*d, ws, POPE_OP_SIM_BWD), U, W, s);
+  else
+    e = pope::launch_sim_bwd_ws(p, U, W, s);
   if (e != hipSuccess) return hip_fail(e, "similarity backward launch");
   return POPE_OK;
 }

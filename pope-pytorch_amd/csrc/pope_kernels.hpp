@@ -118,6 +118,21 @@ struct SimParams {
 hipError_t launch_sim_fwd(const SimParams& p, hipStream_t s);
 // U: (B, Hq, Nq, EP) and W: (B, Hk, Nk, EP) fp32 workspace.
 hipError_t launch_sim_bwd_ws(const SimParams& p, float* U, float* W, hipStream_t s);
+// Chain rule of the polar transform on U (queries) and W (keys) (sim.hip); U2 / W2 are second
+// partial sums added to them, or null.
+hipError_t launch_sim_finalize(const SimParams& p, const float* U, const float* U2, const float* W, const float* W2,
+                               hipStream_t s);
+
+// Split-bf16 similarity (sim_split.hip): hi / lo bf16 planes of Q_hat and K_hat, rows padded
+// to 128, row-major (heads, NP, EP) for the forward or transposed (heads, EP, NP) for the
+// backward.
+struct SimSplit {
+  uint16_t* qh; uint16_t* ql; uint16_t* kh; uint16_t* kl;
+  int NqP, NkP;
+  float* U2; float* W2;      // backward: second partial sums of U and W (split reduction)
+};
+hipError_t launch_sim_split_fwd(const SimParams& p, const SimSplit& sp, hipStream_t s);
+hipError_t launch_sim_split_bwd(const SimParams& p, const SimSplit& sp, float* U, float* W, hipStream_t s);
 
 struct DecodeParams {
   const uint16_t* q; const uint16_t* k; const uint16_t* v;

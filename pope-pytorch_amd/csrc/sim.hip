@@ -355,8 +355,8 @@ __global__ __launch_bounds__(kThreads, 2) void sim_bwd_w_kernel(SimParams p, flo
 //   side 0: rows = queries of (b, h), acc = U, out = dq, phase row = q_off + i, no bias
 //   side 1: rows = keys of (b, hk), acc = W, out = dk, phase row = j, dbias accumulated
 // one workgroup = 32 rows of one (b, head); thread -> (dim lane, row group).
-__global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p, const float* acc, int side,
-                                                                     int nrb) {
+__global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p, const float* acc, const float* acc2,
+                                                                     int side, int nrb) {
   __shared__ float red[4][256];
   const int tid = threadIdx.x;
   const int rb = blockIdx.x % nrb, bh = blockIdx.x / nrb;
@@ -375,6 +375,8 @@ __global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p,
   if (R) tab = side == 0 ? p.qtab + (int64_t)b * p.qt_sb + (int64_t)hh * p.qt_sh
                          : p.ktab + (int64_t)b * p.kt_sb + (int64_t)hh * p.kt_sh;
   const float* ab = acc + (int64_t)bh * rows * EP;
+  // a second partial sum (split reduction of the split-bf16 path), added when present
+  const float* ab2 = acc2 ? acc2 + (int64_t)bh * rows * EP : nullptr;
   const int dl = tid & 63, rg = tid >> 6;
 
   for (int d0 = 0; d0 < D; d0 += 64) {
@@ -384,17 +386,18 @@ __global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p,
       const int n = rb * 32 + rr;
       if (n >= rows || d >= D) continue;
       const float* arow = ab + (int64_t)n * EP;
+      const float* arow2 = ab2 ? ab2 + (int64_t)n * EP : nullptr;
       if (d < R) {
         const int prow = side == 0 ? q_off + n : n;
         const float2 cs = tab[(int64_t)prow * R + d];
         const float xv = x[(int64_t)n * xs + d];
-        const float uc = arow[d], us = arow[R + d];
+        const float uc = arow[d] + (arow2 ? arow2[d] : 0.f), us = arow[R + d] + (arow2 ? arow2[R + d] : 0.f);
         out[(int64_t)n * os + d] = sigmoid_f(xv) * (cs.x * uc + cs.y * us);
         const float dph = softplus_f(xv) * (cs.x * us - cs.y * uc);
         if (p.dfreqs) atomicAdd(p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)hh * p.df_s[1] + (int64_t)prow * p.df_s[2] + d, dph);
         dpsum += dph;
       } else {
-        out[(int64_t)n * os + d] = arow[R + d];
+        out[(int64_t)n * os + d] = arow[R + d] + (arow2 ? arow2[R + d] : 0.f);
       }
     }
     if (side == 1 && p.dbias) {
@@ -427,12 +430,18 @@ hipError_t launch_sim_bwd_ws(const SimParams& p, float* U, float* W, hipStream_t
   if (e != hipSuccess) return e;
   e = launch_named("sim_bwd_w", sim_bwd_w_kernel, dim3(njb * nec * p.B * p.Hk), dim3(kThreads), s, p, W, njb, nec);
   if (e != hipSuccess) return e;
+  return launch_sim_finalize(p, U, nullptr, W, nullptr, s);
+}
+
+hipError_t launch_sim_finalize(const SimParams& p, const float* U, const float* U2, const float* W, const float* W2,
+                               hipStream_t s) {
+  hipError_t e;
   const int nrq = (p.Nq + 31) / 32, nrk = (p.Nk + 31) / 32;
   e = launch_named("sim_bwd_finalize_q", sim_bwd_finalize_kernel, dim3(nrq * p.B * p.Hq), dim3(kThreads), s, p,
-                   (const float*)U, 0, nrq);
+                   U, U2, 0, nrq);
   if (e != hipSuccess) return e;
   return launch_named("sim_bwd_finalize_k", sim_bwd_finalize_kernel, dim3(nrk * p.B * p.Hk), dim3(kThreads), s, p,
-                      (const float*)W, 1, nrk);
+                      W, W2, 1, nrk);
 }
 
 }  // namespace pope

@@ -1,0 +1,475 @@
+// Fused PoPE similarity on bf16 MFMA with split operands (gfx950).
+//
+// The fp32 products of the similarity (triton_pope.py:28-256; sim.hip for the fp32 MFMA path)
+// run here as three bf16 products: every fp32 operand x is split into hi = bf16(x) and
+// lo = bf16(x - hi), and a . b = hi_a hi_b + hi_a lo_b + lo_a hi_b (+ lo_a lo_b, dropped, below
+// 2^-16 of |a||b|), accumulated in fp32 by v_mfma_f32_32x32x16_bf16.  Operands carry 16
+// significant bits: more than the TF32 (10 bits) the reference multiplies in by default
+// (allow_tf32=True, triton_pope.py:63,145,224), less than fp32 (24 bits), which the fp32 MFMA
+// path keeps for allow_tf32=False.  Per product MAC the bf16 MFMA does 16x the fp32 MFMA rate,
+// so the three products take about a fifth of the fp32 time.
+//
+// Kernels
+//   sim_split_prep : the expanded rows Q_hat / K_hat (columns [a cos | a sin | rest], the
+//                    reference's rounding of the key phase fl(F_j + bias), pope.py:56) split
+//                    into hi / lo bf16 planes, row-major (forward) or transposed (backward);
+//   sim_split_fwd  : S = Q_hat K_hat^T, one 128 x 128 tile per workgroup;
+//   sim_split_u    : U = G K_hat (G = dS read from HBM and split on the fly);
+//   sim_split_w    : W = G^T Q_hat (G tiles split once per workgroup into LDS, transposed).
+// The chain rule of the polar transform then runs in sim.hip's finalize kernel on U and W.
+#include "pope_common.hpp"
+#include "pope_kernels.hpp"
+
+namespace pope {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Splits 8 fp32 values into bf16 hi / lo planes (round to nearest even both times).
+__device__ __forceinline__ void split8(const float* v, u32x4& hi, u32x4& lo) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const uint32_t h = BF16::pack2(v[2 * s], v[2 * s + 1]);
+    hi[s] = h;
+    lo[s] = BF16::pack2(v[2 * s] - __uint_as_float(h << 16), v[2 * s + 1] - __uint_as_float(h & 0xffff0000u));
+  }
+}
+
+__device__ __forceinline__ f32x16 mfma3(u32x4 ah, u32x4 al, u32x4 bh, u32x4 bl, f32x16 c) {
+  typedef BF16::vec8 v8;
+  c = BF16::mfma32(as_vec8<v8>(al), as_vec8<v8>(bh), c);
+  c = BF16::mfma32(as_vec8<v8>(ah), as_vec8<v8>(bl), c);
+  return BF16::mfma32(as_vec8<v8>(ah), as_vec8<v8>(bh), c);
+}
+
+// Expanded 8 columns [e0, e0 + 8) of one row (zeros past the row count or past E); the same
+// transform as the fp32 path (sim.hip).
+__device__ __forceinline__ void expand_row8(const float* x, const float2* tab, int e0, int R, int E, bool valid,
+                                            float* out) {
+  if (!valid || e0 >= E) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) out[s] = 0.f;
+    return;
+  }
+  const bool is_cos = e0 < R, is_sin = !is_cos && e0 < 2 * R;
+  const int d0 = is_cos ? e0 : e0 - R;
+  const float4 x0 = *reinterpret_cast<const float4*>(x + d0);
+  const float4 x1 = *reinterpret_cast<const float4*>(x + d0 + 4);
+  const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  if (is_cos || is_sin) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const float2 cs = tab[d0 + s];
+      out[s] = softplus_f(xv[s]) * (is_cos ? cs.x : cs.y);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) out[s] = xv[s];
+  }
+}
+
+// One thread per (row, 8 expanded columns).  side 0: query rows of (b, h) (phase row
+// q_off + i, no bias); side 1: key rows of (b, hk) (phase fl(F_j + bias)).  transposed = 0:
+// planes (heads, NP, EP); 1: planes (heads, EP, NP), rows fastest over threads so that each
+// 2-byte store of a wave covers 64 consecutive rows.
+__global__ __launch_bounds__(kThreads) void sim_split_prep_kernel(SimParams p, SimSplit sp, int side, int transposed) {
+  const int heads = side == 0 ? p.B * p.Hq : p.B * p.Hk;
+  const int N = side == 0 ? p.Nq : p.Nk, NP = side == 0 ? sp.NqP : sp.NkP;
+  const int nch = p.EP / 8;
+  const int64_t total = (int64_t)heads * NP * nch;
+  const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (idx >= total) return;
+  int bh, n, ch;
+  if (transposed) {
+    n = (int)(idx % NP);
+    const int64_t r = idx / NP;
+    ch = (int)(r % nch);
+    bh = (int)(r / nch);
+  } else {
+    ch = (int)(idx % nch);
+    const int64_t r = idx / nch;
+    n = (int)(r % NP);
+    bh = (int)(r / NP);
+  }
+  const int R = p.R, q_off = p.Nk - p.Nq;
+  const int nn = min(n, N - 1);
+  const float* x;
+  const float2* tab = nullptr;
+  if (side == 0) {
+    const int b = bh / p.Hq, h = bh % p.Hq;
+    x = p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + (int64_t)nn * p.q_s[2];
+    if (R) tab = p.qtab + (int64_t)b * p.qt_sb + (int64_t)h * p.qt_sh + (int64_t)(q_off + nn) * R;
+  } else {
+    const int b = bh / p.Hk, hk = bh % p.Hk;
+    x = p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1] + (int64_t)nn * p.k_s[2];
+    if (R) tab = p.ktab + (int64_t)b * p.kt_sb + (int64_t)hk * p.kt_sh + (int64_t)nn * R;
+  }
+  float v[8];
+  expand_row8(x, tab, 8 * ch, R, p.E, n < N, v);
+  u32x4 hi, lo;
+  split8(v, hi, lo);
+  uint16_t* ph = side == 0 ? sp.qh : sp.kh;
+  uint16_t* pl = side == 0 ? sp.ql : sp.kl;
+  if (!transposed) {
+    const int64_t o = ((int64_t)bh * NP + n) * p.EP + 8 * ch;
+    *reinterpret_cast<u32x4*>(ph + o) = hi;
+    *reinterpret_cast<u32x4*>(pl + o) = lo;
+  } else {
+    const int64_t o = ((int64_t)bh * p.EP + 8 * ch) * NP + n;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      ph[o + (int64_t)s * NP] = (uint16_t)((s & 1) ? hi[s >> 1] >> 16 : hi[s >> 1] & 0xffffu);
+      pl[o + (int64_t)s * NP] = (uint16_t)((s & 1) ? lo[s >> 1] >> 16 : lo[s >> 1] & 0xffffu);
+    }
+  }
+}
+
+// Operand tiles in LDS: [hi, lo plane][128 rows][32 k values + 8 pad] bf16.  The 80-byte row
+// stride keeps the 16-byte reads of 16 consecutive rows on distinct banks.  A tile is loaded
+// once per workgroup (thread t: chunks t + 256 m, m < 4, of 16 bytes) and read by every wave.
+constexpr int kLd = 40;
+constexpr int kTile = 2 * 128 * kLd;   // bf16 per tile (both planes)
+
+// Loads rows [0, 128) x k values [k0, k0 + 32) of two planes (row stride rs elements); rows at
+// or past nrows read as zero.
+__device__ __forceinline__ void tile_load(const uint16_t* ph, const uint16_t* pl, int64_t rs, int k0, int nrows,
+                                          u32x4* v, int tid) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int c = tid + kThreads * m, plane = c >> 9, row = (c >> 2) & 127, kc = c & 3;
+    const uint16_t* base = plane ? pl : ph;
+    v[m] = row < nrows ? ld16(base + row * rs + k0 + 8 * kc) : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+__device__ __forceinline__ void tile_store(uint16_t* t, const u32x4* v, int tid) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int c = tid + kThreads * m, plane = c >> 9, row = (c >> 2) & 127, kc = c & 3;
+    *reinterpret_cast<u32x4*>(t + plane * 128 * kLd + row * kLd + 8 * kc) = v[m];
+  }
+}
+// MFMA operand of rows r .. r + 31 (lane = row r + lane % 32), 16-wide k step u: the hi and lo
+// planes' 8 values at k = 16 u + 8 (lane / 32).
+__device__ __forceinline__ void tile_frag(const uint16_t* t, int r, int u, int lr, int hf, u32x4& hi, u32x4& lo) {
+  const int o = (r + lr) * kLd + 16 * u + 8 * hf;
+  hi = *reinterpret_cast<const u32x4*>(t + o);
+  lo = *reinterpret_cast<const u32x4*>(t + 128 * kLd + o);
+}
+
+// Forward: one workgroup = 128 x 128 tile of S; 4 waves of 64 x 64 (2 x 2 blocks of 32 x 32).
+// Per 32 expanded columns the Q_hat and K_hat tiles go through LDS (double-buffered: the next
+// step's loads are in flight during the products).
+__global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p, SimSplit sp, int nib, int njb) {
+  __shared__ __attribute__((aligned(16))) uint16_t ts[2][2][kTile];   // [buffer][Q_hat, K_hat]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int jb = id % njb, ib = (id / njb) % nib, bh = id / (njb * nib);
+  const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
+  const int EP = p.EP;
+  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+  const int64_t qo = ((int64_t)bh * sp.NqP + ib * 128) * EP;
+  const int64_t ko = ((int64_t)(b * p.Hk + hk) * sp.NkP + jb * 128) * EP;
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
+
+  u32x4 va[4], vb[4];
+  const int nst = EP / 32;
+  tile_load(sp.qh + qo, sp.ql + qo, EP, 0, 128, va, tid);
+  tile_load(sp.kh + ko, sp.kl + ko, EP, 0, 128, vb, tid);
+  tile_store(ts[0][0], va, tid);
+  tile_store(ts[0][1], vb, tid);
+  __syncthreads();
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nst) {
+      tile_load(sp.qh + qo, sp.ql + qo, EP, 32 * (st + 1), 128, va, tid);
+      tile_load(sp.kh + ko, sp.kl + ko, EP, 32 * (st + 1), 128, vb, tid);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      u32x4 ah[2], al[2], bh16[2], bl16[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        tile_frag(ts[buf][0], wr + 32 * x, u, lr, hf, ah[x], al[x]);
+        tile_frag(ts[buf][1], wc + 32 * x, u, lr, hf, bh16[x], bl16[x]);
+      }
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) acc[x][y] = mfma3(ah[x], al[x], bh16[y], bl16[y], acc[x][y]);
+    }
+    if (st + 1 < nst) {
+      tile_store(ts[buf ^ 1][0], va, tid);   // the other buffer: its last readers passed the barrier
+      tile_store(ts[buf ^ 1][1], vb, tid);
+    }
+    __syncthreads();
+  }
+
+  float* sbase = p.sim + (int64_t)b * p.sim_s[0] + (int64_t)h * p.sim_s[1];
+  const int i0 = ib * 128 + wr, j0 = jb * 128 + wc;
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int j = j0 + 32 * y + lr;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = i0 + 32 * x + 8 * (r >> 2) + 4 * hf + (r & 3);
+        if (i < p.Nq && j < p.Nk) sbase[(int64_t)i * p.sim_s[2] + j] = acc[x][y][r];
+      }
+    }
+}
+
+// U[b,h,i,e] = sum_j G[b,h,i,j] K_hat[b,hk,j,e] over half of the keys (two halves, the second
+// into sp.U2: twice the waves of one full pass; the finalize adds them).  One workgroup = 128
+// query rows x 128 expanded columns; wave w owns rows 32 w .. 32 w + 31 and all four column
+// blocks, so each G value is loaded and split once.  A = G rows (lane = row, 8 consecutive
+// keys, 32 bytes, split on the fly); B = the transposed K_hat planes (128 columns e x 32 keys)
+// through LDS, loaded once per workgroup and double-buffered.
+__global__ __launch_bounds__(kThreads, 2) void sim_split_u_kernel(SimParams p, SimSplit sp, float* U, int nib, int nec) {
+  __shared__ __attribute__((aligned(16))) uint16_t ts[2][kTile];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int half = id & 1, rest = id >> 1;
+  const int ec = rest % nec, ib = (rest / nec) % nib, bh = rest / (nec * nib);
+  const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
+  const int Nq = p.Nq, Nk = p.Nk, EP = p.EP;
+  const int i = ib * 128 + 32 * wave + lr;
+  const float* grow = p.dsim + (int64_t)b * p.sim_s[0] + (int64_t)h * p.sim_s[1] + (int64_t)min(i, Nq - 1) * p.sim_s[2];
+  const int nst = (Nk + 31) / 32, hst = (nst + 1) / 2;
+  const int s0 = half * hst, s1 = min(nst, s0 + hst);
+  const int64_t bo = ((int64_t)(b * p.Hk + hk) * EP + ec * 128) * sp.NkP;
+  const int erows = min(128, EP - ec * 128);
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int y = 0; y < 4; ++y)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[y][r] = 0.f;
+
+  // G of 32 keys: sub-step u covers keys j0 + 16 u + 8 hf .. + 8
+  auto load_g = [&](int j0, float* g) {
+    if (p.g_vec && j0 + 32 <= Nk) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const float4 a = *reinterpret_cast<const float4*>(grow + j0 + 16 * u + 8 * hf);
+        const float4 c = *reinterpret_cast<const float4*>(grow + j0 + 16 * u + 8 * hf + 4);
+        g[8 * u + 0] = a.x; g[8 * u + 1] = a.y; g[8 * u + 2] = a.z; g[8 * u + 3] = a.w;
+        g[8 * u + 4] = c.x; g[8 * u + 5] = c.y; g[8 * u + 6] = c.z; g[8 * u + 7] = c.w;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int j = j0 + 16 * u + 8 * hf + t;
+          g[8 * u + t] = j < Nk ? grow[j] : 0.f;
+        }
+    }
+  };
+  float g[16];
+  u32x4 vb[4];
+  if (s0 < s1) {
+    load_g(32 * s0, g);
+    tile_load(sp.kh + bo, sp.kl + bo, sp.NkP, 32 * s0, erows, vb, tid);
+    tile_store(ts[0], vb, tid);
+  }
+  __syncthreads();
+  for (int st = s0; st < s1; ++st) {
+    const int buf = (st - s0) & 1;
+    u32x4 ah[2], al[2];
+    split8(g, ah[0], al[0]);
+    split8(g + 8, ah[1], al[1]);
+    if (st + 1 < s1) {
+      load_g(32 * (st + 1), g);
+      tile_load(sp.kh + bo, sp.kl + bo, sp.NkP, 32 * (st + 1), erows, vb, tid);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        u32x4 bh16, bl16;
+        tile_frag(ts[buf], 32 * y, u, lr, hf, bh16, bl16);
+        acc[y] = mfma3(ah[u], al[u], bh16, bl16, acc[y]);
+      }
+    if (st + 1 < s1) tile_store(ts[buf ^ 1], vb, tid);
+    __syncthreads();
+  }
+
+  float* ub = (half ? sp.U2 : U) + (int64_t)bh * Nq * EP;
+#pragma unroll
+  for (int y = 0; y < 4; ++y) {
+    const int e = ec * 128 + 32 * y + lr;
+    if (e >= EP) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int ii = ib * 128 + 32 * wave + 8 * (r >> 2) + 4 * hf + (r & 3);
+      if (ii < Nq) ub[(int64_t)ii * EP + e] = acc[y][r];
+    }
+  }
+}
+
+// W[b,hk,j,e] = sum_{h in group(hk)} sum_i G[b,h,i,j] Q_hat[b,h,i,e] over half of the (query
+// head, 32-query step) sequence (the second half into sp.W2).  One workgroup = 128 keys x 128
+// expanded columns.  Per step the 32 x 128 G tile is loaded coalesced (thread: 4 rows x 4 keys),
+// split once and stored key-major in LDS, so the A operand (lane = key, 8 consecutive queries)
+// is one 16-byte LDS read per plane; the transposed Q_hat planes (128 columns e x 32 queries)
+// go through LDS the same way.  Both double-buffered.  Wave w owns keys 32 w .. 32 w + 31 and
+// all four column blocks.
+__global__ __launch_bounds__(kThreads, 2) void sim_split_w_kernel(SimParams p, SimSplit sp, float* W, int njb, int nec) {
+  __shared__ __attribute__((aligned(16))) uint16_t gs[2][kTile];   // G^T tiles (key-major)
+  __shared__ __attribute__((aligned(16))) uint16_t qs[2][kTile];   // Q_hat^T tiles (column-major)
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int half = id & 1, rest = id >> 1;
+  const int ec = rest % nec, jb = (rest / nec) % njb, bhk = rest / (nec * njb);
+  const int b = bhk / p.Hk, hk = bhk % p.Hk;
+  const int Nq = p.Nq, Nk = p.Nk, EP = p.EP;
+  const int groups = p.Hq / p.Hk;
+  const int nis = (Nq + 31) / 32;              // 32-query steps per head
+  const int nst = groups * nis, hst = (nst + 1) / 2;
+  const int s0 = half * hst, s1 = min(nst, s0 + hst);
+  const int erows = min(128, EP - ec * 128);
+  // G tile loader: thread -> key quad c (keys 4 c .. 4 c + 3), rows 4 rg .. 4 rg + 3 of the step
+  const int c = tid & 31, rg = tid >> 5;
+  const int jq = jb * 128 + 4 * c;
+  const bool vec = p.g_vec && jq + 3 < Nk;
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int y = 0; y < 4; ++y)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[y][r] = 0.f;
+
+  auto load_g = [&](int st, float4* g) {
+    const int h = hk + (st / nis) * p.Hk, i0 = (st % nis) * 32;
+    const float* gb = p.dsim + (int64_t)b * p.sim_s[0] + (int64_t)h * p.sim_s[1];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int ii = i0 + 4 * rg + t;
+      const float* row = gb + (int64_t)min(ii, Nq - 1) * p.sim_s[2];
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (ii < Nq) {
+        if (vec) {
+          v = *reinterpret_cast<const float4*>(row + jq);
+        } else {
+          v.x = jq < Nk ? row[jq] : 0.f;
+          v.y = jq + 1 < Nk ? row[jq + 1] : 0.f;
+          v.z = jq + 2 < Nk ? row[jq + 2] : 0.f;
+          v.w = jq + 3 < Nk ? row[jq + 3] : 0.f;
+        }
+      }
+      g[t] = v;
+    }
+  };
+  // split the thread's 4 x 4 patch; key s gets 4 consecutive queries: one 8-byte store per plane
+  auto store_g = [&](uint16_t* t, const float4* g) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = s == 0 ? g[q].x : s == 1 ? g[q].y : s == 2 ? g[q].z : g[q].w;
+      const uint32_t h0 = BF16::pack2(v[0], v[1]), h1 = BF16::pack2(v[2], v[3]);
+      const uint32_t l0 = BF16::pack2(v[0] - __uint_as_float(h0 << 16), v[1] - __uint_as_float(h0 & 0xffff0000u));
+      const uint32_t l1 = BF16::pack2(v[2] - __uint_as_float(h1 << 16), v[3] - __uint_as_float(h1 & 0xffff0000u));
+      const int o = (4 * c + s) * kLd + 4 * rg;
+      *reinterpret_cast<u32x2*>(t + o) = u32x2{h0, h1};
+      *reinterpret_cast<u32x2*>(t + 128 * kLd + o) = u32x2{l0, l1};
+    }
+  };
+  auto load_q = [&](int st, u32x4* v) {
+    const int h = hk + (st / nis) * p.Hk, i0 = (st % nis) * 32;
+    const int64_t qo = ((int64_t)(b * p.Hq + h) * EP + ec * 128) * sp.NqP;
+    tile_load(sp.qh + qo, sp.ql + qo, sp.NqP, i0, erows, v, tid);
+  };
+  float4 gr[4];
+  u32x4 vq[4];
+  if (s0 < s1) {
+    load_g(s0, gr);
+    load_q(s0, vq);
+    store_g(gs[0], gr);
+    tile_store(qs[0], vq, tid);
+  }
+  __syncthreads();
+  for (int st = s0; st < s1; ++st) {
+    const int buf = (st - s0) & 1;
+    if (st + 1 < s1) {
+      load_g(st + 1, gr);
+      load_q(st + 1, vq);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      u32x4 ah, al;
+      tile_frag(gs[buf], 32 * wave, u, lr, hf, ah, al);
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        u32x4 bh16, bl16;
+        tile_frag(qs[buf], 32 * y, u, lr, hf, bh16, bl16);
+        acc[y] = mfma3(ah, al, bh16, bl16, acc[y]);
+      }
+    }
+    if (st + 1 < s1) {
+      store_g(gs[buf ^ 1], gr);
+      tile_store(qs[buf ^ 1], vq, tid);
+    }
+    __syncthreads();
+  }
+
+  float* wb = (half ? sp.W2 : W) + (int64_t)bhk * Nk * EP;
+#pragma unroll
+  for (int y = 0; y < 4; ++y) {
+    const int e = ec * 128 + 32 * y + lr;
+    if (e >= EP) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int jj = jb * 128 + 32 * wave + 8 * (r >> 2) + 4 * hf + (r & 3);
+      if (jj < Nk) wb[(int64_t)jj * EP + e] = acc[y][r];
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_sim_split_prep(const SimParams& p, const SimSplit& sp, int transposed, hipStream_t s) {
+  for (int side = 0; side < 2; ++side) {
+    const int heads = side == 0 ? p.B * p.Hq : p.B * p.Hk;
+    const int64_t total = (int64_t)heads * (side == 0 ? sp.NqP : sp.NkP) * (p.EP / 8);
+    const hipError_t e = launch_named("sim_split_prep", sim_split_prep_kernel, dim3((unsigned)((total + kThreads - 1) / kThreads)),
+                                      dim3(kThreads), s, p, sp, side, transposed);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_sim_split_fwd(const SimParams& p, const SimSplit& sp, hipStream_t s) {
+  hipError_t e = launch_sim_split_prep(p, sp, 0, s);
+  if (e != hipSuccess) return e;
+  const int nib = (p.Nq + 127) / 128, njb = (p.Nk + 127) / 128;
+  return launch_named("sim_split_fwd", sim_split_fwd_kernel, dim3(nib * njb * p.B * p.Hq), dim3(kThreads), s, p, sp,
+                      nib, njb);
+}
+
+hipError_t launch_sim_split_bwd(const SimParams& p, const SimSplit& sp, float* U, float* W, hipStream_t s) {
+  hipError_t e = launch_sim_split_prep(p, sp, 1, s);
+  if (e != hipSuccess) return e;
+  const int nec = (p.EP + 127) / 128;
+  const int nib = (p.Nq + 127) / 128, njb = (p.Nk + 127) / 128;
+  e = launch_named("sim_split_u", sim_split_u_kernel, dim3(2 * nib * nec * p.B * p.Hq), dim3(kThreads), s, p, sp, U,
+                   nib, nec);
+  if (e != hipSuccess) return e;
+  e = launch_named("sim_split_w", sim_split_w_kernel, dim3(2 * njb * nec * p.B * p.Hk), dim3(kThreads), s, p, sp, W,
+                   njb, nec);
+  if (e != hipSuccess) return e;
+  return launch_sim_finalize(p, U, sp.U2, W, sp.W2, s);
+}
+
+}  // namespace pope

@@ -5,17 +5,20 @@ Operator mirror of the reference's ``PoPE_pytorch/triton_pope.py``:
 (:364-372, here ``hip_compute_qk_similarity``) keep their arguments and return
 values.  The work runs in two ``torch.library`` custom ops:
 
-  pope_amd::sim_fwd(q, k, freqs, bias) -> sim                (fp32 MFMA)
-  pope_amd::sim_bwd(dsim, q, k, freqs, bias, need_dfreqs, need_dbias)
+  pope_amd::sim_fwd(q, k, freqs, bias, split) -> sim
+  pope_amd::sim_bwd(dsim, q, k, freqs, bias, need_dfreqs, need_dbias, split)
                                       -> (dq, dk, dfreqs, dbias)
 
 ``sim_fwd`` is differentiable through ``register_autograd``.  Query head h reads
 kv head h % Hk and bias row h % Hk, which is what the reference's repeat of k and
 bias (:368-370) amounts to, without materialising the repeat.
 
-``allow_tf32`` is accepted and ignored: CDNA4 has no reduced-precision fp32
-matrix format, the kernels always run true fp32 MFMA (the reference's tests pass
-``allow_tf32=False`` for their parity checks, test_triton.py:300,335,359).
+``allow_tf32`` selects the product arithmetic, as it does in the reference
+(triton_pope.py:63,145,224): ``True`` (the default) runs the products on bf16
+MFMA with every fp32 operand split into hi + lo bf16 halves (``split=True``:
+three products per pair, 16 significant operand bits, fp32 accumulation; the
+reference's TF32 keeps 10), ``False`` runs true fp32 MFMA (the reference's tests
+pass ``allow_tf32=False`` for their parity checks, test_triton.py:300,335,359).
 """
 from __future__ import annotations
 
@@ -37,9 +40,10 @@ def divisible_by(num, den):
     return (num % den) == 0
 
 
-def _desc(q, k, freqs, bias) -> _lib.PopeDesc:
+def _desc(q, k, freqs, bias, split=False) -> _lib.PopeDesc:
     B, Hq, Nq, D = q.shape
     d = _lib.PopeDesc()
+    d.flags = _lib.FLAG_SPLIT_BF16 if split else 0
     d.B, d.Hq, d.Hk, d.Nq, d.Nk, d.D = B, Hq, k.shape[1], Nq, k.shape[2], D
     d.R = freqs.shape[-1]
     d.dtype = _lib.POPE_F32
@@ -59,11 +63,12 @@ def _aligned(t: Tensor) -> Tensor:
 
 
 @torch.library.custom_op("pope_amd::sim_fwd", mutates_args=(), device_types="cuda")
-def sim_fwd_op(q: Tensor, k: Tensor, freqs: Tensor, bias: Tensor) -> Tensor:
-    """q (B,Hq,Nq,D), k (B,Hk,Nk,D) fp32; freqs (..,N,R) fp32; bias (1|Hk,R) -> sim (B,Hq,Nq,Nk) fp32."""
+def sim_fwd_op(q: Tensor, k: Tensor, freqs: Tensor, bias: Tensor, split: bool = False) -> Tensor:
+    """q (B,Hq,Nq,D), k (B,Hk,Nk,D) fp32; freqs (..,N,R) fp32; bias (1|Hk,R) -> sim (B,Hq,Nq,Nk) fp32.
+    split: products on split-bf16 MFMA instead of fp32 MFMA."""
     L = _lib.lib()
     q, k = _aligned(q), _aligned(k)
-    d = _desc(q, k, freqs, bias)
+    d = _desc(q, k, freqs, bias, split)
     sim = torch.empty(q.shape[0], q.shape[1], q.shape[2], k.shape[2], device=q.device, dtype=torch.float32)
     d.sim_s[:] = _lib.strides3(sim)
     ws = _lib.workspace(_lib.OP_SIM_FWD, d, q.device)
@@ -74,16 +79,16 @@ def sim_fwd_op(q: Tensor, k: Tensor, freqs: Tensor, bias: Tensor) -> Tensor:
 
 
 @sim_fwd_op.register_fake
-def _(q, k, freqs, bias):
+def _(q, k, freqs, bias, split=False):
     return q.new_empty((q.shape[0], q.shape[1], q.shape[2], k.shape[2]), dtype=torch.float32)
 
 
 @torch.library.custom_op("pope_amd::sim_bwd", mutates_args=(), device_types="cuda")
 def sim_bwd_op(dsim: Tensor, q: Tensor, k: Tensor, freqs: Tensor, bias: Tensor, need_dfreqs: bool,
-               need_dbias: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+               need_dbias: bool, split: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     L = _lib.lib()
     q, k, dsim = _aligned(q), _aligned(k), _aligned(dsim.float())
-    d = _desc(q, k, freqs, bias)
+    d = _desc(q, k, freqs, bias, split)
     d.sim_s[:] = _lib.strides3(dsim)
     dq, dk = torch.empty_like(q), torch.empty_like(k)
     d.dq_s[:], d.dk_s[:] = _lib.strides3(dq), _lib.strides3(dk)
@@ -101,23 +106,24 @@ def sim_bwd_op(dsim: Tensor, q: Tensor, k: Tensor, freqs: Tensor, bias: Tensor, 
 
 
 @sim_bwd_op.register_fake
-def _(dsim, q, k, freqs, bias, need_dfreqs, need_dbias):
+def _(dsim, q, k, freqs, bias, need_dfreqs, need_dbias, split=False):
     df = freqs.new_empty(freqs.shape, dtype=torch.float32) if need_dfreqs else q.new_empty(0, dtype=torch.float32)
     db = bias.new_empty(bias.shape, dtype=torch.float32) if need_dbias else q.new_empty(0, dtype=torch.float32)
     return torch.empty_like(q), torch.empty_like(k), df, db
 
 
 def _sim_setup(ctx, inputs, output):
-    q, k, freqs, bias = inputs
+    q, k, freqs, bias, split = inputs
     ctx.save_for_backward(q, k, freqs, bias)
+    ctx.split = split
 
 
 def _sim_backward(ctx, dsim):
     q, k, freqs, bias = ctx.saved_tensors
     need_df = bool(ctx.needs_input_grad[2]) and freqs.shape[-1] > 0
     need_db = bool(ctx.needs_input_grad[3]) and bias.shape[-1] > 0
-    dq, dk, df, db = sim_bwd_op(dsim, q, k, freqs, bias, need_df, need_db)
-    return dq, dk, df if need_df else None, db if need_db else None
+    dq, dk, df, db = sim_bwd_op(dsim, q, k, freqs, bias, need_df, need_db, ctx.split)
+    return dq, dk, df if need_df else None, db if need_db else None, None
 
 
 sim_fwd_op.register_autograd(_sim_backward, setup_context=_sim_setup)
@@ -164,5 +170,5 @@ def hip_compute_qk_similarity(q, k, freqs, bias, rotate_dim=None, allow_tf32=Tru
         raise ValueError(f"freqs has {freqs.shape[-2]} positions, keys need {k.shape[2]}")
     out_dtype = q.dtype
     qf, kf = q.float(), k.float()
-    sim = sim_fwd_op(qf, kf, freqs, bias)
+    sim = sim_fwd_op(qf, kf, freqs, bias, bool(allow_tf32))
     return sim.to(out_dtype) if out_dtype != torch.float32 else sim

@@ -1,4 +1,5 @@
-"""Fused PoPE similarity on the GPU: fp32 MFMA kernels vs the CPU oracle.
+"""Fused PoPE similarity on the GPU: the fp32 MFMA kernels (allow_tf32=False) and the
+split-bf16 kernels (allow_tf32=True, the default) vs the CPU oracle.
 
 Tolerance (from the build's north star): 1e-4 relative for fp32 similarity,
 read as ||kernel - oracle||_inf <= 1e-4 * ||oracle||_inf for S and for each
@@ -46,11 +47,11 @@ def _oracle(q, k, freqs, bias, G):
     return S.detach(), [x.grad for x in t]
 
 
-def _kernel(q, k, freqs, bias, G, slicer=None):
+def _kernel(q, k, freqs, bias, G, slicer=None, allow_tf32=True):
     import pope_amd
     t = [x.detach().clone().cuda().requires_grad_(True) for x in (q, k, freqs, bias)]
     qq, kk = t[0], t[1]
-    S = pope_amd.compute_attn_similarity(qq, kk, (t[2], t[3]))
+    S = pope_amd.compute_attn_similarity(qq, kk, (t[2], t[3]), allow_tf32=allow_tf32)
     S.backward(G.cuda())
     return S.detach(), [x.grad for x in t]
 
@@ -74,10 +75,11 @@ def _compare(S, grads, S_ref, grads_ref, names=("dq", "dk", "dfreqs", "dbias")):
     (1, 2, 2, 64, 64, 256, 128),     # E = 384: several expanded-column chunks
     (1, 2, 2, 33, 33, 48, 16),       # D = 48
 ], ids=lambda c: "x".join(map(str, c)))
-def test_similarity_multi_config(cuda, cfg):
+@pytest.mark.parametrize("allow_tf32", [True, False], ids=["split_bf16", "fp32"])
+def test_similarity_multi_config(cuda, cfg, allow_tf32):
     q, k, freqs, bias, G = _case(100, *cfg)
     S_ref, g_ref = _oracle(q, k, freqs, bias, G)
-    S, g = _kernel(q, k, freqs, bias, G)
+    S, g = _kernel(q, k, freqs, bias, G, allow_tf32=allow_tf32)
     _compare(S, g, S_ref, g_ref)
 
 
