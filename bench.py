@@ -246,13 +246,19 @@ def sim_bench(steps: int, warmup: int):
     R_ = D_
     flops = 3 * 2 * B_ * H_ * N_ * N_ * (D_ + R_)
     nbytes = 2 * 4 * B_ * H_ * N_ * N_ + 2 * 4 * 2 * B_ * H_ * N_ * D_ + 4 * N_ * R_
-    t_min = max(flops / (PEAK_FP32_TFLOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9))
+    # the default arithmetic (allow_tf32=True) is three bf16 MFMA products per fp32 product:
+    # its compute floor is 3 * flops at the bf16 peak, below the HBM floor
+    t_mfma = 3 * flops / (PEAK_BF16_TFLOPS * 1e12)
+    t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
     return {
-        "workload": "C2 fused similarity fwd+bwd: q, k (2,8,2048,64) fp32, PoPE(64, heads=8), dS N(0,1)",
+        "workload": "C2 fused similarity fwd+bwd: q, k (2,8,2048,64) fp32, PoPE(64, heads=8), dS N(0,1); "
+                    "compute_attn_similarity default allow_tf32=True (split-bf16 MFMA products)",
         "us_per_step": round(el * 1e6, 2), "TFLOPs": round(flops / el / 1e12, 2),
-        "GBps": round(nbytes / el / 1e9, 1), "algorithmic_flops": flops, "algorithmic_bytes": nbytes,
-        "frac_of_roofline": round(t_min / el, 4),
-        "roofline_bound": "fp32" if flops / (PEAK_FP32_TFLOPS * 1e12) > nbytes / (PEAK_HBM_GBS * 1e9) else "hbm",
+        "GBps": round(nbytes / el / 1e9, 1), "frac_of_hbm_peak": round(nbytes / el / 1e9 / PEAK_HBM_GBS, 4),
+        "algorithmic_flops": flops, "algorithmic_bytes": nbytes,
+        "roofline": {"bound": "hbm" if t_hbm >= t_mfma else "mfma", "t_min_us": round(max(t_hbm, t_mfma) * 1e6, 2),
+                     "frac": round(max(t_hbm, t_mfma) / el, 4)},
+        "fp32_peak_frac": round(flops / el / 1e12 / PEAK_FP32_TFLOPS, 4),
         "kernels_us": _kernel_us(ks, sorted(ks)),
     }
 
