@@ -61,6 +61,16 @@ def test_workspace_sizes():
     ds = _desc(dtype=_lib.POPE_F32, R=64)
     st, n = _ws(_lib.OP_SIM_FWD, ds)
     assert st == 0 and n == 8 * 256 * 64 * 8 + 256 * 64 * 8         # key table per kv head + query table
+    # split-bf16 similarity: + hi / lo planes of Q_hat and K_hat (rows padded to 128, EP = 128 columns)
+    ds.flags = _lib.FLAG_SPLIT_BF16
+    planes = 2 * al(2 * 8 * 256 * 128 * 2) + 2 * al(2 * 8 * 256 * 128 * 2)
+    assert _ws(_lib.OP_SIM_FWD, ds) == (0, n + planes)
+    # backward: U, W (fp32, EP columns) and, split, their second partial sums
+    uw = al(2 * 8 * 256 * 128 * 4) + al(2 * 8 * 256 * 128 * 4)
+    ds.flags = 0
+    assert _ws(_lib.OP_SIM_BWD, ds) == (0, n + uw)
+    ds.flags = _lib.FLAG_SPLIT_BF16
+    assert _ws(_lib.OP_SIM_BWD, ds) == (0, n + uw + planes + uw)
 
 
 def _fake(n=1 << 20):
@@ -130,6 +140,10 @@ def test_sim_and_decode_validation():
     d = _desc(Nq=64, dtype=_lib.POPE_BF16)
     st = L.pope_flash_decode(ctypes.byref(d), _A, _A, _A, _A, _A, None, _A, _A, _A, 1 << 16, None)
     assert st == 2 and "one non-causal query row" in _lib.last_error()
+    d = _desc(dtype=_lib.POPE_F32, D=64, R=64)
+    d.flags = 1   # the flash backward's PREPARED: not a similarity flag
+    st = L.pope_sim_fwd(ctypes.byref(d), _A, _A, _A, _A, _A, _A, 1 << 16, None)
+    assert st == 1 and "flags" in _lib.last_error()
     d = _desc(dtype=_lib.POPE_F32, D=64, R=64)
     d.bias_sh = -1
     st = L.pope_sim_bwd(ctypes.byref(d), _A, _A, _A, _A, _A, _A, _A, None, None, _A, 1 << 16, None)
