@@ -159,6 +159,28 @@ int pope_flash_decode(const pope_desc* desc, const void* q, const void* k, const
                       float* lse, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Materialising polar transform: q_hat, k_hat = apply_pope_to_qk(pos, q, k) with the default
+ * softplus magnitude (pope.py:30-86).  q (B, Hq, Nq, D), k (B, Hk, Nk, D) in dtype (F32, F16 or
+ * BF16, q_s / k_s strides, multiples of 4); q_hat (B, Hq, Nq, D + R), k_hat (B, Hk, Nk, D + R)
+ * are contiguous fp32 (the reference's dtype promotion against fp32 cos / sin, :69-70): the
+ * first 2R columns interleave (a cos, a sin) per rotated dim with a = softplus rounded to dtype
+ * (:60), the last D - R are the raw pass-through dims (:82-84).  Query rows take the phases
+ * freqs[Nk - Nq + i] (:64), key rows fl(freqs[j] + bias[h]) (:56); bias is used as given.
+ */
+int pope_polar_fwd(const pope_desc* desc, const void* q, const void* k, const float* freqs, const float* bias,
+                   float* q_hat, float* k_hat, void* stream);
+
+/*
+ * Backward of pope_polar_fwd: dq_hat / dk_hat are contiguous fp32 gradients of its outputs;
+ * dq, dk (dtype, dq_s / dk_s strides) are written; dfreqs (fp32, df_s strides) and dbias (fp32,
+ * bias rows bias_sh) are ACCUMULATED into (NULL = not wanted).  The autograd backward of the
+ * reference's torch ops (pope.py:30-86).
+ */
+int pope_polar_bwd(const pope_desc* desc, const float* dq_hat, const float* dk_hat, const void* q, const void* k,
+                   const float* freqs, const float* bias, void* dq, void* dk, float* dfreqs, float* dbias,
+                   void* stream);
+
+/*
  * Per-kernel timing.  No counterpart in the reference (its tests print only
  * parity diffs, tests/test_flash_attn.py:61,109).  While enabled, every kernel
  * launch of the library carries a pair of hipEvents that its dispatch stamps with

@@ -616,3 +616,79 @@ int pope_sim_bwd(const pope_desc* d, const void* dsim, const void* q, const void
 }
 
 }  // extern "C"
+
+namespace {
+
+int check_polar(const pope_desc* d, const void* q, const void* k, const float* freqs, const float* bias) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (d->dtype != POPE_F32 && d->dtype != POPE_F16 && d->dtype != POPE_BF16)
+    return fail(POPE_ERR_INVALID, "unknown dtype %d", d->dtype);
+  if (d->D > 512) return fail(POPE_ERR_UNSUPPORTED, "polar transform covers head dim <= 512 (got %d)", d->D);
+  if (!q || !k) return fail(POPE_ERR_INVALID, "q, k must be non-NULL");
+  const size_t al = d->dtype == POPE_F32 ? 16 : 8;
+  if (reinterpret_cast<uintptr_t>(q) % al || reinterpret_cast<uintptr_t>(k) % al)
+    return fail(POPE_ERR_INVALID, "q, k must be %zu-byte aligned", al);
+  for (int i = 0; i < 3; ++i)
+    if (d->q_s[i] < 0 || d->q_s[i] % 4 || d->k_s[i] < 0 || d->k_s[i] % 4)
+      return fail(POPE_ERR_INVALID, "q / k strides must be non-negative multiples of 4");
+  if (d->R > 0 && d->bias_sh != 0 && d->bias_sh < d->R) return fail(POPE_ERR_INVALID, "bias row stride below R");
+  return check_pope_ptrs(d, freqs, bias);
+}
+
+void polar_params(const pope_desc* d, const void* q, const void* k, const float* freqs, const float* bias,
+                  pope::PolarParams* p) {
+  std::memset(p, 0, sizeof *p);
+  p->q = q; p->k = k;
+  p->freqs = d->R > 0 ? freqs : nullptr;
+  p->bias = d->R > 0 ? bias : nullptr;
+  p->B = d->B; p->Hq = d->Hq; p->Hk = d->Hk; p->Nq = d->Nq; p->Nk = d->Nk; p->D = d->D; p->R = d->R;
+  copy3(p->q_s, d->q_s); copy3(p->k_s, d->k_s); copy3(p->f_s, d->f_s);
+  p->bias_sh = d->bias_sh;
+}
+
+int polar_dtype(const pope_desc* d) { return d->dtype == POPE_F32 ? 0 : d->dtype == POPE_F16 ? 1 : 2; }
+
+}  // namespace
+
+extern "C" {
+
+int pope_polar_fwd(const pope_desc* d, const void* q, const void* k, const float* freqs, const float* bias,
+                   float* q_hat, float* k_hat, void* stream) {
+  int rc = check_polar(d, q, k, freqs, bias);
+  if (rc) return rc;
+  if (!q_hat || !k_hat || !aligned16(q_hat) || !aligned16(k_hat))
+    return fail(POPE_ERR_INVALID, "q_hat, k_hat must be non-NULL and 16-byte aligned");
+  pope::PolarParams p;
+  polar_params(d, q, k, freqs, bias, &p);
+  p.qh = q_hat; p.kh = k_hat;
+  const hipError_t e = pope::launch_polar(p, polar_dtype(d), false, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "polar transform launch");
+  return POPE_OK;
+}
+
+int pope_polar_bwd(const pope_desc* d, const float* dq_hat, const float* dk_hat, const void* q, const void* k,
+                   const float* freqs, const float* bias, void* dq, void* dk, float* dfreqs, float* dbias,
+                   void* stream) {
+  int rc = check_polar(d, q, k, freqs, bias);
+  if (rc) return rc;
+  if (!dq_hat || !dk_hat || !aligned16(dq_hat) || !aligned16(dk_hat))
+    return fail(POPE_ERR_INVALID, "dq_hat, dk_hat must be non-NULL and 16-byte aligned");
+  const size_t al = d->dtype == POPE_F32 ? 16 : 8;
+  if (!dq || !dk || reinterpret_cast<uintptr_t>(dq) % al || reinterpret_cast<uintptr_t>(dk) % al)
+    return fail(POPE_ERR_INVALID, "dq, dk must be non-NULL and %zu-byte aligned", al);
+  for (int i = 0; i < 3; ++i)
+    if (d->dq_s[i] < 0 || d->dq_s[i] % 4 || d->dk_s[i] < 0 || d->dk_s[i] % 4)
+      return fail(POPE_ERR_INVALID, "dq / dk strides must be non-negative multiples of 4");
+  if (d->R == 0 && (dfreqs || dbias)) return fail(POPE_ERR_INVALID, "dfreqs/dbias requested with rotate dim 0");
+  if (d->df_s[0] < 0 || d->df_s[1] < 0 || d->df_s[2] < 0) return fail(POPE_ERR_INVALID, "negative dfreqs stride");
+  pope::PolarParams p;
+  polar_params(d, q, k, freqs, bias, &p);
+  p.gq = dq_hat; p.gk = dk_hat; p.dq = dq; p.dk = dk; p.dfreqs = dfreqs; p.dbias = dbias;
+  copy3(p.dq_s, d->dq_s); copy3(p.dk_s, d->dk_s); copy3(p.df_s, d->df_s);
+  const hipError_t e = pope::launch_polar(p, polar_dtype(d), true, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "polar transform backward launch");
+  return POPE_OK;
+}
+
+}  // extern "C"

@@ -134,6 +134,19 @@ struct SimSplit {
 hipError_t launch_sim_split_fwd(const SimParams& p, const SimSplit& sp, hipStream_t s);
 hipError_t launch_sim_split_bwd(const SimParams& p, const SimSplit& sp, float* U, float* W, hipStream_t s);
 
+// Materialising polar transform (polar.hip): q_hat / k_hat fp32 rows (heads, N, D + R).
+struct PolarParams {
+  const void* q; const void* k; const float* freqs; const float* bias;
+  float* qh; float* kh;                 // forward outputs
+  const float* gq; const float* gk;     // backward: gradients of q_hat / k_hat
+  void* dq; void* dk; float* dfreqs; float* dbias;
+  int B, Hq, Hk, Nq, Nk, D, R;
+  int64_t q_s[3], k_s[3], dq_s[3], dk_s[3], f_s[3], df_s[3];
+  int64_t bias_sh;
+};
+// dtype: 0 fp32, 1 fp16, 2 bf16 (of q, k, dq, dk)
+hipError_t launch_polar(const PolarParams& p, int dtype, bool bwd, hipStream_t s);
+
 struct DecodeParams {
   const uint16_t* q; const uint16_t* k; const uint16_t* v;
   const float* freqs; const float* bias; const uint8_t* mask;

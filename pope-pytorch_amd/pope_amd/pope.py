@@ -55,6 +55,11 @@ def apply_pope_to_qk(pope: PolarEmbedReturn, q: Tensor, k: Tensor, to_magnitude=
     q_len, k_len, qk_dim, rot = q.shape[-2], k.shape[-2], q.shape[-1], freqs.shape[-1]
     assert q_len <= k_len and rot <= qk_dim
 
+    if q.is_cuda:
+        from . import hip_polar
+        if hip_polar.fits(q, k, freqs, bias, to_magnitude, return_complex):
+            return hip_polar.polar(q, k, freqs, bias)
+
     partial = rot < qk_dim
     if partial:
         q, q_rest = q[..., :rot], q[..., rot:]
