@@ -359,8 +359,8 @@ def cpu_baseline(min_seconds: float = 10.0, max_reps: int = 10):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("train", "decode", "sim", "axial"), default="train",
                     help="train (default): the C3 headline line with C5, C2 and C4 as secondary; "

@@ -10,7 +10,10 @@ arguments, (batch, seq, heads, dim) layout and return values.  Underneath, two
   pope_amd::flash_bwd(do, q, k, v, o, lse, freqs?, bias?, mask?, causal, scale,
                       need_dfreqs, need_dbias) -> (dq, dk, dv, dfreqs, dbias)
 
-with ``flash_fwd`` differentiable through ``register_autograd``.  The ops take
+with ``flash_fwd`` differentiable through ``register_autograd``.  Eager calls of
+``flash_attn`` / ``flash_attn_head_first`` run the same forward and backward through a
+plain ``autograd.Function`` (no custom-op dispatch, which costs more host time than a
+launch); torch.compile tracing records the ops.  The ops take
 head-first logical views (B, H, N, D) with any batch/head/seq strides and a unit
 feature stride, so the (b n h d) <-> (b h n d) permutes of the reference cost no
 copies.  Query head h reads kv head h % Hk (the reference's torch-path GQA
@@ -120,6 +123,135 @@ def _check_pope_shapes(q, k, freqs, bias):
             raise ValueError(f"bias {tuple(bias.shape)} must be (1 or {k.shape[1]}, {R})")
 
 
+def _check_views(q, k, v, mask, lse=None):
+    """Shapes the kernels index by but the descriptor does not carry."""
+    if v.shape != k.shape:
+        raise ValueError(f"v {tuple(v.shape)} must match k {tuple(k.shape)}")
+    if exists(mask) and tuple(mask.shape) != (q.shape[0], k.shape[2]):
+        raise ValueError(f"mask {tuple(mask.shape)} must be (batch, seq_k) = {(q.shape[0], k.shape[2])}")
+    if exists(lse) and tuple(lse.shape) != tuple(q.shape[:3]):
+        raise ValueError(f"lse {tuple(lse.shape)} must be {tuple(q.shape[:3])}")
+
+
+# ------------------------------------------------------------------ call plans
+#
+# A plan is the filled descriptor and workspace size for one combination of shapes,
+# strides, dtype and flags.  Building one costs a few dozen ctypes field writes and a
+# library query; a training loop repeats the same few combinations, so plans are
+# cached by a key of everything the descriptor is made from.  The library only reads
+# the descriptor, so one cached instance serves every call with that key.
+
+_PLANS: dict = {}
+_PLANS_MAX = 1024
+
+
+def _plan(key, build):
+    p = _PLANS.get(key)
+    if p is None:
+        if len(_PLANS) >= _PLANS_MAX:
+            _PLANS.clear()
+        p = _PLANS[key] = build()
+    return p
+
+
+def _opt_key(t):
+    return None if t is None else (t.shape, t.stride())
+
+
+def _stream(t: Tensor) -> int:
+    return torch._C._cuda_getCurrentRawStream(t.get_device())
+
+
+def _data(t):
+    return None if t is None else t.data_ptr()
+
+
+def _fwd_impl(q, k, v, freqs, bias, mask, causal, softmax_scale):
+    q, k, v = _unit_feature(q), _unit_feature(k), _unit_feature(v)
+    o = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
+    key = ("fwd", q.shape, q.stride(), k.shape, k.stride(), v.shape, v.stride(), o.stride(), q.dtype,
+           causal, softmax_scale, _opt_key(freqs), _opt_key(bias), _opt_key(mask))
+
+    def build():
+        _check_pope_shapes(q, k, freqs, bias)
+        _check_views(q, k, v, mask)
+        d = _desc(q, k, freqs, bias, causal, softmax_scale)
+        d.q_s[:], d.k_s[:], d.v_s[:] = _lib.strides3(q), _lib.strides3(k), _lib.strides3(v)
+        d.o_s[:] = _lib.strides3(o)
+        if exists(mask):
+            d.mask_sb = mask.stride(0)
+        # one non-causal query row against a long cache: the split-K decode kernel
+        decode = q.shape[2] == 1 and not causal and k.shape[2] >= 1024
+        dec_bytes = _lib.workspace_bytes(_lib.OP_FLASH_DECODE, d) if decode else -1
+        return d, dec_bytes, _lib.workspace_bytes(_lib.OP_FLASH_FWD, d)
+
+    d, dec_bytes, fwd_bytes = _plan(key, build)
+    L = _lib.lib()
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), _data(freqs), _data(bias), _data(mask),
+            o.data_ptr(), lse.data_ptr())
+    stream = _stream(q)
+    if dec_bytes >= 0:
+        dws = torch.empty(dec_bytes, dtype=torch.uint8, device=q.device) if dec_bytes else None
+        st = L.pope_flash_decode(ctypes.byref(d), *args, _data(dws), dec_bytes, stream)
+        if st == 0:
+            return o, lse, q.new_empty(0, dtype=torch.uint8)
+        if st != 2:   # 2: the decode kernel does not cover this shape -> general forward
+            _lib.check(st, "flash decode")
+    # torch's caching allocator returns 512-byte aligned blocks
+    ws = torch.empty(fwd_bytes, dtype=torch.uint8, device=q.device)
+    _lib.check(L.pope_flash_fwd(ctypes.byref(d), *args, ws.data_ptr(), fwd_bytes, stream), "flash forward")
+    return o, lse, ws
+
+
+def _bwd_impl(do, q, k, v, o, lse, freqs, bias, mask, causal, softmax_scale, need_dfreqs, need_dbias,
+              fwd_ws=None):
+    q, k, v, o, do = (_unit_feature(t) for t in (q, k, v, o, do))
+    if do.dtype != q.dtype:
+        do = do.to(q.dtype)
+    if not lse.is_contiguous():
+        lse = lse.contiguous()
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    # the library clears dfreqs / dbias itself (POPE_FLAG_ZERO_GRADS) before accumulating
+    dfreqs = torch.empty(freqs.shape, device=q.device, dtype=torch.float32) if need_dfreqs else q.new_empty(0, dtype=torch.float32)
+    dbias = torch.empty(bias.shape, device=q.device, dtype=torch.float32) if need_dbias else q.new_empty(0, dtype=torch.float32)
+    key = ("bwd", q.shape, q.stride(), k.shape, k.stride(), v.shape, v.stride(), o.stride(), do.stride(),
+           dq.stride(), dk.stride(), dv.stride(), q.dtype, causal, softmax_scale, _opt_key(freqs),
+           _opt_key(bias), _opt_key(mask), need_dfreqs, need_dbias)
+
+    def build():
+        _check_pope_shapes(q, k, freqs, bias)
+        _check_views(q, k, v, mask, lse)
+        if o.shape != q.shape or do.shape != q.shape:
+            raise ValueError(f"o {tuple(o.shape)} and do {tuple(do.shape)} must match q {tuple(q.shape)}")
+        d = _desc(q, k, freqs, bias, causal, softmax_scale)
+        d.q_s[:], d.k_s[:], d.v_s[:], d.o_s[:] = (_lib.strides3(t) for t in (q, k, v, o))
+        d.do_s[:] = _lib.strides3(do)
+        d.dq_s[:], d.dk_s[:], d.dv_s[:] = _lib.strides3(dq), _lib.strides3(dk), _lib.strides3(dv)
+        if need_dfreqs:
+            d.df_s[:] = _freqs_strides(dfreqs)
+        if exists(mask):
+            d.mask_sb = mask.stride(0)
+        d.flags = _lib.FLAG_ZERO_GRADS
+        # the same descriptor with PREPARED set, for calls that bring the forward's workspace
+        dp = _lib.PopeDesc.from_buffer_copy(d)
+        dp.flags |= _lib.FLAG_PREPARED
+        return d, dp, _lib.workspace_bytes(_lib.OP_FLASH_BWD, d)
+
+    d, dprep, need = _plan(key, build)
+    if exists(fwd_ws) and fwd_ws.numel() == need:
+        ws, d = fwd_ws, dprep
+    else:
+        ws = torch.empty(need, dtype=torch.uint8, device=q.device)
+    st = _lib.lib().pope_flash_bwd(
+        ctypes.byref(d), do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+        _data(freqs), _data(bias), _data(mask), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+        dfreqs.data_ptr() if need_dfreqs else None, dbias.data_ptr() if need_dbias else None,
+        ws.data_ptr(), need, _stream(q))
+    _lib.check(st, "flash backward")
+    return dq, dk, dv, dfreqs, dbias
+
+
 # ----------------------------------------------------------------------------- ops
 
 @torch.library.custom_op("pope_amd::flash_fwd", mutates_args=(), device_types="cuda")
@@ -128,30 +260,7 @@ def flash_fwd_op(q: Tensor, k: Tensor, v: Tensor, freqs: Optional[Tensor], bias:
     """q (B,Hq,Nq,D), k/v (B,Hk,Nk,D) bf16/fp16 views -> o like q, lse (B,Hq,Nq) fp32 and the
     workspace holding the forward's preparation (expanded K/Q rows, phase tables), which the
     backward reuses; empty when the decode kernel ran."""
-    L = _lib.lib()
-    q, k, v = _unit_feature(q), _unit_feature(k), _unit_feature(v)
-    d = _desc(q, k, freqs, bias, causal, softmax_scale)
-    d.q_s[:], d.k_s[:], d.v_s[:] = _lib.strides3(q), _lib.strides3(k), _lib.strides3(v)
-    o = torch.empty_like(q)
-    lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
-    d.o_s[:] = _lib.strides3(o)
-    if exists(mask):
-        d.mask_sb = mask.stride(0)
-    args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(freqs), _lib.ptr(bias), _lib.ptr(mask),
-            _lib.ptr(o), _lib.ptr(lse))
-    stream = _lib.stream_ptr(q.device)
-    # one non-causal query row against a long cache: the split-K decode kernel
-    if q.shape[2] == 1 and not causal and k.shape[2] >= 1024:
-        dws = _lib.workspace(_lib.OP_FLASH_DECODE, d, q.device)
-        st = L.pope_flash_decode(ctypes.byref(d), *args, _lib.ptr(dws), 0 if dws is None else dws.numel(), stream)
-        if st == 0:
-            return o, lse, q.new_empty(0, dtype=torch.uint8)
-        if st != 2:   # 2: the decode kernel does not cover this shape -> general forward
-            _lib.check(st, "flash decode")
-    ws = _lib.workspace(_lib.OP_FLASH_FWD, d, q.device)
-    st = L.pope_flash_fwd(ctypes.byref(d), *args, _lib.ptr(ws), ws.numel(), stream)
-    _lib.check(st, "flash forward")
-    return o, lse, ws
+    return _fwd_impl(q, k, v, freqs, bias, mask, causal, softmax_scale)
 
 
 @flash_fwd_op.register_fake
@@ -168,36 +277,8 @@ def flash_bwd_op(do: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Te
                  ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Gradients of flash_fwd.  ``fwd_ws`` is the workspace flash_fwd returned for the same
     inputs (reused as is); without it the preparation is recomputed."""
-    L = _lib.lib()
-    q, k, v, o, do = (_unit_feature(t) for t in (q, k, v, o, do))
-    if do.dtype != q.dtype:
-        do = do.to(q.dtype)
-    d = _desc(q, k, freqs, bias, causal, softmax_scale)
-    d.q_s[:], d.k_s[:], d.v_s[:], d.o_s[:] = (_lib.strides3(t) for t in (q, k, v, o))
-    d.do_s[:] = _lib.strides3(do)
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    d.dq_s[:], d.dk_s[:], d.dv_s[:] = _lib.strides3(dq), _lib.strides3(dk), _lib.strides3(dv)
-    # the library clears dfreqs / dbias itself (POPE_FLAG_ZERO_GRADS) before accumulating
-    dfreqs = torch.empty(freqs.shape, device=q.device, dtype=torch.float32) if need_dfreqs else q.new_empty(0, dtype=torch.float32)
-    dbias = torch.empty(bias.shape, device=q.device, dtype=torch.float32) if need_dbias else q.new_empty(0, dtype=torch.float32)
-    if need_dfreqs:
-        d.df_s[:] = _freqs_strides(dfreqs)
-    if exists(mask):
-        d.mask_sb = mask.stride(0)
-    d.flags = _lib.FLAG_ZERO_GRADS
-    need = _lib.workspace_bytes(_lib.OP_FLASH_BWD, d)
-    if exists(fwd_ws) and fwd_ws.numel() == need:
-        ws = fwd_ws
-        d.flags |= _lib.FLAG_PREPARED
-    else:
-        ws = torch.empty(need, dtype=torch.uint8, device=q.device)
-    st = L.pope_flash_bwd(ctypes.byref(d), _lib.ptr(do), _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o),
-                          _lib.ptr(lse), _lib.ptr(freqs), _lib.ptr(bias), _lib.ptr(mask), _lib.ptr(dq),
-                          _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dfreqs) if need_dfreqs else None,
-                          _lib.ptr(dbias) if need_dbias else None, _lib.ptr(ws), ws.numel(),
-                          _lib.stream_ptr(q.device))
-    _lib.check(st, "flash backward")
-    return dq, dk, dv, dfreqs, dbias
+    return _bwd_impl(do, q, k, v, o, lse, freqs, bias, mask, causal, softmax_scale, need_dfreqs, need_dbias,
+                     fwd_ws)
 
 
 @flash_bwd_op.register_fake
@@ -226,6 +307,34 @@ def _fwd_backward(ctx, do, dlse, dws):
 flash_fwd_op.register_autograd(_fwd_backward, setup_context=_fwd_setup)
 
 
+class _FlashAttnEager(torch.autograd.Function):
+    """The same forward / backward as the registered ops, called without the custom-op
+    dispatch layers (about 20-30 us of host time per call).  Used outside torch.compile
+    tracing; under tracing the ops above are used so the graph records them."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, freqs, bias, mask, causal, scale):
+        o, lse, ws = _fwd_impl(q, k, v, freqs, bias, mask, causal, scale)
+        ctx.save_for_backward(q, k, v, freqs, bias, mask, o, lse, ws)
+        ctx.causal, ctx.scale = causal, scale
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, freqs, bias, mask, o, lse, ws = ctx.saved_tensors
+        need_df = bool(ctx.needs_input_grad[3]) and exists(freqs)
+        need_db = bool(ctx.needs_input_grad[4]) and exists(bias)
+        dq, dk, dv, df, db = _bwd_impl(do, q, k, v, o, lse, freqs, bias, mask, ctx.causal, ctx.scale,
+                                       need_df, need_db, ws)
+        return dq, dk, dv, df if need_df else None, db if need_db else None, None, None, None
+
+
+def _flash(q, k, v, freqs, bias, mask, causal, scale) -> Tensor:
+    if torch.compiler.is_compiling():
+        return flash_fwd_op(q, k, v, freqs, bias, mask, causal, scale)[0]
+    return _FlashAttnEager.apply(q, k, v, freqs, bias, mask, causal, scale)
+
+
 # ------------------------------------------------------------ head-first entry point
 
 def flash_attn_head_first(q: Tensor, k: Tensor, v: Tensor, freqs: Optional[Tensor] = None,
@@ -236,7 +345,6 @@ def flash_attn_head_first(q: Tensor, k: Tensor, v: Tensor, freqs: Optional[Tenso
         raise RuntimeError("pope_amd flash attention runs on GPU tensors only")
     scale = q.shape[-1] ** -0.5 if softmax_scale is None else softmax_scale
     freqs, pope_bias = _prep_pope(freqs, pope_bias)
-    _check_pope_shapes(q, k, freqs, pope_bias)
     mask = _prep_mask(mask, q.shape[0])
     out_dtype = q.dtype
     if q.dtype not in _MFMA_DTYPES:
@@ -245,7 +353,7 @@ def flash_attn_head_first(q: Tensor, k: Tensor, v: Tensor, freqs: Optional[Tenso
         k = k.to(q.dtype)
     if v.dtype != q.dtype:
         v = v.to(q.dtype)
-    o, _, _ = flash_fwd_op(q, k, v, freqs, pope_bias, mask, causal, float(scale))
+    o = _flash(q, k, v, freqs, pope_bias, mask, causal, float(scale))
     return o.to(out_dtype) if o.dtype != out_dtype else o
 
 

@@ -165,3 +165,25 @@ def test_last_error_is_per_thread():
     t.join()
     assert "multiple of 8" in _lib.last_error()
     assert seen["msg"] == ""
+
+
+def test_flash_wrappers_check_shapes_before_any_call():
+    """Shapes the kernels index by but the descriptor does not carry (v, mask, lse, o, do) are
+    checked on the host when a call plan is built; CPU tensors never reach the library."""
+    import torch
+    from pope_amd.hip_pope_flash_attn import _bwd_impl, _fwd_impl
+    B, H, N, D, R = 1, 2, 64, 32, 16
+    q = torch.zeros(B, H, N, D, dtype=torch.bfloat16)
+    k, v = torch.zeros_like(q), torch.zeros_like(q)
+    f, b = torch.zeros(N, R), torch.zeros(1, R)
+    with pytest.raises(ValueError, match="v "):
+        _fwd_impl(q, k, v[:, :, :N - 1], f, b, None, False, 0.1)
+    with pytest.raises(ValueError, match="mask"):
+        _fwd_impl(q, k, v, f, b, torch.ones(B, N + 1, dtype=torch.bool), False, 0.1)
+    with pytest.raises(ValueError, match="positions"):
+        _fwd_impl(q, k, v, f[: N - 1], b, None, False, 0.1)
+    lse = torch.zeros(B, H, N)
+    with pytest.raises(ValueError, match="lse"):
+        _bwd_impl(q, q, k, v, q, lse[:, :, 1:], f, b, None, True, 0.1, False, False)
+    with pytest.raises(ValueError, match="must match q"):
+        _bwd_impl(q[:, :, 1:], q, k, v, q, lse, f, b, None, True, 0.1, False, False)

@@ -181,3 +181,36 @@ def test_readme_fused_flash_attn(cuda):
     mask = torch.ones((2, 1024)).bool().cuda()
     out = pope_amd.flash_attn_with_pope(q, k, v, pos_emb=pope(1024), causal=True, mask=mask)
     assert out.shape == (2, 8, 1024, 64)
+
+
+def test_registered_ops_match_eager_path(cuda):
+    """The torch.library ops (used under torch.compile tracing) and the eager autograd path run the
+    same kernels: outputs equal, gradients equal up to the order of the fp32 atomic adds."""
+    from pope_amd.hip_pope_flash_attn import _flash, flash_fwd_op
+    inp = make_pope_inputs(7, 2, 4, 2, 192, 256, 64, 32, torch.bfloat16, "prefix")
+
+    def grads(fn):
+        q, k, v, f, b = (inp[n].detach().clone().requires_grad_(True) for n in ("q", "k", "v", "freqs", "bias"))
+        o = fn(q, k, v, f, b, inp["mask"], True, 0.125)
+        o.backward(inp["do"])
+        return [o] + [t.grad for t in (q, k, v, f, b)]
+
+    eager = grads(_flash)
+    via_ops = grads(lambda *a: flash_fwd_op(*a)[0])
+    assert torch.equal(eager[0], via_ops[0])
+    for a, b in zip(eager[1:], via_ops[1:]):
+        assert (a.float() - b.float()).abs().max().item() <= 1e-3 * max(1.0, a.float().abs().max().item())
+
+
+def test_compiled_call_records_ops(cuda):
+    """torch.compile traces the registered ops (no graph break) and gives the eager results."""
+    import pope_amd
+    inp = make_pope_inputs(8, 1, 2, 2, 128, 128, 64, 32, torch.bfloat16, "none")
+
+    def f(q, k, v, fr, b):
+        return pope_amd.flash_attn_with_pope(q, k, v, pos_emb=(fr, b), causal=True)
+
+    args = [inp[n].detach().clone() for n in ("q", "k", "v", "freqs", "bias")]
+    ref = f(*args)
+    out = torch.compile(f, backend="aot_eager", fullgraph=True)(*args)
+    assert torch.equal(out, ref)
