@@ -22,7 +22,9 @@
 //                  across the LPK lanes, scaled scores to LDS.  Pass 2 takes each
 //                  head's max over the split and streams V, accumulating p * v.
 //                  In both passes the loads of the next batch of keys are issued
-//                  before the current batch is computed.  The KP partial states
+//                  before the current batch is computed; the loads are branch-free and the
+//                  batch loops uniform, so each wait covers only the batch being computed.
+//                  With every dim rotated (R == D) the scores run without per-key branches.  The KP partial states
 //                  of a head merge through LDS into one (m, l, o) per (batch,
 //                  head, split).
 //   decode_combine : merges the splits of each (batch, head) by their log-sum-exp
@@ -32,6 +34,8 @@
 //   a_d c_jd cos((F_q,d - b_d) - F_j,d)
 //     = c_jd [a_d cos(F_q,d - b_d) cos F_j,d + a_d sin(F_q,d - b_d) sin F_j,d],
 // so the key side needs only cos / sin(F_j) (shared by every head and batch).
+#include <type_traits>
+
 #include "pope_common.hpp"
 #include "pope_kernels.hpp"
 
@@ -42,7 +46,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kSplit = 128;    // keys per split (one workgroup)
 constexpr int kMaxHG = 16;     // query heads per pass of a workgroup
-constexpr int kBatch = 8;      // keys per batch (loads issued together)
+constexpr int kBatch = 4;      // keys per batch (loads issued together)
 constexpr int kMaxR = 128;
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
@@ -158,14 +162,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
   }
   __syncthreads();
 
-  const int nb = (nkeys - kp + KP * kBatch - 1) / (KP * kBatch);   // batches of this thread
+  // batches per thread, the same for every lane (uniform loops, so the loads can be counted) and
+  // even (the loops below take batches in pairs); keys past the split score -inf
+  int nbu = (nkeys + KP * kBatch - 1) / (KP * kBatch);
+  nbu = max(2, nbu + (nbu & 1));
   // keys of a batch past the split end read clamped rows and score -inf (vis_s = 0)
   for (int hg0 = 0; hg0 < p.Hq; hg0 += HG) {
     const int h = hg0 + hl;
     const bool hact = active && h < p.Hq;
     const int hs = hact ? h : 0;
     const int hk = hs % p.Hk;
-    const int nbh = hact ? nb : 0;
 
     // ---- query weights of this thread's 8 dims (scale and log2(e) folded in) -----
     // rotated dims: (wa, wb) as an fp16 pair for v_dot2 with the (cos, sin) table pair
@@ -188,13 +194,68 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
     // two register sets alternate (no copies): while one batch is computed, the next
     // one's loads are in flight
     u32x4 bufA[kBatch], bufB[kBatch];
-    auto fetch = [&](u32x4* buf, const uint16_t* base, int64_t row_stride, int bt) {
+    // Branch-free loads, so the compiler can count them and wait only for the batch it computes:
+    // every lane reads a valid address (rows past the cache clamp to its last row, chunks past D
+    // to the last chunk, idle lanes read their head's rows; their data meet zero weights or are
+    // never stored).  Masked keys are dropped at the score, so no load waits on a mask byte.
+    // Offsets within one (batch, head) fit in 32 bits (checked on the host).
+    // per lane: its first row (key j_begin + kp; idle lanes take the last parity) and how many
+    // rows past it exist, so a load needs one clamp and one multiply-add
+    const int kpl = min(kp, KP - 1);
+    const int rows_left = Nk - 1 - j_begin - kpl;
+    const int ks2 = (int)p.k_s[2], vs2 = (int)p.v_s[2];
+    const uint16_t* klane = kbase + ((j_begin + kpl) * ks2 + min(d0, D - 8));
+    const uint16_t* vlane = vbase + ((j_begin + kpl) * vs2 + min(d0, D - 8));
+    auto fetch = [&](u32x4* buf, const uint16_t* lanep, int row_stride, int bt) {
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
-        // unconditional loads (rows past the cache clamp to its last row): no load waits on
-        // a mask byte, masked keys are dropped at the score
-        const int j = min(j_begin + kp + (bt * kBatch + u) * KP, Nk - 1);
-        buf[u] = cact ? ld16(base + (int64_t)j * row_stride + d0) : u32x4{0u, 0u, 0u, 0u};
+        const int r = min((bt * kBatch + u) * KP, rows_left);
+        buf[u] = ld16(lanep + r * row_stride);
+      }
+    };
+    // LDS byte address of the lane's table chunk in row 0 (lanes past D read the last staged
+    // chunk: finite values that meet their zero weights)
+    const uint32_t tab_lane = lds_addr(tab_s + min(d0, max(R, 8) - 8));
+    // every dim rotated (R == D): one straight-line score per key, softplus(x) = max(x, 0) +
+    // ln 2 log2(1 + 2^(-|x| log2 e)) with the max taken on the bit pattern (x >= 0 iff its
+    // signed bits are), no per-key branch
+    auto score_rot = [&](const u32x4* cur, int bt) {
+      // the batch's keys side by side: independent chains between the transcendentals and the
+      // dot products (no dependent back-to-back instructions)
+      float part[kBatch];
+      u32x4 t0[kBatch], t1[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int jl = kp + (bt * kBatch + u) * KP;
+        const uint32_t ta = tab_lane + 4 * TS * min(jl, kSplit - 1);
+        t0[u] = lds_read16_at(ta);
+        t1[u] = lds_read16_at(ta + 16);
+        part[u] = 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        float e[kBatch], mx[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const uint32_t w = cur[u][q >> 1];
+          const uint32_t xb = T::kCode == 2 ? ((q & 1) ? (w & 0xffff0000u) : (w << 16))
+                                            : __builtin_bit_cast(uint32_t, T::to_float((uint16_t)((q & 1) ? (w >> 16) : (w & 0xffffu))));
+          e[u] = __builtin_amdgcn_exp2f(-fabsf(__builtin_bit_cast(float, xb)) * kLog2e);
+          mx[u] = __builtin_bit_cast(float, max((int)xb, 0));
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) e[u] = __builtin_amdgcn_logf(1.f + e[u]);
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const f16x2 cs = __builtin_bit_cast(f16x2, q < 4 ? t0[u][q] : t1[u][q - 4]);
+          part[u] = fmaf(fmaf(e[u], kLn2, mx[u]), __builtin_amdgcn_fdot2(cs, wab[q], 0.f, false), part[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int jl = kp + (bt * kBatch + u) * KP;
+        const float sc = group_sum<LPK>(part[u]);
+        if (c == 0 && active && jl < kSplit) s_lds[hl][jl] = vis_s[jl] ? sc : -INFINITY;
       }
     };
     auto score = [&](const u32x4* cur, int bt) {
@@ -218,20 +279,30 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
           for (int q = 0; q < 8; ++q) part += wa[q] * x[q];
         }
         part = group_sum<LPK>(part);
-        if (c == 0 && jl < kSplit) s_lds[hl][jl] = vis_s[jl] ? part : -INFINITY;
+        if (c == 0 && active && jl < kSplit) s_lds[hl][jl] = vis_s[jl] ? part : -INFINITY;
       }
     };
-    if (nbh > 0) fetch(bufA, kbase, p.k_s[2], 0);
-    for (int bt = 0; bt < nbh; bt += 2) {
-      if (bt + 1 < nbh) fetch(bufB, kbase, p.k_s[2], bt + 1);
-      score(bufA, bt);
-      if (bt + 1 < nbh) {
-        if (bt + 2 < nbh) fetch(bufA, kbase, p.k_s[2], bt + 2);
-        score(bufB, bt + 1);
+    // straight-line prefetch (the last pair peeled): while one batch is computed the next is in
+    // flight, and the first V batch is in flight while the K pass ends and the maxima are reduced
+    auto kpass = [&](auto all_rot) {
+      auto sc = [&](const u32x4* cur, int bt) {
+        if constexpr (decltype(all_rot)::value) score_rot(cur, bt);
+        else score(cur, bt);
+      };
+      fetch(bufA, klane, ks2, 0);
+      for (int bt = 0; bt + 2 < nbu; bt += 2) {
+        fetch(bufB, klane, ks2, bt + 1);
+        sc(bufA, bt);
+        fetch(bufA, klane, ks2, bt + 2);
+        sc(bufB, bt + 1);
       }
-    }
-    // the first V batch is in flight while the heads' maxima are reduced
-    if (nbh > 0) fetch(bufA, vbase, p.v_s[2], 0);
+      fetch(bufB, klane, ks2, nbu - 1);
+      sc(bufA, nbu - 2);
+      fetch(bufA, vlane, vs2, 0);
+      sc(bufB, nbu - 1);
+    };
+    if (R == D) kpass(std::true_type{});
+    else kpass(std::false_type{});
     __syncthreads();
 
     // ---- each head's max over the split (LPK * KP threads per head) -----------------
@@ -264,14 +335,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
         lsum += pv;
       }
     };
-    for (int bt = 0; bt < nbh; bt += 2) {
-      if (bt + 1 < nbh) fetch(bufB, vbase, p.v_s[2], bt + 1);
+    for (int bt = 0; bt + 2 < nbu; bt += 2) {
+      fetch(bufB, vlane, vs2, bt + 1);
       accumulate(bufA, bt);
-      if (bt + 1 < nbh) {
-        if (bt + 2 < nbh) fetch(bufA, vbase, p.v_s[2], bt + 2);
-        accumulate(bufB, bt + 1);
-      }
+      fetch(bufA, vlane, vs2, bt + 2);
+      accumulate(bufB, bt + 1);
     }
+    fetch(bufB, vlane, vs2, nbu - 1);
+    accumulate(bufA, nbu - 2);
+    accumulate(bufB, nbu - 1);
 
     // ---- merge the KP key parities of each (head, chunk), write the partial -------
 #pragma unroll

@@ -510,6 +510,10 @@ int pope_flash_decode(const pope_desc* d, const void* q, const void* k, const vo
   if (d->Nq != 1 || d->causal || d->D > 128)
     return fail(POPE_ERR_UNSUPPORTED, "decode kernel covers one non-causal query row with head dim <= 128 "
                                       "(got %d rows, causal %d, head dim %d)", d->Nq, d->causal, d->D);
+  // the split kernel addresses rows of one (batch, head) with 32-bit element offsets
+  if ((int64_t)(d->Nk - 1) * std::max(d->k_s[2], d->v_s[2]) + d->D >= INT32_MAX)
+    return fail(POPE_ERR_UNSUPPORTED, "decode kernel: K / V row offsets exceed 32 bits (rows %d, strides %lld, %lld)",
+                d->Nk, (long long)d->k_s[2], (long long)d->v_s[2]);
   if ((rc = check_ws(decode_ws(*d), workspace, workspace_bytes))) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const Geo g = geometry(*d, d->Hq);
