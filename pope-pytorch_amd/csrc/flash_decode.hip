@@ -10,23 +10,21 @@
 // and a handful of flops.  Work decomposition:
 //   decode_setup : the fp16 cos / sin(F_j) table of the keys and each (batch,
 //                  head)'s query weights (below), once per call;
-//   decode_split : one workgroup (4 waves) per (batch, split of kSplit keys),
-//                  covering every query head of the batch.  A split whose keys
-//                  are all masked exits after reading its mask bytes.  The split's
-//                  rows of the cos / sin(F_j) table (fp16 pairs) are staged in LDS
-//                  once and shared by all heads.  LPK lanes share one key row of
-//                  one head (16 bytes each, coalesced); a thread streams every
-//                  KP-th key of the split for its head.  Pass 1 streams K: the
-//                  polar transform of the key (softplus(k) times the staged cos /
-//                  sin) folded with the query's (cos, sin) weights, reduced
-//                  across the LPK lanes, scaled scores to LDS.  Pass 2 takes each
-//                  head's max over the split and streams V, accumulating p * v.
-//                  In both passes the loads of the next batch of keys are issued
-//                  before the current batch is computed; the loads are branch-free and the
-//                  batch loops uniform, so each wait covers only the batch being computed.
-//                  With every dim rotated (R == D) the scores run without per-key branches.  The KP partial states
-//                  of a head merge through LDS into one (m, l, o) per (batch,
-//                  head, split).
+//   decode_split : one workgroup (4 waves) per (batch, split of S keys), covering
+//                  every query head of the batch; wave w takes heads w, w + 4, ...
+//                  A split whose keys are all masked exits after reading its mask
+//                  bytes.  The split's rows of the cos / sin(F_j) table (fp16 pairs)
+//                  are staged in LDS once and shared by all heads.  A wave load reads
+//                  64 / LPK consecutive key rows of one head (LPK lanes x 16 bytes per
+//                  row), so every wave streams contiguous memory; all K and V rows of a
+//                  head are in flight before its scores are computed, and the next
+//                  head's rows are loaded while the current head is finished.  Per key:
+//                  the polar transform of the key (softplus(k) times the staged cos /
+//                  sin) folded with the query's (cos, sin) weights, summed over the
+//                  row's lanes; the head's max, sum and p-weighted V rows reduce across
+//                  the rows by lane shuffles into one (m, l, o) per (batch, head, split).
+//                  Loads are branch-free (clamped addresses), so each wait covers only
+//                  the rows being computed.
 //   decode_combine : merges the splits of each (batch, head) by their log-sum-exp
 //                  and writes o (input dtype) and lse (natural log, -inf when
 //                  every key is masked).
@@ -44,10 +42,6 @@ namespace pope {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kSplit = 128;    // keys per split (one workgroup)
-constexpr int kMaxHG = 16;     // query heads per pass of a workgroup
-constexpr int kBatch = 4;      // keys per batch (loads issued together)
-constexpr int kMaxR = 128;
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
@@ -107,35 +101,56 @@ __global__ __launch_bounds__(256) void decode_setup_kernel(DecodeParams p, int t
   p.qw[idx] = w;
 }
 
-// Thread layout: t = c + LPK * (hl + HG * kp): c = 8-dim chunk of the head dim, hl =
-// head within the pass, kp = key parity (the thread streams keys kp, kp + KP, ...).
-template <typename T, int LPK, int RMAX>
-__global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams p, int HG, int KP) {
-  // fp16 (cos, sin) per dim; rows padded by 16 bytes so the key groups of a wave start on
-  // different banks
-  constexpr int TS = RMAX + 4;
-  __shared__ __attribute__((aligned(16))) uint32_t tab_s[kSplit * TS];
-  __shared__ float s_lds[kMaxHG][kSplit];
-  __shared__ float red_o[kThreads][8];
-  __shared__ float red_ml[kThreads / LPK][2];
-  __shared__ uint8_t vis_s[kSplit];
+// Split kernel.  A workgroup (4 waves) owns one (batch, split of S keys) for every query head;
+// wave w takes heads w, w + 4, ...  Lane = row r * LPK + chunk c: a load instruction of a wave
+// reads RPI = 64 / LPK consecutive key rows of one head (LPK lanes x 16 bytes per row), so a
+// wave streams contiguous memory, and load u of a head covers keys u * RPI + r.  A head's
+// kLoads K rows and kLoads V rows are all in flight before its scores are computed (the V
+// loads land while the K side is computed).  Per key: the polar-transform score summed over
+// the row's LPK lanes (DPP), masked keys -inf; the head's max, sum and p-weighted V rows are
+// reduced across the RPI rows by lane shuffles, and the row-0 lanes write the partial.
+constexpr int kLoads = 16;
 
-  const int tid = threadIdx.x;
+template <int LPK>
+constexpr int split_rows() { return kLoads * (64 / LPK); }
+
+// Sum over the lanes that share a chunk (lane bits above the LPK ones).
+template <int LPK>
+__device__ __forceinline__ float rows_sum(float x) {
+#pragma unroll
+  for (int m = LPK; m < 64; m <<= 1) x += __shfl_xor(x, m, 64);
+  return x;
+}
+template <int LPK>
+__device__ __forceinline__ float rows_max(float x) {
+#pragma unroll
+  for (int m = LPK; m < 64; m <<= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
+  return x;
+}
+
+template <typename T, int LPK, int RMAX>
+__global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams p) {
+  constexpr int RPI = 64 / LPK;          // key rows per load instruction
+  constexpr int S = split_rows<LPK>();   // keys per split
+  constexpr int TS = RMAX + 4;           // table row stride (words; 16-byte pad spreads banks)
+  __shared__ __attribute__((aligned(16))) uint32_t tab_s[S * TS];
+  __shared__ uint8_t vis_s[S];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane / LPK, c = lane % LPK;
   const int split = blockIdx.x % p.splits;
   const int b = blockIdx.x / p.splits;
   const int D = p.D, R = p.R, Nk = p.Nk;
-  const int c = tid % LPK, rest = tid / LPK, hl = rest % HG, kp = rest / HG;
-  const bool active = kp < KP;
   const int d0 = 8 * c;
-  const bool cact = active && d0 < D;
+  const bool cact = d0 < D;
   const bool rot = cact && d0 < R;   // R is a multiple of 8: a chunk is all rotated or all pass-through
-  const int j_begin = split * kSplit;
-  const int nkeys = min(kSplit, Nk - j_begin);
+  const int j_begin = split * S;
+  const int nkeys = min(S, Nk - j_begin);
   const uint8_t* mrow = p.has_mask ? p.mask + (int64_t)b * p.mask_sb : nullptr;
 
   // ---- key visibility of the split into LDS; skip splits without a visible key ----
   int vis_any = 0;
-  for (int j = tid; j < kSplit; j += kThreads) {
+  for (int j = tid; j < S; j += kThreads) {
     const int v = j < nkeys && (!p.has_mask || mrow[j_begin + j] != 0);
     vis_s[j] = (uint8_t)v;
     vis_any |= v;
@@ -153,224 +168,134 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
   // ---- stage the split's table rows (rows past Nk repeat the last row) ---------
   if (R) {
     const uint32_t* tsrc = p.table + (int64_t)b * p.t_sb;
-    const int n4 = kSplit * R / 4;
+    const int n4 = S * R / 4;
     for (int i = tid; i < n4; i += kThreads) {
-      const int r = i / (R / 4), c4 = i % (R / 4);
-      const int jj = min(j_begin + r, Nk - 1);
-      *reinterpret_cast<u32x4*>(tab_s + r * TS + 4 * c4) = reinterpret_cast<const u32x4*>(tsrc + (int64_t)jj * R)[c4];
+      const int rr = i / (R / 4), c4 = i % (R / 4);
+      const int jj = min(j_begin + rr, Nk - 1);
+      *reinterpret_cast<u32x4*>(tab_s + rr * TS + 4 * c4) = reinterpret_cast<const u32x4*>(tsrc + (int64_t)jj * R)[c4];
     }
   }
   __syncthreads();
 
-  // batches per thread, the same for every lane (uniform loops, so the loads can be counted) and
-  // even (the loops below take batches in pairs); keys past the split score -inf
-  int nbu = (nkeys + KP * kBatch - 1) / (KP * kBatch);
-  nbu = max(2, nbu + (nbu & 1));
-  // keys of a batch past the split end read clamped rows and score -inf (vis_s = 0)
-  for (int hg0 = 0; hg0 < p.Hq; hg0 += HG) {
-    const int h = hg0 + hl;
-    const bool hact = active && h < p.Hq;
-    const int hs = hact ? h : 0;
-    const int hk = hs % p.Hk;
+  // Branch-free loads: every lane reads a valid address (rows past the cache clamp to its last
+  // row, chunks past D to the last chunk; their data meet zero weights or are never stored), so
+  // the compiler counts them.  Offsets within one (batch, head) fit in 32 bits (host check).
+  const int dcl = min(d0, D - 8);
+  const int rows_left = Nk - 1 - j_begin - r;
+  const int ks2 = (int)p.k_s[2], vs2 = (int)p.v_s[2];
+  // LDS byte address of the lane's table chunk in its first row (chunks past R read the last
+  // staged chunk: finite values that meet zero weights)
+  const uint32_t tab_lane = lds_addr(tab_s + r * TS + min(d0, max(R, 8) - 8));
 
-    // ---- query weights of this thread's 8 dims (scale and log2(e) folded in) -----
-    // rotated dims: (wa, wb) as an fp16 pair for v_dot2 with the (cos, sin) table pair
-    float wa[8], wb[8];
+  constexpr int kWaves = kThreads / 64;
+  auto kptr = [&](int h) {
+    return p.k + (int64_t)b * p.k_s[0] + (int64_t)(h % p.Hk) * p.k_s[1] + ((j_begin + r) * ks2 + dcl);
+  };
+  auto vptr = [&](int h) {
+    return p.v + (int64_t)b * p.v_s[0] + (int64_t)(h % p.Hk) * p.v_s[1] + ((j_begin + r) * vs2 + dcl);
+  };
+  u32x4 kb[kLoads], vb[kLoads];
+  auto load = [&](u32x4* buf, const uint16_t* lp, int stride) {
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) buf[u] = ld16(lp + min(u * RPI, rows_left) * stride);
+  };
+  // Head h of this wave; with `next` the K rows of head h + kWaves are loaded as soon as the K
+  // side of h is done and its V rows as soon as the V side is (the last head of the wave,
+  // taken without, loads nothing more).
+  auto head = [&](int h, auto next) {
+    constexpr bool kNext = decltype(next)::value;
+
+    // query weights of this lane's 8 dims (scale and log2(e) folded in): rotated dims
+    // (wa, wb) as an fp16 pair for v_dot2 with the (cos, sin) table pair; pass-through (q, 0)
+    float wa[8];
     f16x2 wab[8];
     {
-      const float2* qwr = p.qw + ((int64_t)b * p.Hq + hs) * D + min(d0, D - 8);
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const float2 w = cact ? qwr[s] : make_float2(0.f, 0.f);
-        wa[s] = w.x;
-        wb[s] = w.y;
-        wab[s] = f16x2{(_Float16)wa[s], (_Float16)wb[s]};
-      }
-    }
-    const uint16_t* kbase = p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1];
-    const uint16_t* vbase = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
-
-    // ---- pass 1: scaled scores into LDS ---------------------------------------------
-    // two register sets alternate (no copies): while one batch is computed, the next
-    // one's loads are in flight
-    u32x4 bufA[kBatch], bufB[kBatch];
-    // Branch-free loads, so the compiler can count them and wait only for the batch it computes:
-    // every lane reads a valid address (rows past the cache clamp to its last row, chunks past D
-    // to the last chunk, idle lanes read their head's rows; their data meet zero weights or are
-    // never stored).  Masked keys are dropped at the score, so no load waits on a mask byte.
-    // Offsets within one (batch, head) fit in 32 bits (checked on the host).
-    // per lane: its first row (key j_begin + kp; idle lanes take the last parity) and how many
-    // rows past it exist, so a load needs one clamp and one multiply-add
-    const int kpl = min(kp, KP - 1);
-    const int rows_left = Nk - 1 - j_begin - kpl;
-    const int ks2 = (int)p.k_s[2], vs2 = (int)p.v_s[2];
-    const uint16_t* klane = kbase + ((j_begin + kpl) * ks2 + min(d0, D - 8));
-    const uint16_t* vlane = vbase + ((j_begin + kpl) * vs2 + min(d0, D - 8));
-    auto fetch = [&](u32x4* buf, const uint16_t* lanep, int row_stride, int bt) {
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int r = min((bt * kBatch + u) * KP, rows_left);
-        buf[u] = ld16(lanep + r * row_stride);
-      }
-    };
-    // LDS byte address of the lane's table chunk in row 0 (lanes past D read the last staged
-    // chunk: finite values that meet their zero weights)
-    const uint32_t tab_lane = lds_addr(tab_s + min(d0, max(R, 8) - 8));
-    // every dim rotated (R == D): one straight-line score per key, softplus(x) = max(x, 0) +
-    // ln 2 log2(1 + 2^(-|x| log2 e)) with the max taken on the bit pattern (x >= 0 iff its
-    // signed bits are), no per-key branch
-    auto score_rot = [&](const u32x4* cur, int bt) {
-      // the batch's keys side by side: independent chains between the transcendentals and the
-      // dot products (no dependent back-to-back instructions)
-      float part[kBatch];
-      u32x4 t0[kBatch], t1[kBatch];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int jl = kp + (bt * kBatch + u) * KP;
-        const uint32_t ta = tab_lane + 4 * TS * min(jl, kSplit - 1);
-        t0[u] = lds_read16_at(ta);
-        t1[u] = lds_read16_at(ta + 16);
-        part[u] = 0.f;
-      }
+      const float2* qwr = p.qw + ((int64_t)b * p.Hq + h) * D + dcl;
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        float e[kBatch], mx[kBatch];
+        const float2 w = cact ? qwr[q] : make_float2(0.f, 0.f);
+        wa[q] = w.x;
+        wab[q] = f16x2{(_Float16)w.x, (_Float16)w.y};
+      }
+    }
+
+    // ---- scores (log2 units) of the lane's kLoads keys ---------------------------------
+    float sc[kLoads];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          const uint32_t w = cur[u][q >> 1];
+    for (int u = 0; u < kLoads; ++u) {
+      float part = 0.f;
+      if (R == D || rot) {
+        // softplus(x) = max(x, 0) + ln 2 log2(1 + 2^(-|x| log2 e)), the max taken on the bit
+        // pattern (x >= 0 iff its signed bits are)
+        const uint32_t ta = tab_lane + 4 * TS * RPI * u;
+        const u32x4 t0 = lds_read16_at(ta), t1 = lds_read16_at(ta + 16);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const uint32_t w = kb[u][q >> 1];
           const uint32_t xb = T::kCode == 2 ? ((q & 1) ? (w & 0xffff0000u) : (w << 16))
                                             : __builtin_bit_cast(uint32_t, T::to_float((uint16_t)((q & 1) ? (w >> 16) : (w & 0xffffu))));
-          e[u] = __builtin_amdgcn_exp2f(-fabsf(__builtin_bit_cast(float, xb)) * kLog2e);
-          mx[u] = __builtin_bit_cast(float, max((int)xb, 0));
+          const float e = __builtin_amdgcn_exp2f(-fabsf(__builtin_bit_cast(float, xb)) * kLog2e);
+          const float sp = fmaf(__builtin_amdgcn_logf(1.f + e), kLn2, __builtin_bit_cast(float, max((int)xb, 0)));
+          const f16x2 cs = __builtin_bit_cast(f16x2, q < 4 ? t0[q] : t1[q - 4]);
+          part = fmaf(sp, __builtin_amdgcn_fdot2(cs, wab[q], 0.f, false), part);
         }
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) e[u] = __builtin_amdgcn_logf(1.f + e[u]);
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          const f16x2 cs = __builtin_bit_cast(f16x2, q < 4 ? t0[u][q] : t1[u][q - 4]);
-          part[u] = fmaf(fmaf(e[u], kLn2, mx[u]), __builtin_amdgcn_fdot2(cs, wab[q], 0.f, false), part[u]);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int jl = kp + (bt * kBatch + u) * KP;
-        const float sc = group_sum<LPK>(part[u]);
-        if (c == 0 && active && jl < kSplit) s_lds[hl][jl] = vis_s[jl] ? sc : -INFINITY;
-      }
-    };
-    auto score = [&](const u32x4* cur, int bt) {
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int jl = kp + (bt * kBatch + u) * KP;
+      } else {
         float x[8];
-        unpack8<T>(cur[u], x);
-        float part = 0.f;
-        if (rot) {
-          const u32x4* t = reinterpret_cast<const u32x4*>(tab_s + min(jl, kSplit - 1) * TS + d0);
-          const u32x4 t0 = t[0], t1 = t[1];
+        unpack8<T>(kb[u], x);
 #pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            // (cos, sin) of dim d0 + q dotted with (wa, wb), accumulated in fp32
-            const f16x2 cs = __builtin_bit_cast(f16x2, q < 4 ? t0[q] : t1[q - 4]);
-            part = fmaf(softplus_f(x[q]), __builtin_amdgcn_fdot2(cs, wab[q], 0.f, false), part);
-          }
-        } else {
-#pragma unroll
-          for (int q = 0; q < 8; ++q) part += wa[q] * x[q];
-        }
-        part = group_sum<LPK>(part);
-        if (c == 0 && active && jl < kSplit) s_lds[hl][jl] = vis_s[jl] ? part : -INFINITY;
+        for (int q = 0; q < 8; ++q) part = fmaf(wa[q], x[q], part);
       }
-    };
-    // straight-line prefetch (the last pair peeled): while one batch is computed the next is in
-    // flight, and the first V batch is in flight while the K pass ends and the maxima are reduced
-    auto kpass = [&](auto all_rot) {
-      auto sc = [&](const u32x4* cur, int bt) {
-        if constexpr (decltype(all_rot)::value) score_rot(cur, bt);
-        else score(cur, bt);
-      };
-      fetch(bufA, klane, ks2, 0);
-      for (int bt = 0; bt + 2 < nbu; bt += 2) {
-        fetch(bufB, klane, ks2, bt + 1);
-        sc(bufA, bt);
-        fetch(bufA, klane, ks2, bt + 2);
-        sc(bufB, bt + 1);
-      }
-      fetch(bufB, klane, ks2, nbu - 1);
-      sc(bufA, nbu - 2);
-      fetch(bufA, vlane, vs2, 0);
-      sc(bufB, nbu - 1);
-    };
-    if (R == D) kpass(std::true_type{});
-    else kpass(std::false_type{});
-    __syncthreads();
-
-    // ---- each head's max over the split (LPK * KP threads per head) -----------------
-    float mx = -INFINITY;
-    if (hact)
-      for (int i = c + LPK * kp; i < kSplit; i += LPK * KP) mx = fmaxf(mx, s_lds[hl][i]);
-    red_o[tid][0] = mx;   // partial max per (hl, kp, c)
-    __syncthreads();
-    if (hact) {
-      float m2 = -INFINITY;
-      for (int k2 = 0; k2 < KP; ++k2)
-        for (int c2 = 0; c2 < LPK; ++c2) m2 = fmaxf(m2, red_o[(hl + HG * k2) * LPK + c2][0]);
-      mx = m2;
+      part = group_sum<LPK>(part);
+      sc[u] = vis_s[u * RPI + r] ? part : -INFINITY;
     }
-    __syncthreads();
-    const float mu = mx == -INFINITY ? 0.f : mx;
+    // keep each group of loads where it is issued (the scheduler would otherwise interleave them
+    // with the other group and the waits would cover both)
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kNext) load(kb, kptr(h + kWaves), ks2);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- pass 2: p = exp2(s - m), o += p v ---------------------------------------
+    // ---- softmax over the split for this head, o = sum p v -------------------------------
+    float m = sc[0];
+#pragma unroll
+    for (int u = 1; u < kLoads; ++u) m = fmaxf(m, sc[u]);
+    m = rows_max<LPK>(m);
+    const float mu = m == -INFINITY ? 0.f : m;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float lsum = 0.f;
-    auto accumulate = [&](const u32x4* cur, int bt) {
+    float l = 0.f;
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int jl = kp + (bt * kBatch + u) * KP;
-        const float pv = jl < kSplit ? __builtin_amdgcn_exp2f(s_lds[hl][jl] - mu) : 0.f;   // 0 when masked
-        float x[8];
-        unpack8<T>(cur[u], x);
+    for (int u = 0; u < kLoads; ++u) {
+      const float pv = __builtin_amdgcn_exp2f(sc[u] - mu);   // 0 when masked
+      float x[8];
+      unpack8<T>(vb[u], x);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) acc[s] = fmaf(pv, x[s], acc[s]);
-        lsum += pv;
-      }
-    };
-    for (int bt = 0; bt + 2 < nbu; bt += 2) {
-      fetch(bufB, vlane, vs2, bt + 1);
-      accumulate(bufA, bt);
-      fetch(bufA, vlane, vs2, bt + 2);
-      accumulate(bufB, bt + 1);
+      for (int q = 0; q < 8; ++q) acc[q] = fmaf(pv, x[q], acc[q]);
+      l += pv;
     }
-    fetch(bufB, vlane, vs2, nbu - 1);
-    accumulate(bufA, nbu - 2);
-    accumulate(bufB, nbu - 1);
-
-    // ---- merge the KP key parities of each (head, chunk), write the partial -------
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kNext) load(vb, vptr(h + kWaves), vs2);
+    __builtin_amdgcn_sched_barrier(0);
+    l = rows_sum<LPK>(l);   // every lane of a row group holds the same p: one lane per row counts
 #pragma unroll
-    for (int s = 0; s < 8; ++s) red_o[tid][s] = acc[s];
-    if (c == 0) red_ml[rest][1] = lsum;
-    __syncthreads();
-    if (hact && kp == 0) {
-      float o8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      float L = 0.f;
-      for (int k2 = 0; k2 < KP; ++k2) {
-        const int r2 = hl + HG * k2;
-        L += red_ml[r2][1];
+    for (int q = 0; q < 8; ++q) acc[q] = rows_sum<LPK>(acc[q]);
+    const int64_t row = ((int64_t)b * p.Hq + h) * p.splits + split;
+    if (r == 0 && cact) {
 #pragma unroll
-        for (int s = 0; s < 8; ++s) o8[s] += red_o[r2 * LPK + c][s];
-      }
-      const int64_t row = ((int64_t)b * p.Hq + h) * p.splits + split;
-      if (cact) {
-#pragma unroll
-        for (int s = 0; s < 8; ++s)
-          if (d0 + s < D) p.part_o[row * D + d0 + s] = o8[s];
-      }
-      if (c == 0) {
-        p.part_ml[row * 2] = mx;
-        p.part_ml[row * 2 + 1] = L;
-      }
+      for (int q = 0; q < 8; ++q)
+        if (d0 + q < D) p.part_o[row * D + d0 + q] = acc[q];
     }
-    __syncthreads();
+    if (lane == 0) {
+      p.part_ml[row * 2] = m;
+      p.part_ml[row * 2 + 1] = l;
+    }
+  };
+  if (wave < p.Hq) {
+    load(kb, kptr(wave), ks2);
+    __builtin_amdgcn_sched_barrier(0);
+    load(vb, vptr(wave), vs2);
+    __builtin_amdgcn_sched_barrier(0);
+    int h = wave;
+    for (; h + kWaves < p.Hq; h += kWaves) head(h, std::true_type{});
+    head(h, std::false_type{});
   }
 }
 
@@ -437,9 +362,6 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
 
 template <typename T, int LPK, int RMAX>
 hipError_t launch_t(const DecodeParams& p, hipStream_t s) {
-  int HG = kThreads / LPK < kMaxHG ? kThreads / LPK : kMaxHG;
-  if (p.Hq < HG) HG = p.Hq;
-  const int KP = (kThreads / LPK) / HG;
   const int64_t n_tab = p.R > 0 ? (int64_t)(p.t_sb != 0 ? p.B : 1) * p.Nk * p.R : 0;
   const int tab_blocks = (int)((n_tab + 1023) / 1024);   // 4 entries per thread
   const int qw_blocks = (p.B * p.Hq * p.D + 255) / 256;
@@ -447,7 +369,7 @@ hipError_t launch_t(const DecodeParams& p, hipStream_t s) {
                               s, p, tab_blocks, n_tab);
   if (e != hipSuccess) return e;
   e = launch_named("flash_decode_split", decode_split_kernel<T, LPK, RMAX>, dim3(p.B * p.splits),
-                   dim3(kThreads), s, p, HG, KP);
+                   dim3(kThreads), s, p);
   if (e != hipSuccess) return e;
   return launch_named("flash_decode_combine", decode_combine_kernel<T>, dim3(p.B * p.Hq), dim3(256), s, p);
 }
@@ -463,7 +385,10 @@ hipError_t dispatch(const DecodeParams& p, hipStream_t s) {
 
 }  // namespace
 
-int decode_split_keys() { return kSplit; }
+int decode_split_keys(int D) {
+  const int chunks = (D + 7) / 8;
+  return chunks <= 4 ? split_rows<4>() : chunks <= 8 ? split_rows<8>() : split_rows<16>();
+}
 
 hipError_t launch_flash_decode(const DecodeParams& p, int dtype, hipStream_t s) {
   // per-head phase tables would need a table chunk per head: the general forward covers them

@@ -241,7 +241,7 @@ pope::SimSplit sim_split_planes(const pope_desc& d, char* ws, int op) {
 // (rows, splits, 2) | query weights (rows, D) float2], one split per pope::decode_split_keys()
 // keys.
 int decode_splits(const pope_desc& d) {
-  const int per = pope::decode_split_keys();
+  const int per = pope::decode_split_keys(d.D);
   return (d.Nk + per - 1) / per;
 }
 

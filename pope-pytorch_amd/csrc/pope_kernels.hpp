@@ -159,9 +159,9 @@ struct DecodeParams {
   int64_t q_s[3], k_s[3], v_s[3], o_s[3], f_s[3];
   int64_t bias_sh, mask_sb, t_sb, t_sh;
 };
-// Keys per split of the decode kernel.  Returns hipErrorInvalidValue for shapes the
-// kernel does not cover (Nq != 1, causal, D > 128).
-int decode_split_keys();
+// Keys per split of the decode kernel at head dim D.  launch_flash_decode returns
+// hipErrorInvalidValue for shapes the kernel does not cover (Nq != 1, causal, D > 128).
+int decode_split_keys(int D);
 hipError_t launch_flash_decode(const DecodeParams& p, int dtype, hipStream_t s);
 
 }  // namespace pope
