@@ -66,18 +66,32 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// sin / cos of x (radians) for the fp16 table: x / 2pi as an FMA-split product (about 2^-40
+// absolute for |x| < 2^24), its fraction, and the hardware sine / cosine of revolutions
+// (v_sin_f32 / v_cos_f32, absolute error far below the fp16 half ulp the table keeps).
+__device__ __forceinline__ void sincos_rev(float x, float* s, float* c) {
+#pragma clang fp contract(off)   // hi must stay the rounded product: contracted, lo would count twice
+  constexpr float kHi = 0.15915494f;                                          // fl(1 / 2pi)
+  constexpr float kLo = (float)(0.15915494309189533577 - (double)0.15915494f);   // 1 / 2pi - kHi
+  const float hi = x * kHi;
+  const float lo = fmaf(x, kHi, -hi) + x * kLo;
+  const float fr = (hi - __builtin_rintf(hi)) + lo;   // hi - rint(hi) is exact
+  *s = __builtin_amdgcn_sinf(fr);
+  *c = __builtin_amdgcn_cosf(fr);
+}
+
 // Setup: the fp16 (cos, sin) table of F[bt, n, d] for n < Nk, and each (batch, head)'s query
 // weights (scale * log2 e folded in): rotated dims (a cos(F_q - b), a sin(F_q - b)) with
 // a = softplus(q) and F_q = F[Nk - 1]; pass-through dims (q, 0).
 template <typename T>
 __global__ __launch_bounds__(256) void decode_setup_kernel(DecodeParams p, int tab_blocks, int64_t n_tab) {
   if ((int)blockIdx.x < tab_blocks) {
-    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < n_tab; idx += (int64_t)tab_blocks * 256) {
-      const int d = (int)(idx % p.R);
-      const int64_t rest = idx / p.R;
-      const int n = (int)(rest % p.Nk), bt = (int)(rest / p.Nk);
+    // 32-bit indices (the host keeps the table below 2^31 entries)
+    for (int idx = blockIdx.x * 256 + threadIdx.x; idx < (int)n_tab; idx += tab_blocks * 256) {
+      const int d = idx % p.R, rest = idx / p.R;
+      const int n = rest % p.Nk, bt = rest / p.Nk;
       float sn, cs;
-      sincos_acc(p.freqs[(int64_t)bt * p.f_s[0] + (int64_t)n * p.f_s[2] + d], &sn, &cs);
+      sincos_rev(p.freqs[(int64_t)bt * p.f_s[0] + (int64_t)n * p.f_s[2] + d], &sn, &cs);
       const f16x2 v = {(_Float16)cs, (_Float16)sn};
       p.table[idx] = __builtin_bit_cast(uint32_t, v);
     }

@@ -510,6 +510,10 @@ int pope_flash_decode(const pope_desc* d, const void* q, const void* k, const vo
   if (d->Nq != 1 || d->causal || d->D > 128)
     return fail(POPE_ERR_UNSUPPORTED, "decode kernel covers one non-causal query row with head dim <= 128 "
                                       "(got %d rows, causal %d, head dim %d)", d->Nq, d->causal, d->D);
+  // the setup kernel indexes the key-phase table with 32-bit indices
+  if ((int64_t)d->B * d->Nk * d->R >= INT32_MAX)
+    return fail(POPE_ERR_UNSUPPORTED, "decode kernel: key-phase table of %lld entries exceeds 32-bit indices",
+                (long long)d->B * d->Nk * d->R);
   // the split kernel addresses rows of one (batch, head) with 32-bit element offsets
   if ((int64_t)(d->Nk - 1) * std::max(d->k_s[2], d->v_s[2]) + d->D >= INT32_MAX)
     return fail(POPE_ERR_UNSUPPORTED, "decode kernel: K / V row offsets exceed 32 bits (rows %d, strides %lld, %lld)",
