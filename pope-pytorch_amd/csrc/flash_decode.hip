@@ -318,7 +318,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
   __shared__ float w_s[1024];
   __shared__ float red[4];
-  __shared__ float part[4][128];
+  __shared__ float4 red4[256];
   const int bh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = bh / p.Hq, h = bh % p.Hq;
   const int D = p.D, S = p.splits;
@@ -345,31 +345,44 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
   __syncthreads();
   L = red[0] + red[1] + red[2] + red[3];
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  // thread = (split group g of 4, dim d): 4 groups x up to 64 dims per pass
-  for (int d0 = 0; d0 < D; d0 += 64) {
-    const int d = d0 + lane;
-    float acc = 0.f;
-    if (d < D) {
-      int s = wave;
-      for (; s + 28 < S; s += 32) {   // 8 independent loads in flight
-        float v[8];
+  // thread = (split group g, 4-dim quad q): the groups take every G-th split with 8 loads in
+  // flight, then sum through LDS
+  const int qd = D / 4, G = 256 / qd;
+  const int g = tid / qd, q = tid % qd;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (g < G) {
+    const float4* po4 = reinterpret_cast<const float4*>(po) + q;
+    auto wt = [&](int s) { return s < 1024 ? w_s[s] : __builtin_amdgcn_exp2f(pml[2 * s] - Mu); };
+    int s = g;
+    for (; s + 7 * G < S; s += 8 * G) {
+      float4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = po[(int64_t)(s + 4 * u) * D + d];
+      for (int u = 0; u < 8; ++u) v[u] = po4[(int64_t)(s + u * G) * qd];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int su = s + 4 * u;
-          acc += v[u] * (su < 1024 ? w_s[su] : __builtin_amdgcn_exp2f(pml[2 * su] - Mu));
-        }
+      for (int u = 0; u < 8; ++u) {
+        const float w = wt(s + u * G);
+        acc.x += v[u].x * w; acc.y += v[u].y * w; acc.z += v[u].z * w; acc.w += v[u].w * w;
       }
-      for (; s < S; s += 4) acc += po[(int64_t)s * D + d] * (s < 1024 ? w_s[s] : __builtin_amdgcn_exp2f(pml[2 * s] - Mu));
     }
-    part[wave][lane] = acc;
-    __syncthreads();
-    if (wave == 0 && d < D) {
-      uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1];
-      orow[d] = T::bits((part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane]) * inv);
+    for (; s < S; s += G) {
+      const float4 v = po4[(int64_t)s * qd];
+      const float w = wt(s);
+      acc.x += v.x * w; acc.y += v.y * w; acc.z += v.z * w; acc.w += v.w * w;
     }
-    __syncthreads();
+  }
+  red4[tid] = acc;
+  __syncthreads();
+  if (tid < qd) {
+    float4 o = red4[tid];
+    for (int g2 = 1; g2 < G; ++g2) {
+      const float4 v = red4[g2 * qd + tid];
+      o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
+    }
+    uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1] + 4 * tid;
+    orow[0] = T::bits(o.x * inv);
+    orow[1] = T::bits(o.y * inv);
+    orow[2] = T::bits(o.z * inv);
+    orow[3] = T::bits(o.w * inv);
   }
   if (tid == 0) p.lse[bh] = L > 0.f ? (M + __builtin_amdgcn_logf(L)) * kLn2 : -INFINITY;
 }
