@@ -105,6 +105,8 @@ SHAPES = [
     (2, 2, 2, 64, 64, 64, 32, False, "dead_row"),     # fully masked batch row -> 0
     (1, 2, 2, 1, 2048, 64, 64, False, "prefix"),      # single-query decode, long cache
     (2, 2, 2, 3, 1500, 64, 32, False, "random"),      # short query block, long cache
+    (1, 2, 2, 2048, 2048, 64, 32, True, "prefix"),    # causal, 8 key blocks of 256
+    (1, 1, 1, 2100, 2100, 96, 96, True, "none"),      # causal, wide rows (128-key jobs), ragged end
 ]
 
 
