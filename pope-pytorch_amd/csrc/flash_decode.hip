@@ -66,20 +66,6 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
-// sin / cos of x (radians) for the fp16 table: x / 2pi as an FMA-split product (about 2^-40
-// absolute for |x| < 2^24), its fraction, and the hardware sine / cosine of revolutions
-// (v_sin_f32 / v_cos_f32, absolute error far below the fp16 half ulp the table keeps).
-__device__ __forceinline__ void sincos_rev(float x, float* s, float* c) {
-#pragma clang fp contract(off)   // hi must stay the rounded product: contracted, lo would count twice
-  constexpr float kHi = 0.15915494f;                                          // fl(1 / 2pi)
-  constexpr float kLo = (float)(0.15915494309189533577 - (double)0.15915494f);   // 1 / 2pi - kHi
-  const float hi = x * kHi;
-  const float lo = fmaf(x, kHi, -hi) + x * kLo;
-  const float fr = (hi - __builtin_rintf(hi)) + lo;   // hi - rint(hi) is exact
-  *s = __builtin_amdgcn_sinf(fr);
-  *c = __builtin_amdgcn_cosf(fr);
-}
-
 // Setup: the fp16 (cos, sin) table of F[bt, n, d] for n < Nk, and each (batch, head)'s query
 // weights (scale * log2 e folded in): rotated dims (a cos(F_q - b), a sin(F_q - b)) with
 // a = softplus(q) and F_q = F[Nk - 1]; pass-through dims (q, 0).
