@@ -216,3 +216,15 @@ def test_compiled_call_records_ops(cuda):
     ref = f(*args)
     out = torch.compile(f, backend="aot_eager", fullgraph=True)(*args)
     assert torch.equal(out, ref)
+
+
+def test_registered_op_checks(cuda):
+    """torch.library.opcheck on pope_amd::flash_fwd: schema, autograd registration and the fake
+    (meta) implementation.  Its AOT-dispatch check is left out: it compares every output of a traced
+    and an eager call bit for bit, and the third output, the workspace handed to the backward, holds
+    regions the forward does not write (the backward's row terms, alignment gaps)."""
+    from pope_amd.hip_pope_flash_attn import flash_fwd_op
+    inp = make_pope_inputs(3, 1, 2, 2, 128, 128, 64, 32, torch.bfloat16, "prefix")
+    q, k, v, f, b = (inp[n].detach().clone().requires_grad_(True) for n in ("q", "k", "v", "freqs", "bias"))
+    torch.library.opcheck(flash_fwd_op, (q, k, v, f, b, inp["mask"], True, 0.125),
+                          test_utils=("test_schema", "test_autograd_registration", "test_faketensor"))
