@@ -35,9 +35,11 @@ def _decode_inputs(seed, B, Hq, Hk, Nk, D, R, dtype, lengths=None, dead_row=Fals
 def _run(inp, need_grads=False):
     import pope_amd
     q, k, v = (inp[n].detach().clone().requires_grad_(need_grads) for n in ("q", "k", "v"))
-    freqs = inp["freqs"].detach().clone().requires_grad_(need_grads)
-    bias = inp["bias"].detach().clone().requires_grad_(need_grads)
-    o = pope_amd.flash_attn_with_pope(q, k, v, pos_emb=(freqs, bias), mask=inp["mask"], causal=False)
+    rot = inp["freqs"].shape[-1] > 0
+    freqs = inp["freqs"].detach().clone().requires_grad_(need_grads and rot)
+    bias = inp["bias"].detach().clone().requires_grad_(need_grads and rot)
+    pos = (freqs, bias) if rot else None
+    o = pope_amd.flash_attn_with_pope(q, k, v, pos_emb=pos, mask=inp["mask"], causal=False)
     res = dict(o=o)
     if need_grads:
         o.backward(inp["do"])
@@ -53,6 +55,9 @@ CASES = [
     (2, 2, 2, 3000, 128, 64, torch.bfloat16),         # D = 128
     (2, 2, 2, 3000, 96, 96, torch.bfloat16),          # D = 96 (axial-style)
     (2, 2, 2, 2048, 32, 16, torch.float16),           # D = 32, fp16
+    (1, 5, 5, 2500, 48, 16, torch.bfloat16),          # 5 heads over 4 waves, D = 48 (idle chunk lanes)
+    (2, 1, 1, 4100, 64, 0, torch.float16),            # one head (three idle waves), no rotation
+    (1, 6, 3, 3333, 128, 128, torch.bfloat16),        # GQA 2:1, full rotation at D = 128, ragged
 ]
 
 
