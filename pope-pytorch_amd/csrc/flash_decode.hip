@@ -67,8 +67,9 @@ __device__ __forceinline__ float group_sum(float x) {
 }
 
 // Setup: the fp16 (cos, sin) table of F[bt, n, d] for n < Nk, and each (batch, head)'s query
-// weights (scale * log2 e folded in): rotated dims (a cos(F_q - b), a sin(F_q - b)) with
-// a = softplus(q) and F_q = F[Nk - 1]; pass-through dims (q, 0).
+// weights (scale * log2 e folded in), one 32-bit word per dim: rotated dims the fp16 pair
+// (a cos(F_q - b), a sin(F_q - b)) with a = softplus(q) and F_q = F[Nk - 1]; pass-through dims
+// the fp32 weight q.
 template <typename T>
 __global__ __launch_bounds__(256) void decode_setup_kernel(DecodeParams p, int tab_blocks, int64_t n_tab) {
   if ((int)blockIdx.x < tab_blocks) {
@@ -88,15 +89,15 @@ __global__ __launch_bounds__(256) void decode_setup_kernel(DecodeParams p, int t
   const int d = idx % p.D, bh = idx / p.D;
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const float qv = T::to_float(p.q[(int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + d]);
-  float2 w;
+  uint32_t w;
   if (d < p.R) {
     float sn, cs;
     sincos_acc(p.freqs[(int64_t)b * p.f_s[0] + (int64_t)(p.Nk - 1) * p.f_s[2] + d] - p.bias[(int64_t)hk * p.bias_sh + d],
                &sn, &cs);
     const float a = softplus_f(qv) * p.scale_log2;
-    w = make_float2(a * cs, a * sn);
+    w = __builtin_bit_cast(uint32_t, f16x2{(_Float16)(a * cs), (_Float16)(a * sn)});
   } else {
-    w = make_float2(qv * p.scale_log2, 0.f);
+    w = __builtin_bit_cast(uint32_t, qv * p.scale_log2);
   }
   p.qw[idx] = w;
 }
@@ -194,6 +195,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
   auto vptr = [&](int h) {
     return p.v + (int64_t)b * p.v_s[0] + (int64_t)(h % p.Hk) * p.v_s[1] + ((j_begin + r) * vs2 + dcl);
   };
+  // The query weight words of a head: two 16-byte loads at the clamped chunk, issued before
+  // the head's K rows (waits count loads in issue order, so waiting for the weights leaves the
+  // K and V rows in flight).
+  u32x4 qwc[2];
+  auto qwload = [&](int h) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(p.qw + ((int64_t)b * p.Hq + h) * D + dcl);
+    qwc[0] = src[0];
+    qwc[1] = src[1];
+  };
   u32x4 kb[kLoads], vb[kLoads];
   auto load = [&](u32x4* buf, const uint16_t* lp, int stride) {
 #pragma unroll
@@ -205,19 +215,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
   auto head = [&](int h, auto next) {
     constexpr bool kNext = decltype(next)::value;
 
-    // query weights of this lane's 8 dims (scale and log2(e) folded in): rotated dims
-    // (wa, wb) as an fp16 pair for v_dot2 with the (cos, sin) table pair; pass-through (q, 0)
-    float wa[8];
-    f16x2 wab[8];
-    {
-      const float2* qwr = p.qw + ((int64_t)b * p.Hq + h) * D + dcl;
+    // query weight words of this lane's 8 dims (zero past D): rotated dims an fp16 pair for
+    // v_dot2 with the (cos, sin) table pair, pass-through dims an fp32 weight
+    uint32_t wq[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const float2 w = cact ? qwr[q] : make_float2(0.f, 0.f);
-        wa[q] = w.x;
-        wab[q] = f16x2{(_Float16)w.x, (_Float16)w.y};
-      }
-    }
+    for (int q = 0; q < 8; ++q) wq[q] = cact ? qwc[q >> 2][q & 3] : 0u;
 
     // ---- scores (log2 units) of the lane's kLoads keys ---------------------------------
     float sc[kLoads];
@@ -237,13 +239,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
           const float e = __builtin_amdgcn_exp2f(-fabsf(__builtin_bit_cast(float, xb)) * kLog2e);
           const float sp = fmaf(__builtin_amdgcn_logf(1.f + e), kLn2, __builtin_bit_cast(float, max((int)xb, 0)));
           const f16x2 cs = __builtin_bit_cast(f16x2, q < 4 ? t0[q] : t1[q - 4]);
-          part = fmaf(sp, __builtin_amdgcn_fdot2(cs, wab[q], 0.f, false), part);
+          part = fmaf(sp, __builtin_amdgcn_fdot2(cs, __builtin_bit_cast(f16x2, wq[q]), 0.f, false), part);
         }
       } else {
         float x[8];
         unpack8<T>(kb[u], x);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) part = fmaf(wa[q], x[q], part);
+        for (int q = 0; q < 8; ++q) part = fmaf(__builtin_bit_cast(float, wq[q]), x[q], part);
       }
       part = group_sum<LPK>(part);
       sc[u] = vis_s[u * RPI + r] ? part : -INFINITY;
@@ -251,7 +253,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
     // keep each group of loads where it is issued (the scheduler would otherwise interleave them
     // with the other group and the waits would cover both)
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (kNext) load(kb, kptr(h + kWaves), ks2);
+    if constexpr (kNext) {
+      qwload(h + kWaves);
+      load(kb, kptr(h + kWaves), ks2);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- softmax over the split for this head, o = sum p v -------------------------------
@@ -289,6 +294,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
     }
   };
   if (wave < p.Hq) {
+    qwload(wave);
     load(kb, kptr(wave), ks2);
     __builtin_amdgcn_sched_barrier(0);
     load(vb, vptr(wave), vs2);

@@ -254,7 +254,7 @@ size_t decode_ws(const pope_desc& d) {
   const int splits = decode_splits(d);
   const size_t rows = (size_t)d.B * d.Hq * d.Nq;
   return decode_table_bytes(d) + align_up(rows * splits * d.D * sizeof(float)) +
-         align_up(rows * splits * 2 * sizeof(float)) + align_up(rows * d.D * sizeof(float2));
+         align_up(rows * splits * 2 * sizeof(float)) + align_up(rows * d.D * sizeof(uint32_t));
 }
 
 hipError_t build_table(const pope_desc& d, const float* freqs, const float* bias, int Bt, int Ht,
@@ -528,7 +528,7 @@ int pope_flash_decode(const pope_desc* d, const void* q, const void* k, const vo
   const size_t tb = decode_table_bytes(*d);
   float* part_o = reinterpret_cast<float*>(ws + tb);
   float* part_ml = reinterpret_cast<float*>(ws + tb + align_up(rows * splits * d->D * sizeof(float)));
-  float2* qw = reinterpret_cast<float2*>(reinterpret_cast<char*>(part_ml) + align_up(rows * splits * 2 * sizeof(float)));
+  uint32_t* qw = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(part_ml) + align_up(rows * splits * 2 * sizeof(float)));
   pope::DecodeParams p;
   std::memset(&p, 0, sizeof p);
   p.q = static_cast<const uint16_t*>(q);

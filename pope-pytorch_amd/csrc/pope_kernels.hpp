@@ -151,7 +151,7 @@ struct DecodeParams {
   const uint16_t* q; const uint16_t* k; const uint16_t* v;
   const float* freqs; const float* bias; const uint8_t* mask;
   uint32_t* table;           // fp16 (cos, sin) of F[bt, n, d] for n < Nk, packed per 32-bit word
-  float2* qw;                // (B, Hq, D) query weights, written by the decode setup kernel
+  uint32_t* qw;              // (B, Hq, D) query weight words, written by the decode setup kernel
   uint16_t* o; float* lse;
   float* part_o; float* part_ml;   // split-K partials (B*Hq*Nq, splits, D) and (.., splits, 2)
   int B, Hq, Hk, Nq, Nk, D, R, causal, has_mask, splits, keys_per_split;
