@@ -166,18 +166,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
     return;
   }
 
-  // ---- stage the split's table rows (rows past Nk repeat the last row) ---------
-  if (R) {
-    const uint32_t* tsrc = p.table + (int64_t)b * p.t_sb;
-    const int n4 = S * R / 4;
-    for (int i = tid; i < n4; i += kThreads) {
-      const int rr = i / (R / 4), c4 = i % (R / 4);
-      const int jj = min(j_begin + rr, Nk - 1);
-      *reinterpret_cast<u32x4*>(tab_s + rr * TS + 4 * c4) = reinterpret_cast<const u32x4*>(tsrc + (int64_t)jj * R)[c4];
-    }
-  }
-  __syncthreads();
-
   // Branch-free loads: every lane reads a valid address (rows past the cache clamp to its last
   // row, chunks past D to the last chunk; their data meet zero weights or are never stored), so
   // the compiler counts them.  Offsets within one (batch, head) fit in 32 bits (host check).
@@ -209,6 +197,39 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
 #pragma unroll
     for (int u = 0; u < kLoads; ++u) buf[u] = ld16(lp + min(u * RPI, rows_left) * stride);
   };
+
+  // ---- the split's table rows (rows past Nk repeat the last row), then the first head's
+  // weights, K and V rows, all issued before the table is stored to LDS: the K / V loads do not
+  // wait for the table's round trip.  Waves past Hq load a valid head and never use it.
+  constexpr int C4 = RMAX / 4;                        // 16-byte chunks per staged table row
+  constexpr int kTabIt = S * C4 / kThreads;           // table chunks per thread
+  static_assert(S * C4 % kThreads == 0, "whole table chunks per thread");
+  u32x4 tb[kTabIt];
+  if (R) {
+    const uint32_t* tsrc = p.table + (int64_t)b * p.t_sb;
+#pragma unroll
+    for (int it = 0; it < kTabIt; ++it) {
+      const int i = tid + it * kThreads;
+      const int c4 = min(i % C4, R / 4 - 1), jj = min(j_begin + i / C4, Nk - 1);
+      tb[it] = *reinterpret_cast<const u32x4*>(tsrc + (int64_t)jj * R + 4 * c4);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int h0 = min(wave, p.Hq - 1);
+  qwload(h0);
+  load(kb, kptr(h0), ks2);
+  __builtin_amdgcn_sched_barrier(0);
+  load(vb, vptr(h0), vs2);
+  __builtin_amdgcn_sched_barrier(0);
+  if (R) {
+#pragma unroll
+    for (int it = 0; it < kTabIt; ++it) {
+      const int i = tid + it * kThreads;
+      if (i % C4 < R / 4) *reinterpret_cast<u32x4*>(tab_s + (i / C4) * TS + 4 * (i % C4)) = tb[it];
+    }
+  }
+  __syncthreads();
+
   // Head h of this wave; with `next` the K rows of head h + kWaves are loaded as soon as the K
   // side of h is done and its V rows as soon as the V side is (the last head of the wave,
   // taken without, loads nothing more).
@@ -294,11 +315,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
     }
   };
   if (wave < p.Hq) {
-    qwload(wave);
-    load(kb, kptr(wave), ks2);
-    __builtin_amdgcn_sched_barrier(0);
-    load(vb, vptr(wave), vs2);
-    __builtin_amdgcn_sched_barrier(0);
     int h = wave;
     for (; h + kWaves < p.Hq; h += kWaves) head(h, std::true_type{});
     head(h, std::false_type{});
