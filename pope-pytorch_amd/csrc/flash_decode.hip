@@ -112,6 +112,12 @@ __global__ __launch_bounds__(256) void decode_setup_kernel(DecodeParams p, int t
 // reduced across the RPI rows by lane shuffles, and the row-0 lanes write the partial.
 constexpr int kLoads = 16;
 
+// bf16 keys: log2(1 + 2^(-|x| log2 e)) (the softplus term beyond max(x, 0), in log2 units) is
+// tabulated in LDS over the bf16 magnitudes 2^-24 <= |x| < 32, indexed by the 15 magnitude bits
+// less kSpLo.  Smaller magnitudes take the first entry (off by < 1e-7), larger ones the last
+// (the term is below 2e-14 there).  In range, the entry is the value the formula computes.
+constexpr int kSpLo = 103 << 7, kSpN = (132 << 7) - kSpLo;
+
 template <int LPK>
 constexpr int split_rows() { return kLoads * (64 / LPK); }
 
@@ -136,6 +142,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
   constexpr int TS = RMAX + 4;           // table row stride (words; 16-byte pad spreads banks)
   __shared__ __attribute__((aligned(16))) uint32_t tab_s[S * TS];
   __shared__ uint8_t vis_s[S];
+  __shared__ float sp_s[T::kCode == 2 ? kSpN : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane / LPK, c = lane % LPK;
@@ -228,6 +235,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
       if (i % C4 < R / 4) *reinterpret_cast<u32x4*>(tab_s + (i / C4) * TS + 4 * (i % C4)) = tb[it];
     }
   }
+  if constexpr (T::kCode == 2) {
+    for (int i = tid; i < kSpN; i += kThreads) {
+      const float t = __builtin_bit_cast(float, (uint32_t)(i + kSpLo) << 16);
+      sp_s[i] = __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(-t * kLog2e));
+    }
+  }
   __syncthreads();
 
   // Head h of this wave; with `next` the K rows of head h + kWaves are loaded as soon as the K
@@ -257,8 +270,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
           const uint32_t w = kb[u][q >> 1];
           const uint32_t xb = T::kCode == 2 ? ((q & 1) ? (w & 0xffff0000u) : (w << 16))
                                             : __builtin_bit_cast(uint32_t, T::to_float((uint16_t)((q & 1) ? (w >> 16) : (w & 0xffffu))));
-          const float e = __builtin_amdgcn_exp2f(-fabsf(__builtin_bit_cast(float, xb)) * kLog2e);
-          const float sp = fmaf(__builtin_amdgcn_logf(1.f + e), kLn2, __builtin_bit_cast(float, max((int)xb, 0)));
+          float lt;
+          if constexpr (T::kCode == 2) {
+            lt = sp_s[min(max((int)((xb >> 16) & 0x7fffu) - kSpLo, 0), kSpN - 1)];
+          } else {
+            lt = __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(-fabsf(__builtin_bit_cast(float, xb)) * kLog2e));
+          }
+          const float sp = fmaf(lt, kLn2, __builtin_bit_cast(float, max((int)xb, 0)));
           const f16x2 cs = __builtin_bit_cast(f16x2, q < 4 ? t0[q] : t1[q - 4]);
           part = fmaf(sp, __builtin_amdgcn_fdot2(cs, __builtin_bit_cast(f16x2, wq[q]), 0.f, false), part);
         }
