@@ -72,6 +72,24 @@ def test_decode_forward(cuda, case):
     assert err <= TOL
 
 
+def test_decode_extreme_key_magnitudes(cuda):
+    """bf16 keys outside the tabulated softplus range (|x| >= 32, |x| < 2^-24, zeros) and at its
+    edges, sprinkled over N(0, 1) keys: the kernel's table clamps must match the oracle's softplus."""
+    inp = _decode_inputs(41, 2, 4, 4, 3000, 64, 64, torch.bfloat16)
+    g = torch.Generator().manual_seed(43)
+    k = inp["k"].float().cpu()
+    vals = torch.tensor([0.0, -0.0, 2.0 ** -30, -(2.0 ** -30), 2.0 ** -24, 2.0 ** -20, 31.75, -31.75, 32.0, -32.0,
+                         40.0, -40.0, 100.0, -100.0])
+    pick = torch.rand(k.shape, generator=g) < 0.02
+    k[pick] = vals[torch.randint(0, len(vals), (int(pick.sum()),), generator=g)]
+    inp["k"] = k.to(torch.bfloat16).to("cuda")
+    res = _run(inp)
+    ref = oracle_attention(inp, False, grads=False)
+    err = max_abs(res["o"], ref["o"])
+    print(f"o={err:.2e}")
+    assert err <= TOL
+
+
 def test_decode_lse_and_dead_row(cuda):
     from pope_amd.hip_pope_flash_attn import flash_attn_forward
     inp = _decode_inputs(5, 3, 4, 4, 6000, 64, 64, torch.bfloat16, lengths=[6000, 1, 4097], dead_row=True)
