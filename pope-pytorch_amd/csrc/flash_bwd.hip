@@ -127,7 +127,12 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(FlashBwdParams p) {
   if (p.zero_grads) {
     if (p.dbias && gid < (int64_t)p.Hb * p.R) p.dbias[(gid / p.R) * p.bias_sh + gid % p.R] = 0.f;
     const int64_t ndf = (int64_t)p.Bt * p.Ht * p.Nk * p.R;
-    if (p.dfreqs)
+    // dense (bt, ht, n, d) layout (the usual one): a flat range, no index decomposition
+    const bool dense = p.df_s[2] == p.R && (p.Ht == 1 || p.df_s[1] == (int64_t)p.Nk * p.R) &&
+                       (p.Bt == 1 || p.df_s[0] == (int64_t)p.Ht * p.Nk * p.R);
+    if (p.dfreqs && dense)
+      for (int64_t x = gid; x < ndf; x += (int64_t)gridDim.x * 256) p.dfreqs[x] = 0.f;
+    else if (p.dfreqs)
       for (int64_t x = gid; x < ndf; x += (int64_t)gridDim.x * 256) {
         const int d = (int)(x % p.R);
         int64_t rest = x / p.R;
