@@ -73,14 +73,24 @@ __device__ __forceinline__ float group_sum(float x) {
 template <typename T>
 __global__ __launch_bounds__(256) void decode_setup_kernel(DecodeParams p, int tab_blocks, int64_t n_tab) {
   if ((int)blockIdx.x < tab_blocks) {
-    // 32-bit indices (the host keeps the table below 2^31 entries)
-    for (int idx = blockIdx.x * 256 + threadIdx.x; idx < (int)n_tab; idx += tab_blocks * 256) {
-      const int d = idx % p.R, rest = idx / p.R;
+    // four consecutive entries per thread, in one row (R is a multiple of 8): four independent
+    // loads, one 16-byte store; 32-bit indices (the host keeps the table below 2^31 entries)
+    const int i4 = 4 * ((int)blockIdx.x * 256 + (int)threadIdx.x);
+    if (i4 < (int)n_tab) {
+      const int d = i4 % p.R, rest = i4 / p.R;
       const int n = rest % p.Nk, bt = rest / p.Nk;
-      float sn, cs;
-      sincos_rev(p.freqs[(int64_t)bt * p.f_s[0] + (int64_t)n * p.f_s[2] + d], &sn, &cs);
-      const f16x2 v = {(_Float16)cs, (_Float16)sn};
-      p.table[idx] = __builtin_bit_cast(uint32_t, v);
+      const float* f = p.freqs + (int64_t)bt * p.f_s[0] + (int64_t)n * p.f_s[2] + d;
+      float x[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) x[t] = f[t];
+      u32x4 w;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        float sn, cs;
+        sincos_rev(x[t], &sn, &cs);
+        w[t] = __builtin_bit_cast(uint32_t, f16x2{(_Float16)cs, (_Float16)sn});
+      }
+      *reinterpret_cast<u32x4*>(p.table + i4) = w;
     }
     return;
   }
