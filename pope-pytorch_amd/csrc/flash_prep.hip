@@ -29,7 +29,7 @@ struct SetupGrid {
 SetupGrid setup_grid(const FlashPrep& p) {
   SetupGrid g;
   g.n_tab = (int64_t)p.Bt * p.Ht * p.Nk * p.R;
-  const int64_t bt = (g.n_tab + 255) / 256;
+  const int64_t bt = (g.n_tab / 4 + 255) / 256;   // four entries per thread
   g.b_tab = (int)(bt > kSetupBlocksMax ? kSetupBlocksMax : bt);
   g.b_bias = p.R > 0 ? (p.Hb * p.R + 255) / 256 : 0;
   g.b_mask = (p.B * p.NW + 3) / 4;
@@ -38,18 +38,37 @@ SetupGrid setup_grid(const FlashPrep& p) {
 
 __global__ __launch_bounds__(256) void flash_setup_kernel(FlashPrep p, SetupGrid g) {
   const int blk = blockIdx.x;
-  if (blk < g.b_tab) {   // cos/sin(F) rows, grid-stride over (bt, ht, n, d)
-    for (int64_t idx = (int64_t)blk * 256 + threadIdx.x; idx < g.n_tab; idx += (int64_t)g.b_tab * 256) {
-      const int d = (int)(idx % p.R);
-      int64_t rest = idx / p.R;
-      const int n = (int)(rest % p.Nk);
-      rest /= p.Nk;
-      const int ht = (int)(rest % p.Ht);
-      const int bt = (int)(rest / p.Ht);
-      const float th = p.freqs[(int64_t)bt * p.f_s[0] + (int64_t)ht * p.f_s[1] + (int64_t)n * p.f_s[2] + d];
-      float sn, cs;
-      sincos_acc(th, &sn, &cs);
-      p.table[idx] = make_float2(cs, sn);
+  if (blk < g.b_tab) {
+    // cos/sin(F) rows, grid-stride over (bt, ht, n, d): four consecutive entries of one row per
+    // thread (R is a multiple of 8), four independent loads, two 16-byte stores; the index is
+    // decomposed in 32 bits when the table allows
+    for (int64_t i4 = 4 * ((int64_t)blk * 256 + threadIdx.x); i4 < g.n_tab; i4 += 4 * (int64_t)g.b_tab * 256) {
+      int d, n, ht, bt;
+      if (g.n_tab < INT32_MAX) {
+        const int i = (int)i4;
+        d = i % p.R;
+        int rest = i / p.R;
+        n = rest % p.Nk;
+        rest /= p.Nk;
+        ht = rest % p.Ht;
+        bt = rest / p.Ht;
+      } else {
+        d = (int)(i4 % p.R);
+        int64_t rest = i4 / p.R;
+        n = (int)(rest % p.Nk);
+        rest /= p.Nk;
+        ht = (int)(rest % p.Ht);
+        bt = (int)(rest / p.Ht);
+      }
+      const float* f = p.freqs + (int64_t)bt * p.f_s[0] + (int64_t)ht * p.f_s[1] + (int64_t)n * p.f_s[2] + d;
+      float x[4], sn[4], cs[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) x[t] = f[t];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) sincos_acc(x[t], &sn[t], &cs[t]);
+      float4* dst = reinterpret_cast<float4*>(p.table + i4);
+      dst[0] = make_float4(cs[0], sn[0], cs[1], sn[1]);
+      dst[1] = make_float4(cs[2], sn[2], cs[3], sn[3]);
     }
     return;
   }
