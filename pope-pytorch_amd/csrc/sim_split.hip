@@ -83,7 +83,20 @@ __global__ __launch_bounds__(kThreads) void sim_split_prep_kernel(SimParams p, S
   const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (idx >= total) return;
   int bh, n, ch;
-  if (transposed) {
+  if (total < INT32_MAX) {   // the usual case: 32-bit index decomposition
+    const int i = (int)idx;
+    if (transposed) {
+      n = i % NP;
+      const int r = i / NP;
+      ch = r % nch;
+      bh = r / nch;
+    } else {
+      ch = i % nch;
+      const int r = i / nch;
+      n = r % NP;
+      bh = r / NP;
+    }
+  } else if (transposed) {
     n = (int)(idx % NP);
     const int64_t r = idx / NP;
     ch = (int)(r % nch);
