@@ -158,11 +158,20 @@ __global__ __launch_bounds__(256) void flash_prep_kernel(FlashPrep p, PrepGrid g
   const bool is_k = blk < g.b_k;
   const int64_t idx = (int64_t)(is_k ? blk : blk - g.b_k) * 256 + threadIdx.x;
   if (idx >= (is_k ? g.n_k : g.n_q)) return;
-  const int item = (int)(idx % g.nitem);
-  const int64_t row = idx / g.nitem;
   const int NP = is_k ? p.NkP : p.NqP;
-  const int n = (int)(row % NP);
-  const int bh = (int)(row / NP);
+  int item, n, bh;
+  if (idx < INT32_MAX) {   // the usual case: 32-bit index decomposition
+    const int i = (int)idx;
+    item = i % g.nitem;
+    const int row = i / g.nitem;
+    n = row % NP;
+    bh = row / NP;
+  } else {
+    item = (int)(idx % g.nitem);
+    const int64_t row = idx / g.nitem;
+    n = (int)(row % NP);
+    bh = (int)(row / NP);
+  }
   const int H = is_k ? p.Hk : p.Hq;
   const int b = bh / H, h = bh % H;
   uint16_t* out = (is_k ? p.kh : p.qh) + ((int64_t)bh * NP + n) * EP;
