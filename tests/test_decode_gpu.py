@@ -6,8 +6,9 @@ flash, with the oracle in float64 on the same bf16/fp16-rounded inputs.  Cases
 follow BASELINE config C5 in miniature (one query row, PoPE with full rotation,
 valid prefix lengths per batch via the key-padding mask) plus ragged cache
 lengths, head dims 32..128 (including 96, whose 12 chunks of 8 dims leave lanes
-idle), GQA, a batch row with every key masked, fp16, and the backward through
-the decode's log-sum-exp.
+idle), GQA, a batch row with every key masked, fp16, bf16 keys at and beyond the
+range of the kernel's softplus table, and the backward through the decode's
+log-sum-exp.
 """
 import pytest
 import torch
