@@ -148,29 +148,27 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(FlashBwdParams p) {
   const int i = (int)(idx % NqP);
   const int bh = (int)(idx / NqP);
   const int b = bh / p.Hq, h = bh % p.Hq;
+  // padding rows (i >= Nq) read the last row and discard it: the loads, the LSE's included, are
+  // unconditional and issued together
+  const int ic = min(i, p.Nq - 1);
+  const float l = p.lse[(int64_t)bh * p.Nq + ic];
+  const uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1] + (int64_t)ic * p.o_s[2];
+  const uint16_t* drow = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1] + (int64_t)ic * p.do_s[2];
   float dl = 0.f;
-  if (i < p.Nq) {
-    const uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1] + (int64_t)i * p.o_s[2];
-    const uint16_t* drow = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1] + (int64_t)i * p.do_s[2];
-    for (int d0 = 8 * part; d0 < D; d0 += 64) {
-      float xo[8], xd[8];
-      unpack8<T>(ld16(orow + d0), xo);
-      unpack8<T>(ld16(drow + d0), xd);
+  for (int d0 = 8 * part; d0 < D; d0 += 64) {
+    float xo[8], xd[8];
+    unpack8<T>(ld16(orow + d0), xo);
+    unpack8<T>(ld16(drow + d0), xd);
 #pragma unroll
-      for (int s = 0; s < 8; ++s) dl = fmaf(xo[s], xd[s], dl);
-    }
+    for (int s = 0; s < 8; ++s) dl = fmaf(xo[s], xd[s], dl);
   }
   dl += __shfl_xor(dl, 1, 64);
   dl += __shfl_xor(dl, 2, 64);
   dl += __shfl_xor(dl, 4, 64);
   if (part == 0) {
-    float nl = -INFINITY;
-    if (i < p.Nq) {
-      const float l = p.lse[(int64_t)bh * p.Nq + i];
-      nl = l == -INFINITY ? -INFINITY : -l * kLog2e;
-    }
-    p.nl[idx] = nl;
-    p.nd[idx] = -dl;
+    const bool live = i < p.Nq;
+    p.nl[idx] = live && l != -INFINITY ? -l * kLog2e : -INFINITY;
+    p.nd[idx] = live ? -dl : 0.f;
   }
 }
 
