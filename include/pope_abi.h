@@ -59,7 +59,11 @@ enum pope_flags {
    * into hi + lo bf16 halves (three products per pair, 16 significant operand bits, fp32
    * accumulation) -- the counterpart of the reference's default allow_tf32=True (TF32 keeps 10
    * bits, triton_pope.py:63,145,224).  Without it the products are true fp32 MFMA. */
-  POPE_FLAG_SPLIT_BF16 = 4
+  POPE_FLAG_SPLIT_BF16 = 4,
+  /* Polar transform: q_hat / k_hat rows are D (re, im) fp32 pairs, the complex64 layout of the
+   * reference's return_complex=True output (torch.polar, pope.py:49-51,66-67,74-75): the rotated
+   * dims as (a cos, a sin), pass-through dim d as (x_d, 0). */
+  POPE_FLAG_COMPLEX = 8
 };
 
 /*
@@ -166,6 +170,8 @@ int pope_flash_decode(const pope_desc* desc, const void* q, const void* k, const
  * first 2R columns interleave (a cos, a sin) per rotated dim with a = softplus rounded to dtype
  * (:60), the last D - R are the raw pass-through dims (:82-84).  Query rows take the phases
  * freqs[Nk - Nq + i] (:64), key rows fl(freqs[j] + bias[h]) (:56); bias is used as given.
+ * With POPE_FLAG_COMPLEX (the only flag it takes) the rows are (B, H, N, 2 D) instead: complex64
+ * pairs, pass-through dims as (x, 0) (return_complex, :49-51,66-67,74-75).
  */
 int pope_polar_fwd(const pope_desc* desc, const void* q, const void* k, const float* freqs, const float* bias,
                    float* q_hat, float* k_hat, void* stream);
@@ -174,7 +180,9 @@ int pope_polar_fwd(const pope_desc* desc, const void* q, const void* k, const fl
  * Backward of pope_polar_fwd: dq_hat / dk_hat are contiguous fp32 gradients of its outputs;
  * dq, dk (dtype, dq_s / dk_s strides) are written; dfreqs (fp32, df_s strides) and dbias (fp32,
  * bias rows bias_sh) are ACCUMULATED into (NULL = not wanted).  The autograd backward of the
- * reference's torch ops (pope.py:30-86).
+ * reference's torch ops (pope.py:30-86).  With POPE_FLAG_COMPLEX the gradients come in the
+ * complex layout of the forward (a pass-through dim takes sign(x) times the real part of its
+ * pair's gradient: the backward of torch.polar(x, 0) the reference builds it with).
  */
 int pope_polar_bwd(const pope_desc* desc, const float* dq_hat, const float* dk_hat, const void* q, const void* k,
                    const float* freqs, const float* bias, void* dq, void* dk, float* dfreqs, float* dbias,

@@ -14,6 +14,13 @@ How each function is pinned (tests/test_oracle.py, tests/golden/):
   * ``inv_freqs`` / ``pope_freqs`` / ``axial_*``: closed forms
     (freqs[i, j] = i * theta**(-j/dim), reversed-axis grid order) and the
     shapes the reference's tests assert (test_readme.py:36,47).
+  * ``clamp_bias``: closed form on values inside, at and beyond [-2 pi, 0] and
+    the gradient torch's clamp passes (1 inside and at the bounds, 0 beyond).
+  * ``softplus``: torch.nn.functional.softplus (beta 1, threshold 20) over
+    [-100, 100] in float32 and float64, and golden inputs past the threshold.
+  * ``_repeat_heads``: einops.repeat(t, 'b h ... -> b (g h) ...') -- the
+    reference's own layout call (attention.py:44-45) -- and a golden case with
+    Hq = 4, Hk = 2, where h % Hk and h // (Hq / Hk) differ.
   * ``apply_pope_to_qk``: interleave order and raw pass-through dims by
     construction checks, right-aligned query rows, output shapes of
     test_pope.py:21-29 / test_readme.py:18-24,54.
@@ -37,7 +44,7 @@ import torch.nn.functional as F
 __all__ = [
     "inv_freqs", "pope_freqs", "clamp_bias", "axial_inv_freqs", "axial_grid_positions",
     "axial_freqs", "softplus", "apply_pope_to_qk", "sim_nonfused", "flash_nonfused",
-    "flash_lse", "expand_freqs",
+    "flash_lse",
 ]
 
 
@@ -182,7 +189,3 @@ def flash_lse(q, k, freqs=None, bias=None, mask=None, causal=False, softmax_scal
     keep = _attn_mask(q.shape[0], q.shape[-2], k.shape[-2], mask, causal, q.device)
     return torch.logsumexp(s.masked_fill(~keep, float("-inf")), dim=-1)
 
-
-def expand_freqs(freqs: torch.Tensor, B: int) -> torch.Tensor:
-    """(N,R) or (B,N,R) -> (B,N,R) view."""
-    return freqs.expand(B, *freqs.shape) if freqs.ndim == 2 else freqs

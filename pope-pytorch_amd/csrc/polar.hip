@@ -14,6 +14,12 @@
 // Pass-through dims copy g.  dfreqs and dbias are fp32 and accumulated (atomics; dbias summed
 // over the workgroup's rows first).
 //
+// Complex layout (return_complex, pope.py:49-51,66-67,74-75): rows of D (re, im) fp32 pairs, the
+// memory layout of torch.polar's complex64 output.  The rotated dims are the same interleaved
+// pairs; pass-through dim d is the pair (q_d, 0) at columns 2d, 2d + 1, and its gradient is
+// sign(q_d) times the real part of the pair's gradient (torch.polar's backward for a possibly
+// negative magnitude, which the reference's torch path differentiates).
+//
 // One thread per (row, 4 input dims); a workgroup covers 256 / (D / 4) rows of one (batch, head)
 // (grid y), so the dbias partial sums reduce in LDS.
 #include <type_traits>
@@ -86,7 +92,7 @@ __global__ __launch_bounds__(kThreads) void polar_fwd_kernel(PolarParams p, Side
   const int bh = blockIdx.y, n = blockIdx.x * rpb + r;
   if (r >= rpb || n >= sd.N) return;
   const int b = bh / sd.H, h = bh % sd.H;
-  const int d0 = 4 * u, E = p.D + p.R;
+  const int d0 = 4 * u, E = p.cplx ? 2 * p.D : p.D + p.R;
   float x[4];
   load4<T>(sd.x, (int64_t)b * sd.xs0 + (int64_t)h * sd.xs1 + (int64_t)n * sd.xs2 + d0, x);
   float* orow = sd.out + ((int64_t)bh * sd.N + n) * E;
@@ -105,6 +111,9 @@ __global__ __launch_bounds__(kThreads) void polar_fwd_kernel(PolarParams p, Side
     }
     *reinterpret_cast<float4*>(orow + 2 * d0) = make_float4(o[0], o[1], o[2], o[3]);
     *reinterpret_cast<float4*>(orow + 2 * d0 + 4) = make_float4(o[4], o[5], o[6], o[7]);
+  } else if (p.cplx) {
+    *reinterpret_cast<float4*>(orow + 2 * d0) = make_float4(x[0], 0.f, x[1], 0.f);
+    *reinterpret_cast<float4*>(orow + 2 * d0 + 4) = make_float4(x[2], 0.f, x[3], 0.f);
   } else {
     *reinterpret_cast<float4*>(orow + p.R + d0) = make_float4(x[0], x[1], x[2], x[3]);
   }
@@ -118,7 +127,7 @@ __global__ __launch_bounds__(kThreads) void polar_bwd_kernel(PolarParams p, Side
   const int bh = blockIdx.y, n = blockIdx.x * rpb + r;
   const bool live = r < rpb && n < sd.N;
   const int b = bh / sd.H, h = bh % sd.H;
-  const int d0 = 4 * u, E = p.D + p.R;
+  const int d0 = 4 * u, E = p.cplx ? 2 * p.D : p.D + p.R;
   float dph[4] = {0.f, 0.f, 0.f, 0.f};
   if (live) {
     float x[4];
@@ -146,6 +155,14 @@ __global__ __launch_bounds__(kThreads) void polar_bwd_kernel(PolarParams p, Side
 #pragma unroll
         for (int t = 0; t < 4; ++t) atomicAdd(df + t, dph[t]);
       }
+    } else if (p.cplx) {
+      // real parts of the (re, im) gradient pairs, times sign(x): the reference builds the pair
+      // with torch.polar(x, 0) (pope.py:50-51), whose backward takes Re(g * conj(sgn(result)))
+      const float4 g0 = *reinterpret_cast<const float4*>(grow + 2 * d0);
+      const float4 g1 = *reinterpret_cast<const float4*>(grow + 2 * d0 + 4);
+      const float gr[4] = {g0.x, g0.z, g1.x, g1.z};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dx[t] = x[t] > 0.f ? gr[t] : x[t] < 0.f ? -gr[t] : 0.f;
     } else {
       const float4 g = *reinterpret_cast<const float4*>(grow + p.R + d0);
       dx[0] = g.x; dx[1] = g.y; dx[2] = g.z; dx[3] = g.w;

@@ -641,6 +641,7 @@ int check_polar(const pope_desc* d, const void* q, const void* k, const float* f
     if (d->q_s[i] < 0 || d->q_s[i] % 4 || d->k_s[i] < 0 || d->k_s[i] % 4)
       return fail(POPE_ERR_INVALID, "q / k strides must be non-negative multiples of 4");
   if (d->R > 0 && d->bias_sh != 0 && d->bias_sh < d->R) return fail(POPE_ERR_INVALID, "bias row stride below R");
+  if (d->flags & ~POPE_FLAG_COMPLEX) return fail(POPE_ERR_INVALID, "unknown flags 0x%x", (unsigned)d->flags);
   return check_pope_ptrs(d, freqs, bias);
 }
 
@@ -651,6 +652,7 @@ void polar_params(const pope_desc* d, const void* q, const void* k, const float*
   p->freqs = d->R > 0 ? freqs : nullptr;
   p->bias = d->R > 0 ? bias : nullptr;
   p->B = d->B; p->Hq = d->Hq; p->Hk = d->Hk; p->Nq = d->Nq; p->Nk = d->Nk; p->D = d->D; p->R = d->R;
+  p->cplx = (d->flags & POPE_FLAG_COMPLEX) != 0;
   copy3(p->q_s, d->q_s); copy3(p->k_s, d->k_s); copy3(p->f_s, d->f_s);
   p->bias_sh = d->bias_sh;
 }

@@ -141,6 +141,7 @@ struct PolarParams {
   const float* gq; const float* gk;     // backward: gradients of q_hat / k_hat
   void* dq; void* dk; float* dfreqs; float* dbias;
   int B, Hq, Hk, Nq, Nk, D, R;
+  int cplx;                             // rows of D (re, im) pairs (complex64 layout) instead of D + R
   int64_t q_s[3], k_s[3], dq_s[3], dk_s[3], f_s[3], df_s[3];
   int64_t bias_sh;
 };

@@ -15,7 +15,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpope_hip.so")
 ABI_VERSION = 2
-FLAG_PREPARED, FLAG_ZERO_GRADS, FLAG_SPLIT_BF16 = 1, 2, 4
+FLAG_PREPARED, FLAG_ZERO_GRADS, FLAG_SPLIT_BF16, FLAG_COMPLEX = 1, 2, 4, 8
 
 POPE_F32, POPE_F16, POPE_BF16 = 0, 1, 2
 OP_SIM_FWD, OP_SIM_BWD, OP_FLASH_FWD, OP_FLASH_BWD, OP_FLASH_DECODE = range(5)

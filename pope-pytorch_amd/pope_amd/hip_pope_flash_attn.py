@@ -124,13 +124,41 @@ def _check_pope_shapes(q, k, freqs, bias):
 
 
 def _check_views(q, k, v, mask, lse=None):
-    """Shapes the kernels index by but the descriptor does not carry."""
+    """Shapes the kernels index by but the descriptor does not carry.  Cheap tuple compares:
+    run on every call, not only when a call plan is built."""
     if v.shape != k.shape:
         raise ValueError(f"v {tuple(v.shape)} must match k {tuple(k.shape)}")
     if exists(mask) and tuple(mask.shape) != (q.shape[0], k.shape[2]):
         raise ValueError(f"mask {tuple(mask.shape)} must be (batch, seq_k) = {(q.shape[0], k.shape[2])}")
     if exists(lse) and tuple(lse.shape) != tuple(q.shape[:3]):
         raise ValueError(f"lse {tuple(lse.shape)} must be {tuple(q.shape[:3])}")
+
+
+def _check_dtypes(q, *others):
+    """The descriptor carries one element type, q's: every other 16-bit operand must match it."""
+    for t in others:
+        if t.dtype != q.dtype:
+            raise TypeError(f"pope_amd flash: operand of dtype {t.dtype} next to q of dtype {q.dtype}")
+
+
+_INT32_MAX = 2 ** 31 - 1
+
+
+def _decode_eligible(q, k, v, freqs, causal) -> bool:
+    """Whether the forward runs the split-K decode kernel (pope_flash_decode): one non-causal query
+    row against a cache of at least 1024 keys, within the decode kernel's head-dim and 32-bit index
+    limits.  The forward op and its fake implementation both decide with this predicate, so the
+    workspace they return has the same size (empty for decode)."""
+    B, Hq, Nq, D = q.shape
+    Nk = k.shape[2]
+    R = freqs.shape[-1] if exists(freqs) else 0
+    if Nq != 1 or causal or Nk < 1024 or D > 128:
+        return False
+    if exists(freqs) and freqs.ndim == 4 and freqs.shape[1] > 1:
+        return False   # per-head phase tables: the general forward covers them
+    if B * Nk * R >= _INT32_MAX:
+        return False
+    return (Nk - 1) * max(k.stride(2), v.stride(2)) + D < _INT32_MAX
 
 
 # ------------------------------------------------------------------ call plans
@@ -170,19 +198,20 @@ def _fwd_impl(q, k, v, freqs, bias, mask, causal, softmax_scale):
     q, k, v = _unit_feature(q), _unit_feature(k), _unit_feature(v)
     o = torch.empty_like(q)
     lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
+    _check_views(q, k, v, mask)
     key = ("fwd", q.shape, q.stride(), k.shape, k.stride(), v.shape, v.stride(), o.stride(), q.dtype,
-           causal, softmax_scale, _opt_key(freqs), _opt_key(bias), _opt_key(mask))
+           k.dtype, v.dtype, causal, softmax_scale, _opt_key(freqs), _opt_key(bias), _opt_key(mask))
 
     def build():
+        _check_dtypes(q, k, v)
         _check_pope_shapes(q, k, freqs, bias)
-        _check_views(q, k, v, mask)
         d = _desc(q, k, freqs, bias, causal, softmax_scale)
         d.q_s[:], d.k_s[:], d.v_s[:] = _lib.strides3(q), _lib.strides3(k), _lib.strides3(v)
         d.o_s[:] = _lib.strides3(o)
         if exists(mask):
             d.mask_sb = mask.stride(0)
         # one non-causal query row against a long cache: the split-K decode kernel
-        decode = q.shape[2] == 1 and not causal and k.shape[2] >= 1024
+        decode = _decode_eligible(q, k, v, freqs, causal)
         dec_bytes = _lib.workspace_bytes(_lib.OP_FLASH_DECODE, d) if decode else -1
         return d, dec_bytes, _lib.workspace_bytes(_lib.OP_FLASH_FWD, d)
 
@@ -193,11 +222,8 @@ def _fwd_impl(q, k, v, freqs, bias, mask, causal, softmax_scale):
     stream = _stream(q)
     if dec_bytes >= 0:
         dws = torch.empty(dec_bytes, dtype=torch.uint8, device=q.device) if dec_bytes else None
-        st = L.pope_flash_decode(ctypes.byref(d), *args, _data(dws), dec_bytes, stream)
-        if st == 0:
-            return o, lse, q.new_empty(0, dtype=torch.uint8)
-        if st != 2:   # 2: the decode kernel does not cover this shape -> general forward
-            _lib.check(st, "flash decode")
+        _lib.check(L.pope_flash_decode(ctypes.byref(d), *args, _data(dws), dec_bytes, stream), "flash decode")
+        return o, lse, q.new_empty(0, dtype=torch.uint8)
     # torch's caching allocator returns 512-byte aligned blocks
     ws = torch.empty(fwd_bytes, dtype=torch.uint8, device=q.device)
     _lib.check(L.pope_flash_fwd(ctypes.byref(d), *args, ws.data_ptr(), fwd_bytes, stream), "flash forward")
@@ -211,19 +237,24 @@ def _bwd_impl(do, q, k, v, o, lse, freqs, bias, mask, causal, softmax_scale, nee
         do = do.to(q.dtype)
     if not lse.is_contiguous():
         lse = lse.contiguous()
+    _check_views(q, k, v, mask, lse)
+    if o.shape != q.shape or do.shape != q.shape:
+        raise ValueError(f"o {tuple(o.shape)} and do {tuple(do.shape)} must match q {tuple(q.shape)}")
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    # the library clears dfreqs / dbias itself (POPE_FLAG_ZERO_GRADS) before accumulating
-    dfreqs = torch.empty(freqs.shape, device=q.device, dtype=torch.float32) if need_dfreqs else q.new_empty(0, dtype=torch.float32)
+    # the library clears dfreqs / dbias itself (POPE_FLAG_ZERO_GRADS) before accumulating, over the
+    # key positions n < Nk it addresses; rows of a longer freqs table get no gradient, so such a
+    # table's gradient starts from zeros
+    long_freqs = need_dfreqs and freqs.shape[-2] > k.shape[2]
+    alloc_df = torch.zeros if long_freqs else torch.empty
+    dfreqs = alloc_df(freqs.shape, device=q.device, dtype=torch.float32) if need_dfreqs else q.new_empty(0, dtype=torch.float32)
     dbias = torch.empty(bias.shape, device=q.device, dtype=torch.float32) if need_dbias else q.new_empty(0, dtype=torch.float32)
     key = ("bwd", q.shape, q.stride(), k.shape, k.stride(), v.shape, v.stride(), o.stride(), do.stride(),
-           dq.stride(), dk.stride(), dv.stride(), q.dtype, causal, softmax_scale, _opt_key(freqs),
-           _opt_key(bias), _opt_key(mask), need_dfreqs, need_dbias)
+           dq.stride(), dk.stride(), dv.stride(), q.dtype, k.dtype, v.dtype, o.dtype, causal, softmax_scale,
+           _opt_key(freqs), _opt_key(bias), _opt_key(mask), need_dfreqs, need_dbias)
 
     def build():
+        _check_dtypes(q, k, v, o)
         _check_pope_shapes(q, k, freqs, bias)
-        _check_views(q, k, v, mask, lse)
-        if o.shape != q.shape or do.shape != q.shape:
-            raise ValueError(f"o {tuple(o.shape)} and do {tuple(do.shape)} must match q {tuple(q.shape)}")
         d = _desc(q, k, freqs, bias, causal, softmax_scale)
         d.q_s[:], d.k_s[:], d.v_s[:], d.o_s[:] = (_lib.strides3(t) for t in (q, k, v, o))
         d.do_s[:] = _lib.strides3(do)
@@ -265,8 +296,10 @@ def flash_fwd_op(q: Tensor, k: Tensor, v: Tensor, freqs: Optional[Tensor], bias:
 
 @flash_fwd_op.register_fake
 def _(q, k, v, freqs, bias, mask, causal, softmax_scale):
-    d = _desc(q, k, freqs, bias, causal, softmax_scale)
-    n = _lib.workspace_bytes(_lib.OP_FLASH_FWD, d)
+    if _decode_eligible(q, k, v, freqs, causal):
+        n = 0   # the decode kernel keeps nothing for the backward
+    else:
+        n = _lib.workspace_bytes(_lib.OP_FLASH_FWD, _desc(q, k, freqs, bias, causal, softmax_scale))
     return torch.empty_like(q), q.new_empty(q.shape[:3], dtype=torch.float32), q.new_empty(n, dtype=torch.uint8)
 
 
@@ -373,7 +406,11 @@ def flash_attn_forward(q, k, v, freqs=None, pope_bias=None, mask=None, causal=Fa
 
 def flash_attn_backward(do, q, k, v, o, lse, dq, dk, dv, dfreqs=None, dpope_bias=None, freqs=None,
                         pope_bias=None, mask=None, causal=False, softmax_scale=None):
-    """Writes grads into caller tensors, (B, N, H, D) layout; triton_pope_flash_attn.py:273-335."""
+    """Gradients into caller tensors, (B, N, H, D) layout; triton_pope_flash_attn.py:273-335.
+
+    The same write semantics as the reference launcher: dq, dfreqs and dpope_bias are added to
+    (its kernel accumulates them with atomics, :207-210,215, into buffers the caller zeroes,
+    :358-359), dk and dv are overwritten (:217-218)."""
     scale = q.shape[-1] ** -0.5 if softmax_scale is None else softmax_scale
     freqs, pope_bias = _prep_pope(freqs, pope_bias)
     mask = _prep_mask(mask, q.shape[0])
@@ -381,7 +418,7 @@ def flash_attn_backward(do, q, k, v, o, lse, dq, dk, dv, dfreqs=None, dpope_bias
     f = freqs.transpose(1, 2) if exists(freqs) and freqs.ndim == 4 else freqs
     gq, gk, gv, gf, gb = flash_bwd_op(tr(do), tr(q), tr(k), tr(v), tr(o), lse, f, pope_bias, mask, causal,
                                       float(scale), exists(dfreqs), exists(dpope_bias))
-    dq.copy_(tr(gq))
+    dq.add_(tr(gq))
     dk.copy_(tr(gk))
     dv.copy_(tr(gv))
     if exists(dfreqs):

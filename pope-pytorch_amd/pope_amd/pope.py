@@ -58,7 +58,7 @@ def apply_pope_to_qk(pope: PolarEmbedReturn, q: Tensor, k: Tensor, to_magnitude=
     if q.is_cuda:
         from . import hip_polar
         if hip_polar.fits(q, k, freqs, bias, to_magnitude, return_complex):
-            return hip_polar.polar(q, k, freqs, bias)
+            return hip_polar.polar(q, k, freqs, bias, return_complex)
 
     partial = rot < qk_dim
     if partial:

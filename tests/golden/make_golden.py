@@ -82,10 +82,16 @@ def fd_grad(f, x, eps=1e-5):
     return g
 
 
-def make_case(rng, B, Hq, Hk, Nq, Nk, D, R, causal, masked, offset):
+def make_case(rng, B, Hq, Hk, Nq, Nk, D, R, causal, masked, offset, big=False):
     q = rng.standard_normal((B, Hq, Nq, D))
     k = rng.standard_normal((B, Hk, Nk, D))
     v = rng.standard_normal((B, Hk, Nk, D))
+    if big:
+        # magnitudes past softplus's threshold (x > 20 -> x) and deep in its negative tail
+        q[..., 0] = 25.0
+        q[..., 1] = -23.0
+        k[..., 2] = 21.5
+        k[..., 3] = -30.0
     inv = 10000.0 ** -(np.arange(R) / max(R, 1))
     F = (np.arange(Nk)[:, None] + offset) * inv[None, :]
     bias = rng.uniform(-2 * math.pi, 0.0, (Hk, R))
@@ -116,6 +122,10 @@ def main():
         dict(B=1, Hq=2, Hk=2, Nq=4, Nk=4, D=8, R=8, causal=False, masked=False, offset=0),
         dict(B=2, Hq=2, Hk=1, Nq=3, Nk=5, D=8, R=4, causal=True, masked=True, offset=3),
         dict(B=1, Hq=2, Hk=2, Nq=1, Nk=6, D=8, R=8, causal=False, masked=True, offset=0),
+        # grouped heads with Hk > 1: query head h reads kv head h % Hk (not h // (Hq / Hk))
+        dict(B=1, Hq=4, Hk=2, Nq=3, Nk=5, D=8, R=8, causal=False, masked=False, offset=2),
+        # inputs beyond softplus's threshold, partial rotation
+        dict(B=1, Hq=1, Hk=1, Nq=4, Nk=4, D=8, R=6, causal=True, masked=False, offset=0, big=True),
     ]
     arrays = {}
     for c, kw in enumerate(cases):

@@ -228,3 +228,70 @@ def test_registered_op_checks(cuda):
     q, k, v, f, b = (inp[n].detach().clone().requires_grad_(True) for n in ("q", "k", "v", "freqs", "bias"))
     torch.library.opcheck(flash_fwd_op, (q, k, v, f, b, inp["mask"], True, 0.125),
                           test_utils=("test_schema", "test_autograd_registration", "test_faketensor"))
+
+
+# ---- the reference's operator-level names (triton_pope_flash_attn.py:222-373) -------------------
+
+def test_reference_named_operators(cuda):
+    """flash_attn, FlashAttnFunction.apply and flash_attn_forward / flash_attn_backward in the
+    reference's (B, N, H, D) layout, against the oracle -- the binding a maintainer plugs in at
+    attention.py:21-26.  flash_attn_backward keeps the reference launcher's write semantics: dq,
+    dfreqs and dpope_bias accumulate into caller-zeroed buffers, dk and dv are overwritten."""
+    from pope_amd.hip_pope_flash_attn import (FlashAttnFunction, flash_attn, flash_attn_backward,
+                                              flash_attn_forward)
+    inp = make_pope_inputs(21, 2, 4, 4, 192, 192, 64, 32, torch.bfloat16, "prefix")
+    ref = oracle_attention(inp, True)
+    tr = lambda t: t.transpose(1, 2)
+    for fn in (flash_attn, FlashAttnFunction.apply):
+        q, k, v = (tr(inp[n]).detach().clone().requires_grad_(True) for n in ("q", "k", "v"))
+        f, b = (inp[n].detach().clone().requires_grad_(True) for n in ("freqs", "bias"))
+        o = fn(q, k, v, f, b, inp["mask"], True)
+        assert o.shape == q.shape
+        o.backward(tr(inp["do"]))
+        got = dict(o=tr(o), dq=tr(q.grad), dk=tr(k.grad), dv=tr(v.grad), dfreqs=f.grad, dbias=b.grad)
+        _check(got, ref, ["o", "dq", "dk", "dv", "dfreqs", "dbias"])
+
+    q, k, v, do = (tr(inp[n]).contiguous() for n in ("q", "k", "v", "do"))
+    o, lse = flash_attn_forward(q, k, v, inp["freqs"], inp["bias"], inp["mask"], causal=True)
+    assert lse.shape == (2, 4, 192) and lse.dtype == torch.float32
+    dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+    df, db = torch.zeros_like(inp["freqs"]), torch.zeros_like(inp["bias"])
+    for _ in range(2):   # a second call adds to dq / dfreqs / dbias and rewrites dk / dv
+        flash_attn_backward(do, q, k, v, o, lse, dq, dk, dv, df, db, inp["freqs"], inp["bias"], inp["mask"],
+                            causal=True)
+    got = dict(o=tr(o), dq=tr(dq) / 2, dk=tr(dk), dv=tr(dv), dfreqs=df / 2, dbias=db / 2)
+    _check(got, ref, ["o", "dq", "dk", "dv", "dfreqs", "dbias"])
+    with pytest.raises(ValueError):   # a mis-shaped lse is rejected on every call, cached plan or not
+        flash_attn_backward(do, q, k, v, o, lse[:, :, :-1], dq, dk, dv, None, None, inp["freqs"], inp["bias"],
+                            inp["mask"], causal=True)
+
+
+def test_freqs_longer_than_keys_get_zero_rows(cuda):
+    """freqs may hold more positions than there are keys (the kernels use rows n < Nk); the rows past
+    Nk get a zero gradient, as the reference's zeros_like(f) buffer gives them (:359)."""
+    inp = make_pope_inputs(23, 1, 2, 2, 96, 96, 64, 32, torch.bfloat16, "none")
+    long_f = torch.cat([inp["freqs"], inp["freqs"][:40] + 1000.0])   # 136 rows for 96 keys
+    inp_long = dict(inp, freqs=long_f)
+    res = _run(inp_long, causal=False)
+    assert res["dfreqs"].shape == (136, 32)
+    assert torch.equal(res["dfreqs"][96:].cpu(), torch.zeros(40, 32))
+    ref = oracle_attention(inp, causal=False)
+    _check(dict(res, dfreqs=res["dfreqs"][:96]), ref, ["o", "dq", "dk", "dv", "dfreqs", "dbias"])
+
+
+def test_operand_dtypes_must_match(cuda):
+    from pope_amd.hip_pope_flash_attn import flash_fwd_op
+    inp = make_pope_inputs(3, 1, 2, 2, 64, 64, 64, 32, torch.bfloat16, "none")
+    with pytest.raises(TypeError):
+        flash_fwd_op(inp["q"], inp["k"].half(), inp["v"], inp["freqs"], inp["bias"], None, False, 0.125)
+
+
+def test_registered_op_checks_on_the_decode_path(cuda):
+    """opcheck's fake-tensor test on a call the decode kernel serves (Nq = 1, Nk >= 1024): the fake
+    implementation returns the same (empty) workspace as the real one."""
+    from pope_amd.hip_pope_flash_attn import flash_fwd_op
+    inp = make_pope_inputs(4, 2, 2, 2, 1, 1024, 64, 64, torch.bfloat16, "prefix")
+    args = (inp["q"], inp["k"], inp["v"], inp["freqs"], inp["bias"], inp["mask"], False, 0.125)
+    o, lse, ws = flash_fwd_op(*args)
+    assert ws.numel() == 0
+    torch.library.opcheck(flash_fwd_op, args, test_utils=("test_schema", "test_faketensor"))

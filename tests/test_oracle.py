@@ -211,3 +211,58 @@ def test_planted_mistakes_are_caught(kind):
     # ... and each plausible mistake does not
     bad = _mutant_sim(kind)(q, k, F, bias)
     assert np.abs(bad.numpy() - g["S"]).max() > 1e-3
+
+
+# ---- functions the golden fixtures alone leave open ----
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_softplus_matches_torch(dtype):
+    """softplus with beta 1 and threshold 20 (x > 20 -> x): torch's F.softplus, the reference's
+    magnitude function (pope.py:34,60), over both branches and the deep negative tail."""
+    import torch.nn.functional as Fn
+    x = torch.cat([torch.linspace(-100, 100, 20001, dtype=dtype),
+                   torch.tensor([20.0, 20.0 + 1e-3, 19.999, -1e-30, 0.0], dtype=dtype)])
+    tol = dict(rtol=1e-6, atol=1e-30) if dtype == torch.float32 else dict(rtol=1e-13, atol=1e-300)
+    torch.testing.assert_close(orc.softplus(x), Fn.softplus(x), **tol)
+    assert torch.equal(orc.softplus(x[x > 20]), x[x > 20])
+
+
+@pytest.mark.parametrize("groups", [1, 2, 4])
+def test_repeat_heads_matches_einops(groups):
+    """The grouped-head repeat is einops' 'b h ... -> b (g h) ...' (attention.py:44-45,118-120)."""
+    from einops import repeat
+    t = torch.randn(2, 3, 5, 4)
+    torch.testing.assert_close(orc._repeat_heads(t, groups), repeat(t, "b h ... -> b (g h) ...", g=groups),
+                               rtol=0, atol=0)
+
+
+def test_clamp_bias_closed_form_and_gradient():
+    x = torch.tensor([-10.0, -2 * math.pi, -3.0, -1e-7, 0.0, 1e-7, 4.0], dtype=torch.float64,
+                     requires_grad=True)
+    y = orc.clamp_bias(x)
+    want = torch.tensor([-2 * math.pi, -2 * math.pi, -3.0, -1e-7, 0.0, 0.0, 0.0], dtype=torch.float64)
+    assert torch.equal(y.detach(), want)
+    y.sum().backward()
+    assert x.grad.tolist() == [0.0, 1.0, 1.0, 1.0, 1.0, 0.0, 0.0]
+
+
+def test_planted_gqa_mapping_mistake_is_caught(monkeypatch):
+    """Query head h must read kv head h % Hk; the blocked mapping h // (Hq / Hk) is a plausible
+    mistake that the Hq = 4, Hk = 2 golden case must reject."""
+    g = CASES[3]
+    assert tuple(int(x) for x in g["meta"][1:3]) == (4, 2)
+    q, k, F, bias = (_t(g[n]) for n in ("q", "k", "F", "bias"))
+    np.testing.assert_allclose(orc.sim_nonfused(q, k, F, bias).numpy(), g["S"], rtol=1e-12, atol=1e-12)
+    monkeypatch.setattr(orc, "_repeat_heads",
+                        lambda t, groups: t.repeat_interleave(groups, dim=1) if groups > 1 else t)
+    assert np.abs(orc.sim_nonfused(q, k, F, bias).numpy() - g["S"]).max() > 1e-3
+
+
+def test_planted_softplus_threshold_mistake_is_caught(monkeypatch):
+    """Clamping the input at the threshold instead of passing x > 20 through must fail the golden
+    case whose inputs reach 25."""
+    g = CASES[4]
+    q, k, F, bias = (_t(g[n]) for n in ("q", "k", "F", "bias"))
+    np.testing.assert_allclose(orc.sim_nonfused(q, k, F, bias).numpy(), g["S"], rtol=1e-12, atol=1e-12)
+    monkeypatch.setattr(orc, "softplus", lambda x: torch.log1p(torch.exp(torch.clamp(x, max=20.0))))
+    assert np.abs(orc.sim_nonfused(q, k, F, bias).numpy() - g["S"]).max() > 1e-3

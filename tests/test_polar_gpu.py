@@ -82,14 +82,53 @@ def test_polar_forward_backward(cuda, cfg):
         assert e <= tol, f"{name}: {e:.3e} > {tol:.3e}"
 
 
+@pytest.mark.parametrize("cfg", [(1, 2, 2, 16, 16, 32, 16, False), (2, 4, 2, 40, 72, 64, 64, True)],
+                         ids=["partial", "full-f3"])
+def test_polar_complex_output(cuda, cfg):
+    """return_complex=True on the kernels: complex64 rows of (a cos, a sin) pairs with pass-through
+    dims as (x, 0) (pope.py:49-51,66-67,74-75), forward and backward vs the oracle's torch.polar."""
+    import pope_amd
+    from pope_amd import _lib
+    B, Hq, Hk, Nq, Nk, D, R, f3 = cfg
+    q, k, freqs, bias = _case(3, B, Hq, Hk, Nq, Nk, D, R, torch.float32, f3, Hk)
+    t_ref = [x.clone().requires_grad_(True) for x in (q, k, freqs, bias)]
+    qr, kr = orc.apply_pope_to_qk(t_ref[2], t_ref[3], t_ref[0], t_ref[1], return_complex=True)
+    g = torch.Generator().manual_seed(5)
+    gq = torch.randn(*qr.shape, 2, generator=g)
+    gk = torch.randn(*kr.shape, 2, generator=g)
+    ((torch.view_as_real(qr) * gq).sum() + (torch.view_as_real(kr) * gk).sum()).backward()
+
+    t = [x.clone().cuda().requires_grad_(True) for x in (q, k, freqs, bias)]
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    qc, kc = pope_amd.apply_pope_to_qk(pope_amd.PolarEmbedReturn(t[2], t[3]), t[0], t[1], return_complex=True)
+    ((torch.view_as_real(qc) * gq.cuda()).sum() + (torch.view_as_real(kc) * gk.cuda()).sum()).backward()
+    torch.cuda.synchronize()
+    _lib.profile_enable(False)
+    ran = _lib.profile_read()
+    assert "polar_fwd" in ran and "polar_bwd" in ran, ran
+    assert qc.dtype == torch.complex64 and qc.shape == qr.shape and kc.shape == kr.shape
+    for name, a, r, rel in (("q_hat", torch.view_as_real(qc), torch.view_as_real(qr), 1e-5),
+                            ("k_hat", torch.view_as_real(kc), torch.view_as_real(kr), 1e-5),
+                            ("dq", t[0].grad, t_ref[0].grad, 1e-5), ("dk", t[1].grad, t_ref[1].grad, 1e-5),
+                            ("dfreqs", t[2].grad, t_ref[2].grad, 1e-4), ("dbias", t[3].grad, t_ref[3].grad, 1e-4)):
+        e, m = _err(a, r)
+        print(f"{name}: err {e:.3e} (max {m:.3e})")
+        assert e <= rel * m, f"{name}: {e:.3e} > {rel * m:.3e}"
+    if R < D:   # pass-through dims: (x, 0)
+        assert torch.equal(qc[..., R:].real.cpu(), q[..., R:]) and torch.all(qc[..., R:].imag == 0)
+
+
 def test_polar_other_calls_keep_torch_ops(cuda):
-    """Complex outputs and custom magnitudes are outside the kernels: the torch ops answer."""
+    """Custom magnitudes and half-precision complex outputs are outside the kernels: the torch ops
+    answer (a bf16 magnitude with fp32 phases is the reference's torch.polar error, pope.py:67)."""
     import pope_amd
     import torch.nn.functional as F
     q, k, freqs, bias = _case(3, 1, 2, 2, 16, 16, 32, 16, torch.float32, False, 2)
     pos = pope_amd.PolarEmbedReturn(freqs.cuda(), bias.cuda())
-    qc, kc = pope_amd.apply_pope_to_qk(pos, q.cuda(), k.cuda(), return_complex=True)
-    qr, kr = orc.apply_pope_to_qk(freqs, bias, q, k, return_complex=True)
-    assert torch.allclose(qc.cpu(), qr, atol=1e-5) and torch.allclose(kc.cpu(), kr, atol=1e-5)
     qe, _ = pope_amd.apply_pope_to_qk(pos, q.cuda(), k.cuda(), to_magnitude=F.relu)
     assert qe.shape == (1, 2, 16, 48)
+    a = torch.relu(q[..., :16]).cuda()
+    torch.testing.assert_close(qe[..., 0:32:2], a * freqs[-16:].cuda().cos())
+    with pytest.raises(RuntimeError):
+        pope_amd.apply_pope_to_qk(pos, q.cuda().bfloat16(), k.cuda().bfloat16(), return_complex=True)

@@ -3,7 +3,8 @@ split-bf16 kernels (allow_tf32=True, the default) vs the CPU oracle.
 
 Tolerance (from the build's north star): 1e-4 relative for fp32 similarity,
 read as ||kernel - oracle||_inf <= 1e-4 * ||oracle||_inf for S and for each
-gradient (dq, dk, dbias, dfreqs).  The oracle runs in fp32 on the same inputs
+gradient (dq, dk, dbias, dfreqs), and element by element as
+allclose(rtol=1e-4, atol=1e-4 * rms(oracle)).  The oracle runs in fp32 on the same inputs
 (reproducing the reference's fl(freqs + bias) phase rounding, pope.py:56).
 Cases follow the reference's test_triton.py: multi-config incl. R = 0
 (:15-54), non-contiguous slices (:56-85), dfreqs with random freqs/bias
@@ -24,6 +25,14 @@ RTOL = 1e-4
 def _rel_inf(a, b):
     a, b = a.detach().double().cpu(), b.detach().double().cpu()
     return ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item()
+
+
+def _elementwise(a, b):
+    """Largest |a - b| / (RTOL |b| + RTOL rms(b)): at most 1 means allclose(rtol=1e-4,
+    atol=1e-4 rms(ref)) holds element by element."""
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    rms = b.pow(2).mean().sqrt().clamp_min(1e-30)
+    return ((a - b).abs() / (RTOL * b.abs() + RTOL * rms)).max().item()
 
 
 def _case(seed, B, Hq, Hk, Nq, Nk, D, R, rand_freqs=False):
@@ -58,12 +67,15 @@ def _kernel(q, k, freqs, bias, G, slicer=None, allow_tf32=True):
 
 def _compare(S, grads, S_ref, grads_ref, names=("dq", "dk", "dfreqs", "dbias")):
     e = {"S": _rel_inf(S, S_ref)}
+    el = {"S": _elementwise(S, S_ref)}
     for n, g, r in zip(names, grads, grads_ref):
         if r is not None and g is not None and r.numel():
             e[n] = _rel_inf(g, r)
-    print(" ".join(f"{n}={v:.2e}" for n, v in e.items()))
+            el[n] = _elementwise(g, r)
+    print(" ".join(f"{n}={v:.2e}/{el[n]:.2f}" for n, v in e.items()))
     for n, v in e.items():
         assert v <= RTOL, f"{n}: relative error {v:.3e} > {RTOL}"
+        assert el[n] <= 1.0, f"{n}: elementwise allclose(rtol=1e-4, atol=1e-4 rms) fails by {el[n]:.2f}x"
 
 
 @pytest.mark.parametrize("cfg", [
@@ -127,3 +139,16 @@ def test_readme_fused_similarity(cuda):
     assert sim.shape == (1, 8, 1024, 1024)
     ref = orc.sim_nonfused(q.cpu(), k.cpu(), pos_emb.freqs.cpu(), pos_emb.bias.detach().cpu())
     assert _rel_inf(sim, ref) <= RTOL
+
+
+def test_reference_named_similarity_function(cuda):
+    """PoPESimilarityFunction.apply(q, k, freqs, bias, rotate_dim, allow_tf32) and
+    hip_compute_qk_similarity, the reference's operator names (triton_pope.py:258-372)."""
+    from pope_amd.hip_pope import PoPESimilarityFunction, hip_compute_qk_similarity
+    q, k, freqs, bias, G = _case(31, 1, 4, 2, 96, 128, 64, 32)
+    S_ref, g_ref = _oracle(q, k, freqs, bias, G)
+    for fn in (PoPESimilarityFunction.apply, hip_compute_qk_similarity):
+        t = [x.detach().clone().cuda().requires_grad_(True) for x in (q, k, freqs, bias)]
+        S = fn(t[0], t[1], t[2], t[3], 32, False)
+        S.backward(G.cuda())
+        _compare(S, [x.grad for x in t], S_ref, g_ref)
