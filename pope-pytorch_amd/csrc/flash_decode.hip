@@ -7,14 +7,14 @@
 // forward path).
 //
 // The path is bound by HBM: every valid key costs 2 * D * 2 bytes of K and V
-// and a handful of flops.  Work decomposition:
-//   decode_setup : the fp16 cos / sin(F_j) table of the keys and each (batch,
-//                  head)'s query weights (below), once per call;
+// and a handful of flops.  Work decomposition (two launches):
 //   decode_split : one workgroup (4 waves) per (batch, split of S keys), covering
 //                  every query head of the batch; wave w takes heads w, w + 4, ...
 //                  A split whose keys are all masked exits after reading its mask
-//                  bytes.  The split's rows of the cos / sin(F_j) table (fp16 pairs)
-//                  are staged in LDS once and shared by all heads.  A wave load reads
+//                  bytes.  The workgroup computes the batch's query weights (below)
+//                  into LDS, and the cos / sin of its rows of F (fp16 pairs, from the
+//                  fp32 rows of the caller's freqs, which every batch's splits read
+//                  out of L2), staged in LDS once and shared by all heads.  A wave load reads
 //                  64 / LPK consecutive key rows of one head (LPK lanes x 16 bytes per
 //                  row), so every wave streams contiguous memory; all K and V rows of a
 //                  head are in flight before its scores are computed, and the next
@@ -66,50 +66,21 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
-// Setup: the fp16 (cos, sin) table of F[bt, n, d] for n < Nk, and each (batch, head)'s query
-// weights (scale * log2 e folded in), one 32-bit word per dim: rotated dims the fp16 pair
-// (a cos(F_q - b), a sin(F_q - b)) with a = softplus(q) and F_q = F[Nk - 1]; pass-through dims
-// the fp32 weight q.
+// Query weight word of (batch b, head h, dim d), scale * log2 e folded in: rotated dims the fp16
+// pair (a cos(F_q - b), a sin(F_q - b)) with a = softplus(q) and F_q = F[Nk - 1]; pass-through
+// dims the fp32 weight q.
 template <typename T>
-__global__ __launch_bounds__(256) void decode_setup_kernel(DecodeParams p, int tab_blocks, int64_t n_tab) {
-  if ((int)blockIdx.x < tab_blocks) {
-    // four consecutive entries per thread, in one row (R is a multiple of 8): four independent
-    // loads, one 16-byte store; 32-bit indices (the host keeps the table below 2^31 entries)
-    const int i4 = 4 * ((int)blockIdx.x * 256 + (int)threadIdx.x);
-    if (i4 < (int)n_tab) {
-      const int d = i4 % p.R, rest = i4 / p.R;
-      const int n = rest % p.Nk, bt = rest / p.Nk;
-      const float* f = p.freqs + (int64_t)bt * p.f_s[0] + (int64_t)n * p.f_s[2] + d;
-      float x[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) x[t] = f[t];
-      u32x4 w;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        float sn, cs;
-        sincos_rev(x[t], &sn, &cs);
-        w[t] = __builtin_bit_cast(uint32_t, f16x2{(_Float16)cs, (_Float16)sn});
-      }
-      *reinterpret_cast<u32x4*>(p.table + i4) = w;
-    }
-    return;
-  }
-  const int idx = ((int)blockIdx.x - tab_blocks) * 256 + threadIdx.x;
-  if (idx >= p.B * p.Hq * p.D) return;
-  const int d = idx % p.D, bh = idx / p.D;
-  const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
+__device__ __forceinline__ uint32_t query_weight(const DecodeParams& p, int b, int h, int d) {
   const float qv = T::to_float(p.q[(int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + d]);
-  uint32_t w;
   if (d < p.R) {
     float sn, cs;
-    sincos_acc(p.freqs[(int64_t)b * p.f_s[0] + (int64_t)(p.Nk - 1) * p.f_s[2] + d] - p.bias[(int64_t)hk * p.bias_sh + d],
+    sincos_acc(p.freqs[(int64_t)b * p.f_s[0] + (int64_t)(p.Nk - 1) * p.f_s[2] + d] -
+                   p.bias[(int64_t)(h % p.Hk) * p.bias_sh + d],
                &sn, &cs);
     const float a = softplus_f(qv) * p.scale_log2;
-    w = __builtin_bit_cast(uint32_t, f16x2{(_Float16)(a * cs), (_Float16)(a * sn)});
-  } else {
-    w = __builtin_bit_cast(uint32_t, qv * p.scale_log2);
+    return __builtin_bit_cast(uint32_t, f16x2{(_Float16)(a * cs), (_Float16)(a * sn)});
   }
-  p.qw[idx] = w;
+  return __builtin_bit_cast(uint32_t, qv * p.scale_log2);
 }
 
 // Split kernel.  A workgroup (4 waves) owns one (batch, split of S keys) for every query head;
@@ -121,6 +92,9 @@ __global__ __launch_bounds__(256) void decode_setup_kernel(DecodeParams p, int t
 // the row's LPK lanes (DPP), masked keys -inf; the head's max, sum and p-weighted V rows are
 // reduced across the RPI rows by lane shuffles, and the row-0 lanes write the partial.
 constexpr int kLoads = 16;
+// Query weight words staged in LDS per workgroup: Hq * D of them (the host sends calls with more
+// to the general forward).
+constexpr int kQwMax = 4096;
 
 // bf16 keys: log2(1 + 2^(-|x| log2 e)) (the softplus term beyond max(x, 0), in log2 units) is
 // tabulated in LDS over the bf16 magnitudes 2^-24 <= |x| < 32, indexed by the 15 magnitude bits
@@ -151,6 +125,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
   constexpr int S = split_rows<LPK>();   // keys per split
   constexpr int TS = RMAX + 4;           // table row stride (words; 16-byte pad spreads banks)
   __shared__ __attribute__((aligned(16))) uint32_t tab_s[S * TS];
+  __shared__ __attribute__((aligned(16))) uint32_t qw_s[kQwMax];
   __shared__ uint8_t vis_s[S];
   __shared__ float sp_s[T::kCode == 2 ? kSpN : 1];
 
@@ -200,14 +175,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
   auto vptr = [&](int h) {
     return p.v + (int64_t)b * p.v_s[0] + (int64_t)(h % p.Hk) * p.v_s[1] + ((j_begin + r) * vs2 + dcl);
   };
-  // The query weight words of a head: two 16-byte loads at the clamped chunk, issued before
-  // the head's K rows (waits count loads in issue order, so waiting for the weights leaves the
-  // K and V rows in flight).
+  // The query weight words of a head: two 16-byte LDS reads at the clamped chunk.
   u32x4 qwc[2];
   auto qwload = [&](int h) {
-    const u32x4* src = reinterpret_cast<const u32x4*>(p.qw + ((int64_t)b * p.Hq + h) * D + dcl);
-    qwc[0] = src[0];
-    qwc[1] = src[1];
+    const uint32_t a = lds_addr(qw_s + h * D + dcl);
+    qwc[0] = lds_read16_at(a);
+    qwc[1] = lds_read16_at(a + 16);
   };
   u32x4 kb[kLoads], vb[kLoads];
   auto load = [&](u32x4* buf, const uint16_t* lp, int stride) {
@@ -215,25 +188,26 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
     for (int u = 0; u < kLoads; ++u) buf[u] = ld16(lp + min(u * RPI, rows_left) * stride);
   };
 
-  // ---- the split's table rows (rows past Nk repeat the last row), then the first head's
-  // weights, K and V rows, all issued before the table is stored to LDS: the K / V loads do not
-  // wait for the table's round trip.  Waves past Hq load a valid head and never use it.
-  constexpr int C4 = RMAX / 4;                        // 16-byte chunks per staged table row
-  constexpr int kTabIt = S * C4 / kThreads;           // table chunks per thread
+  // ---- the split's phase rows F[j] (rows past Nk repeat the last row), then the first head's
+  // K and V rows, all issued before the rows' (cos, sin) are computed and stored to LDS as fp16
+  // pairs: the K / V loads do not wait for that round trip.  Waves past Hq load a valid head and
+  // never use it.  The rows of the freqs table are read by every batch's splits (L2 hits after
+  // the first): no table is built beforehand.
+  constexpr int C4 = RMAX / 4;                        // 16-byte chunks per staged row
+  constexpr int kTabIt = S * C4 / kThreads;           // chunks per thread
   static_assert(S * C4 % kThreads == 0, "whole table chunks per thread");
-  u32x4 tb[kTabIt];
+  float4 tb[kTabIt];
   if (R) {
-    const uint32_t* tsrc = p.table + (int64_t)b * p.t_sb;
+    const float* fsrc = p.freqs + (int64_t)b * p.f_s[0];
 #pragma unroll
     for (int it = 0; it < kTabIt; ++it) {
       const int i = tid + it * kThreads;
       const int c4 = min(i % C4, R / 4 - 1), jj = min(j_begin + i / C4, Nk - 1);
-      tb[it] = *reinterpret_cast<const u32x4*>(tsrc + (int64_t)jj * R + 4 * c4);
+      tb[it] = *reinterpret_cast<const float4*>(fsrc + (int64_t)jj * p.f_s[2] + 4 * c4);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
   const int h0 = min(wave, p.Hq - 1);
-  qwload(h0);
   load(kb, kptr(h0), ks2);
   __builtin_amdgcn_sched_barrier(0);
   load(vb, vptr(h0), vs2);
@@ -242,9 +216,21 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
 #pragma unroll
     for (int it = 0; it < kTabIt; ++it) {
       const int i = tid + it * kThreads;
-      if (i % C4 < R / 4) *reinterpret_cast<u32x4*>(tab_s + (i / C4) * TS + 4 * (i % C4)) = tb[it];
+      if (i % C4 < R / 4) {
+        const float x[4] = {tb[it].x, tb[it].y, tb[it].z, tb[it].w};
+        u32x4 w;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          float sn, cs;
+          sincos_rev(x[t], &sn, &cs);
+          w[t] = __builtin_bit_cast(uint32_t, f16x2{(_Float16)cs, (_Float16)sn});
+        }
+        *reinterpret_cast<u32x4*>(tab_s + (i / C4) * TS + 4 * (i % C4)) = w;
+      }
     }
   }
+  // query weights of every head of the batch (after the rows: their registers are free again)
+  for (int i = tid; i < p.Hq * D; i += kThreads) qw_s[i] = query_weight<T>(p, b, i / D, i % D);
   if constexpr (T::kCode == 2) {
     for (int i = tid; i < kSpN; i += kThreads) {
       const float t = __builtin_bit_cast(float, (uint32_t)(i + kSpLo) << 16);
@@ -343,6 +329,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
     }
   };
   if (wave < p.Hq) {
+    qwload(wave);
     int h = wave;
     for (; h + kWaves < p.Hq; h += kWaves) head(h, std::true_type{});
     head(h, std::false_type{});
@@ -425,14 +412,8 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
 
 template <typename T, int LPK, int RMAX>
 hipError_t launch_t(const DecodeParams& p, hipStream_t s) {
-  const int64_t n_tab = p.R > 0 ? (int64_t)(p.t_sb != 0 ? p.B : 1) * p.Nk * p.R : 0;
-  const int tab_blocks = (int)((n_tab + 1023) / 1024);   // 4 entries per thread
-  const int qw_blocks = (p.B * p.Hq * p.D + 255) / 256;
-  hipError_t e = launch_named("flash_decode_setup", decode_setup_kernel<T>, dim3(tab_blocks + qw_blocks), dim3(256),
-                              s, p, tab_blocks, n_tab);
-  if (e != hipSuccess) return e;
-  e = launch_named("flash_decode_split", decode_split_kernel<T, LPK, RMAX>, dim3(p.B * p.splits),
-                   dim3(kThreads), s, p);
+  hipError_t e = launch_named("flash_decode_split", decode_split_kernel<T, LPK, RMAX>, dim3(p.B * p.splits),
+                              dim3(kThreads), s, p);
   if (e != hipSuccess) return e;
   return launch_named("flash_decode_combine", decode_combine_kernel<T>, dim3(p.B * p.Hq), dim3(256), s, p);
 }
@@ -453,9 +434,11 @@ int decode_split_keys(int D) {
   return chunks <= 4 ? split_rows<4>() : chunks <= 8 ? split_rows<8>() : split_rows<16>();
 }
 
+int decode_max_query_words() { return kQwMax; }
+
 hipError_t launch_flash_decode(const DecodeParams& p, int dtype, hipStream_t s) {
   // per-head phase tables would need a table chunk per head: the general forward covers them
-  if (p.Nq != 1 || p.causal || p.D > 128 || p.t_sh != 0) return hipErrorInvalidValue;
+  if (p.Nq != 1 || p.causal || p.D > 128 || p.t_sh != 0 || p.Hq * p.D > kQwMax) return hipErrorInvalidValue;
   return dtype == 2 ? dispatch<BF16>(p, s) : dispatch<F16>(p, s);
 }
 

@@ -245,16 +245,10 @@ int decode_splits(const pope_desc& d) {
   return (d.Nk + per - 1) / per;
 }
 
-size_t decode_table_bytes(const pope_desc& d) {
-  const Geo g = geometry(d, d.Hq);
-  return d.R > 0 ? align_up((size_t)g.Bt * g.Ht * d.Nk * d.R * sizeof(uint32_t)) : 0;
-}
-
 size_t decode_ws(const pope_desc& d) {
   const int splits = decode_splits(d);
   const size_t rows = (size_t)d.B * d.Hq * d.Nq;
-  return decode_table_bytes(d) + align_up(rows * splits * d.D * sizeof(float)) +
-         align_up(rows * splits * 2 * sizeof(float)) + align_up(rows * d.D * sizeof(uint32_t));
+  return align_up(rows * splits * d.D * sizeof(float)) + align_up(rows * splits * 2 * sizeof(float));
 }
 
 hipError_t build_table(const pope_desc& d, const float* freqs, const float* bias, int Bt, int Ht,
@@ -510,10 +504,14 @@ int pope_flash_decode(const pope_desc* d, const void* q, const void* k, const vo
   if (d->Nq != 1 || d->causal || d->D > 128)
     return fail(POPE_ERR_UNSUPPORTED, "decode kernel covers one non-causal query row with head dim <= 128 "
                                       "(got %d rows, causal %d, head dim %d)", d->Nq, d->causal, d->D);
-  // the setup kernel indexes the key-phase table with 32-bit indices
-  if ((int64_t)d->B * d->Nk * d->R >= INT32_MAX)
-    return fail(POPE_ERR_UNSUPPORTED, "decode kernel: key-phase table of %lld entries exceeds 32-bit indices",
-                (long long)d->B * d->Nk * d->R);
+  if (d->R > 0 && d->f_s[1] != 0)
+    return fail(POPE_ERR_UNSUPPORTED, "decode kernel: per-head freqs tables are not covered");
+  if ((int64_t)d->Hq * d->D > pope::decode_max_query_words())
+    return fail(POPE_ERR_UNSUPPORTED, "decode kernel: query heads x head dim = %lld exceeds %d",
+                (long long)d->Hq * d->D, pope::decode_max_query_words());
+  // the split kernel reads freqs rows as 16-byte vectors
+  if (d->R > 0 && ((reinterpret_cast<uintptr_t>(freqs) & 15u) || d->f_s[0] % 4 || d->f_s[2] % 4))
+    return fail(POPE_ERR_UNSUPPORTED, "decode kernel: freqs rows must be 16-byte aligned");
   // the split kernel addresses rows of one (batch, head) with 32-bit element offsets
   if ((int64_t)(d->Nk - 1) * std::max(d->k_s[2], d->v_s[2]) + d->D >= INT32_MAX)
     return fail(POPE_ERR_UNSUPPORTED, "decode kernel: K / V row offsets exceed 32 bits (rows %d, strides %lld, %lld)",
@@ -524,11 +522,8 @@ int pope_flash_decode(const pope_desc* d, const void* q, const void* k, const vo
   char* ws = static_cast<char*>(workspace);
   const int splits = decode_splits(*d);
   const size_t rows = (size_t)d->B * d->Hq * d->Nq;
-  uint32_t* table = reinterpret_cast<uint32_t*>(ws);
-  const size_t tb = decode_table_bytes(*d);
-  float* part_o = reinterpret_cast<float*>(ws + tb);
-  float* part_ml = reinterpret_cast<float*>(ws + tb + align_up(rows * splits * d->D * sizeof(float)));
-  uint32_t* qw = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(part_ml) + align_up(rows * splits * 2 * sizeof(float)));
+  float* part_o = reinterpret_cast<float*>(ws);
+  float* part_ml = reinterpret_cast<float*>(ws + align_up(rows * splits * d->D * sizeof(float)));
   pope::DecodeParams p;
   std::memset(&p, 0, sizeof p);
   p.q = static_cast<const uint16_t*>(q);
@@ -537,8 +532,6 @@ int pope_flash_decode(const pope_desc* d, const void* q, const void* k, const vo
   p.freqs = d->R > 0 ? freqs : nullptr;
   p.bias = d->R > 0 ? bias : nullptr;
   p.mask = mask;
-  p.table = d->R > 0 ? table : nullptr;
-  p.qw = qw;
   p.o = static_cast<uint16_t*>(o);
   p.lse = lse;
   p.part_o = part_o;

@@ -150,9 +150,7 @@ hipError_t launch_polar(const PolarParams& p, int dtype, bool bwd, hipStream_t s
 
 struct DecodeParams {
   const uint16_t* q; const uint16_t* k; const uint16_t* v;
-  const float* freqs; const float* bias; const uint8_t* mask;
-  uint32_t* table;           // fp16 (cos, sin) of F[bt, n, d] for n < Nk, packed per 32-bit word
-  uint32_t* qw;              // (B, Hq, D) query weight words, written by the decode setup kernel
+  const float* freqs; const float* bias; const uint8_t* mask;   // freqs rows 16-byte aligned
   uint16_t* o; float* lse;
   float* part_o; float* part_ml;   // split-K partials (B*Hq*Nq, splits, D) and (.., splits, 2)
   int B, Hq, Hk, Nq, Nk, D, R, causal, has_mask, splits, keys_per_split;
@@ -161,8 +159,10 @@ struct DecodeParams {
   int64_t bias_sh, mask_sb, t_sb, t_sh;
 };
 // Keys per split of the decode kernel at head dim D.  launch_flash_decode returns
-// hipErrorInvalidValue for shapes the kernel does not cover (Nq != 1, causal, D > 128).
+// hipErrorInvalidValue for shapes the kernel does not cover (Nq != 1, causal, D > 128, per-head
+// freqs, more than decode_max_query_words() query heads x head dim).
 int decode_split_keys(int D);
+int decode_max_query_words();
 hipError_t launch_flash_decode(const DecodeParams& p, int dtype, hipStream_t s);
 
 }  // namespace pope

@@ -41,8 +41,8 @@ class PopeDesc(ctypes.Structure):
 
 EXPORTS = (
     "pope_abi_version", "pope_last_error", "pope_workspace_bytes", "pope_sim_fwd", "pope_sim_bwd",
-    "pope_flash_fwd", "pope_flash_bwd", "pope_flash_decode", "pope_polar_fwd", "pope_polar_bwd",
-    "pope_profile_enable", "pope_profile_read", "pope_profile_reset",
+    "pope_flash_fwd", "pope_flash_bwd", "pope_flash_decode", "pope_polar_fwd",
+    "pope_polar_bwd", "pope_profile_enable", "pope_profile_read", "pope_profile_reset",
 )
 
 _lib = None

@@ -142,6 +142,7 @@ def _check_dtypes(q, *others):
 
 
 _INT32_MAX = 2 ** 31 - 1
+_DECODE_QUERY_WORDS = 4096   # decode_max_query_words() of the library
 
 
 def _decode_eligible(q, k, v, freqs, causal) -> bool:
@@ -156,8 +157,10 @@ def _decode_eligible(q, k, v, freqs, causal) -> bool:
         return False
     if exists(freqs) and freqs.ndim == 4 and freqs.shape[1] > 1:
         return False   # per-head phase tables: the general forward covers them
-    if B * Nk * R >= _INT32_MAX:
-        return False
+    if Hq * D > _DECODE_QUERY_WORDS:
+        return False   # the kernel stages Hq * D query weights in LDS
+    if R and (freqs.data_ptr() % 16 or any(s % 4 for s in freqs.stride()[:-1])):
+        return False   # freqs rows are read as 16-byte vectors
     return (Nk - 1) * max(k.stride(2), v.stride(2)) + D < _INT32_MAX
 
 

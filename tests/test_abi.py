@@ -187,3 +187,4 @@ def test_flash_wrappers_check_shapes_before_any_call():
         _bwd_impl(q, q, k, v, q, lse[:, :, 1:], f, b, None, True, 0.1, False, False)
     with pytest.raises(ValueError, match="must match q"):
         _bwd_impl(q[:, :, 1:], q, k, v, q, lse, f, b, None, True, 0.1, False, False)
+
