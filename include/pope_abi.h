@@ -163,6 +163,20 @@ int pope_flash_decode(const pope_desc* desc, const void* q, const void* k, const
                       float* lse, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * pope_flash_decode without a workspace argument and without any allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The split partials live in a
+ * 16 MiB device array of the library (one per GPU, held until the process ends); a call whose
+ * partials need more (pope_workspace_bytes(POPE_OP_FLASH_DECODE) above 16 MiB, i.e. more batch
+ * rows x query heads x splits) fails with POPE_ERR_WORKSPACE.  Calls that overlap on one GPU
+ * share that array and race: serialise them (one stream, or events).  Same results as
+ * pope_flash_decode.
+ */
+int pope_flash_decode_noalloc(const pope_desc* desc, const void* q, const void* k, const void* v,
+                              const float* freqs, const float* bias, const uint8_t* mask, void* o,
+                              float* lse, void* stream);
+
+/*
  * Materialising polar transform: q_hat, k_hat = apply_pope_to_qk(pos, q, k) with the default
  * softplus magnitude (pope.py:30-86).  q (B, Hq, Nq, D), k (B, Hk, Nk, D) in dtype (F32, F16 or
  * BF16, q_s / k_s strides, multiples of 4); q_hat (B, Hq, Nq, D + R), k_hat (B, Hk, Nk, D + R)

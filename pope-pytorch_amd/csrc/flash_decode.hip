@@ -32,6 +32,7 @@
 //   a_d c_jd cos((F_q,d - b_d) - F_j,d)
 //     = c_jd [a_d cos(F_q,d - b_d) cos F_j,d + a_d sin(F_q,d - b_d) sin F_j,d],
 // so the key side needs only cos / sin(F_j) (shared by every head and batch).
+#include <mutex>
 #include <type_traits>
 
 #include "pope_common.hpp"
@@ -428,6 +429,37 @@ hipError_t dispatch(const DecodeParams& p, hipStream_t s) {
 }
 
 }  // namespace
+
+// ---- the decode's own scratch memory, for callers that cannot allocate --------------------------
+//
+// One array per GPU the library runs on, held until the process ends.  In host code `scratch`
+// names a host-side stand-in, never the device memory: its device address comes from
+// hipGetSymbolAddress, asked once per device with that device current, and only that address
+// reaches kernels.  Every call on a GPU shares its array (calls that overlap on one GPU race);
+// the decode writes every partial it reads in the same call, so nothing must start at zero.
+namespace {
+static __device__ __align__(256) char scratch[kDecodeScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+}  // namespace
+
+hipError_t decode_scratch(void** ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return hipSuccess;
+}
 
 int decode_split_keys(int D) {
   const int chunks = (D + 7) / 8;

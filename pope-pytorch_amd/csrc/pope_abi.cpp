@@ -555,6 +555,22 @@ int pope_flash_decode(const pope_desc* d, const void* q, const void* k, const vo
   return POPE_OK;
 }
 
+int pope_flash_decode_noalloc(const pope_desc* d, const void* q, const void* k, const void* v,
+                              const float* freqs, const float* bias, const uint8_t* mask, void* o, float* lse,
+                              void* stream) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  const size_t need = decode_ws(*d);
+  if (need > pope::kDecodeScratchBytes)
+    return fail(POPE_ERR_WORKSPACE, "decode without allocation: %zu bytes of split partials exceed the library's "
+                "%zu-byte scratch array (fewer batch rows x query heads or a shorter cache fit)",
+                need, pope::kDecodeScratchBytes);
+  void* ws = nullptr;
+  const hipError_t e = pope::decode_scratch(&ws);
+  if (e != hipSuccess) return hip_fail(e, "decode scratch address");
+  return pope_flash_decode(d, q, k, v, freqs, bias, mask, o, lse, ws, pope::kDecodeScratchBytes, stream);
+}
+
 int pope_sim_fwd(const pope_desc* d, const void* q, const void* k, const float* freqs, const float* bias,
                  void* sim, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_sim_common(d, q, k, freqs, bias);

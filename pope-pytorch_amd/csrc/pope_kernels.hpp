@@ -163,6 +163,10 @@ struct DecodeParams {
 // freqs, more than decode_max_query_words() query heads x head dim).
 int decode_split_keys(int D);
 int decode_max_query_words();
+// The decode's scratch array on the current device (its device address, looked up once per
+// device): kDecodeScratchBytes, for the entry point that allocates nothing.
+constexpr size_t kDecodeScratchBytes = (size_t)16 << 20;
+hipError_t decode_scratch(void** ptr);
 hipError_t launch_flash_decode(const DecodeParams& p, int dtype, hipStream_t s);
 
 }  // namespace pope

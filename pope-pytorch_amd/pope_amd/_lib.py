@@ -41,7 +41,7 @@ class PopeDesc(ctypes.Structure):
 
 EXPORTS = (
     "pope_abi_version", "pope_last_error", "pope_workspace_bytes", "pope_sim_fwd", "pope_sim_bwd",
-    "pope_flash_fwd", "pope_flash_bwd", "pope_flash_decode", "pope_polar_fwd",
+    "pope_flash_fwd", "pope_flash_bwd", "pope_flash_decode", "pope_flash_decode_noalloc", "pope_polar_fwd",
     "pope_polar_bwd", "pope_profile_enable", "pope_profile_read", "pope_profile_reset",
 )
 
@@ -68,6 +68,8 @@ def _declare(lib):
     lib.pope_flash_bwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     lib.pope_flash_decode.restype = i32
     lib.pope_flash_decode.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
+    lib.pope_flash_decode_noalloc.restype = i32
+    lib.pope_flash_decode_noalloc.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.pope_polar_fwd.restype = i32
     lib.pope_polar_fwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp]
     lib.pope_polar_bwd.restype = i32

@@ -188,3 +188,10 @@ def test_flash_wrappers_check_shapes_before_any_call():
     with pytest.raises(ValueError, match="must match q"):
         _bwd_impl(q[:, :, 1:], q, k, v, q, lse, f, b, None, True, 0.1, False, False)
 
+
+def test_noalloc_decode_rejects_sizes_beyond_its_scratch():
+    """The allocation-free decode holds its split partials in a 16 MiB array of the library: a call
+    whose partials need more fails on the host, before any HIP call, with a clear error."""
+    d = _desc(B=64, Hq=64, Hk=64, Nq=1, Nk=32768, D=64, R=64)
+    st = _lib.lib().pope_flash_decode_noalloc(ctypes.byref(d), _A, _A, _A, _A, _A, None, _A, _A, None)
+    assert st == 3 and "scratch array" in _lib.last_error()
