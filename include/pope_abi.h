@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define POPE_ABI_VERSION 2
+#define POPE_ABI_VERSION 3
 
 enum pope_dtype { POPE_F32 = 0, POPE_F16 = 1, POPE_BF16 = 2 };
 
@@ -43,9 +43,10 @@ enum pope_status {
 };
 
 enum pope_op { POPE_OP_SIM_FWD = 0, POPE_OP_SIM_BWD = 1, POPE_OP_FLASH_FWD = 2,
-               POPE_OP_FLASH_BWD = 3, POPE_OP_FLASH_DECODE = 4 };
+               POPE_OP_FLASH_BWD = 3, POPE_OP_FLASH_DECODE = 4, POPE_OP_POLAR_BWD = 5 };
 
-/* pope_desc.flags (flash backward: PREPARED, ZERO_GRADS; similarity: SPLIT_BF16; 0 elsewhere). */
+/* pope_desc.flags (flash backward: PREPARED, ZERO_GRADS, DETERMINISTIC; similarity: SPLIT_BF16,
+ * DETERMINISTIC; polar transform: COMPLEX, DETERMINISTIC; 0 elsewhere). */
 enum pope_flags {
   /* The workspace holds the preparation (expanded K/Q rows, phase tables, key visibility)
    * written by a pope_flash_fwd call with the same descriptor, q, k, freqs, bias and mask,
@@ -63,7 +64,13 @@ enum pope_flags {
   /* Polar transform: q_hat / k_hat rows are D (re, im) fp32 pairs, the complex64 layout of the
    * reference's return_complex=True output (torch.polar, pope.py:49-51,66-67,74-75): the rotated
    * dims as (a cos, a sin), pass-through dim d as (x_d, 0). */
-  POPE_FLAG_COMPLEX = 8
+  POPE_FLAG_COMPLEX = 8,
+  /* Backward of the flash attention, the similarity and the polar transform: dfreqs and dbias
+   * are bitwise reproducible from call to call.  Every phase derivative is written once to the
+   * workspace (which grows by (B Hk Nk + B Hq Nq) R + 64 Hb R floats) and summed in a fixed
+   * order, instead of fp32 atomics whose order varies.  The other gradients are deterministic
+   * either way. */
+  POPE_FLAG_DETERMINISTIC = 16
 };
 
 /*
@@ -196,11 +203,12 @@ int pope_polar_fwd(const pope_desc* desc, const void* q, const void* k, const fl
  * bias rows bias_sh) are ACCUMULATED into (NULL = not wanted).  The autograd backward of the
  * reference's torch ops (pope.py:30-86).  With POPE_FLAG_COMPLEX the gradients come in the
  * complex layout of the forward (a pass-through dim takes sign(x) times the real part of its
- * pair's gradient: the backward of torch.polar(x, 0) the reference builds it with).
+ * pair's gradient: the backward of torch.polar(x, 0) the reference builds it with).  The
+ * workspace (pope_workspace_bytes(POPE_OP_POLAR_BWD)) is empty unless POPE_FLAG_DETERMINISTIC.
  */
 int pope_polar_bwd(const pope_desc* desc, const float* dq_hat, const float* dk_hat, const void* q, const void* k,
                    const float* freqs, const float* bias, void* dq, void* dk, float* dfreqs, float* dbias,
-                   void* stream);
+                   void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Per-kernel timing.  No counterpart in the reference (its tests print only

@@ -421,6 +421,8 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
   uint16_t* dkb = p.dk + (int64_t)b * p.dk_s[0] + (int64_t)hk * p.dk_s[1];
   const float2* tb = R ? p.table + (int64_t)b * p.t_sb + (int64_t)hk * p.t_sh : nullptr;
   float* dfb = p.dfreqs ? p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)hk * p.df_s[1] : nullptr;
+  // deterministic mode: each key's dpsi is written once, summed later in a fixed order
+  float* kpb = p.kpart ? p.kpart + (int64_t)(b * p.Hk + hk) * Nk * R : nullptr;
   if (R % 32 == 0) {
     auto key_of = [&](int r) { return kw0 + 8 * (r >> 2) + 4 * hf + (r & 3); };
     with_const<EP / 64>(R / 32, [&](auto rbc) {   // rotated blocks: R / 32 <= EP / 64
@@ -445,11 +447,12 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
         const int key = key_of(r);
         if (key < Nk) {
           dkb[(int64_t)key * p.dk_s[2] + d] = T::bits(g);
-          if (dfb) atomicAdd(dfb + (int64_t)key * p.df_s[2] + d, dpsi);
+          if (kpb) kpb[(int64_t)key * R + d] = dpsi;
+          else if (dfb) atomicAdd(dfb + (int64_t)key * p.df_s[2] + d, dpsi);
           dsum += dpsi;
         }
       }
-      if (p.dbias) {
+      if (p.dbias && !kpb) {
         dsum += wave_shfl_xor(dsum, 32);
         if (hf == 0) atomicAdd(&dbias_s[d], dsum);
       }
@@ -490,8 +493,12 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
           const float uc = row[d] * kLn2, us = row[R + d] * kLn2;
           g = sigmoid_f(x) * (cs.x * uc + cs.y * us);
           const float dpsi = softplus_f(x) * (cs.x * us - cs.y * uc);
-          if (dfb) atomicAdd(dfb + (int64_t)key * p.df_s[2] + d, dpsi);
-          if (p.dbias) atomicAdd(&dbias_s[d], dpsi);
+          if (kpb) {
+            kpb[(int64_t)key * R + d] = dpsi;
+          } else {
+            if (dfb) atomicAdd(dfb + (int64_t)key * p.df_s[2] + d, dpsi);
+            if (p.dbias) atomicAdd(&dbias_s[d], dpsi);
+          }
         } else {
           g = row[R + d] * kLn2;
         }
@@ -499,7 +506,7 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
       }
     }
   }
-  if (p.dbias) {
+  if (p.dbias && !kpb) {
     __syncthreads();
     for (int d = tid; d < R; d += C::THREADS) atomicAdd(p.dbias + (int64_t)hk * p.bias_sh + d, dbias_s[d]);
   }
@@ -677,6 +684,8 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
   const float2* tq = R ? p.table + (int64_t)b * p.t_sb + (int64_t)h * p.t_sh : nullptr;
   const float2* bq = R ? p.btab + (p.Hb > 1 ? hk : 0) * R : nullptr;
   float* dfb = p.dfreqs ? p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)h * p.df_s[1] : nullptr;
+  // deterministic mode: each query's dphi is written once, summed later in a fixed order
+  float* qpb = p.qpart && p.dfreqs ? p.qpart + (int64_t)(b * p.Hq + h) * Nq * R : nullptr;
   if (R % 32 == 0) {
     if (qi < Nq) {
       uint16_t* dqrow = dqb + (int64_t)qi * p.dq_s[2];
@@ -712,7 +721,9 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
             const float sn = fmaf(tf[r].y, tbv[r].x, -tf[r].x * tbv[r].y);
             const float uc = dqa[rb][r] * p.scale, us = dqa[rb + RB][r] * p.scale;
             out[c] = sigmoid_f(x[r]) * (cs * uc + sn * us);
-            if (dfb) atomicAdd(dfb + (int64_t)(q_off + qi) * p.df_s[2] + d0 + c, softplus_f(x[r]) * (cs * us - sn * uc));
+            const float dph = softplus_f(x[r]) * (cs * us - sn * uc);
+            if (qpb) qpb[(int64_t)qi * R + d0 + c] = dph;
+            else if (dfb) atomicAdd(dfb + (int64_t)(q_off + qi) * p.df_s[2] + d0 + c, dph);
           }
           u32x2 w;
           w[0] = T::pack2(out[0], out[1]);
@@ -760,7 +771,9 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
           const float cs = fmaf(tf.x, tb.x, tf.y * tb.y), sn = fmaf(tf.y, tb.x, -tf.x * tb.y);
           const float uc = row[d] * p.scale, us = row[R + d] * p.scale;
           g = sigmoid_f(x) * (cs * uc + sn * us);
-          if (dfb) atomicAdd(dfb + (int64_t)(q_off + i) * p.df_s[2] + d, softplus_f(x) * (cs * us - sn * uc));
+          const float dph = softplus_f(x) * (cs * us - sn * uc);
+          if (qpb) qpb[(int64_t)i * R + d] = dph;
+          else if (dfb) atomicAdd(dfb + (int64_t)(q_off + i) * p.df_s[2] + d, dph);
         } else {
           g = row[R + d] * p.scale;
         }

@@ -150,7 +150,12 @@ __global__ __launch_bounds__(kThreads) void polar_bwd_kernel(PolarParams p, Side
         dx[t] = sigmoid_f(x[t]) * (cs * g[2 * t] + sn * g[2 * t + 1]);
         dph[t] = a * (cs * g[2 * t + 1] - sn * g[2 * t]);
       }
-      if (p.dfreqs) {
+      float* part = sd.key ? p.kpart : p.qpart;   // deterministic mode: written once, summed later
+      if (part) {
+        float* dst = part + (((int64_t)b * sd.H + h) * sd.N + n) * p.R + d0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) dst[t] = dph[t];
+      } else if (p.dfreqs) {
         float* df = p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)h * p.df_s[1] + (int64_t)frow * p.df_s[2] + d0;
 #pragma unroll
         for (int t = 0; t < 4; ++t) atomicAdd(df + t, dph[t]);
@@ -169,7 +174,7 @@ __global__ __launch_bounds__(kThreads) void polar_bwd_kernel(PolarParams p, Side
     }
     store4<T>(sd.dx, doff, dx);
   }
-  if (sd.key && p.dbias) {   // sum the workgroup's rows per dim, one atomic per dim
+  if (sd.key && p.dbias && !p.kpart) {   // sum the workgroup's rows per dim, one atomic per dim
 #pragma unroll
     for (int t = 0; t < 4; ++t) red[threadIdx.x][t] = dph[t];
     __syncthreads();

@@ -102,6 +102,57 @@ int check_ws(size_t need, void* ws, size_t have) {
   return POPE_OK;
 }
 
+// Deterministic-mode region at the end of a backward's workspace (POPE_FLAG_DETERMINISTIC):
+//   dpsi (B, Hk, Nk, R) | dphi (B, Hq, Nq, R) | dbias slices            fp32
+// The kernels write every phase derivative once; launch_phase_grad_reduce sums them in a fixed
+// order into dfreqs / dbias.
+size_t det_bytes(const pope_desc& d) {
+  if (!(d.flags & POPE_FLAG_DETERMINISTIC) || d.R == 0) return 0;
+  const int Hb = d.bias_sh != 0 ? d.Hk : 1;
+  return align_up((size_t)d.B * d.Hk * d.Nk * d.R * sizeof(float)) +
+         align_up((size_t)d.B * d.Hq * d.Nq * d.R * sizeof(float)) +
+         align_up(pope::phase_grad_slices(Hb, d.R) * sizeof(float));
+}
+
+struct DetParts {
+  float* kpart;
+  float* qpart;
+  float* slices;
+};
+
+// The region at `base`; null pointers outside deterministic mode, and for parts nothing reads
+// (kpart feeds dfreqs and dbias, qpart dfreqs only).
+DetParts det_parts(const pope_desc& d, char* base, const float* dfreqs, const float* dbias) {
+  DetParts r{nullptr, nullptr, nullptr};
+  if (!det_bytes(d) || (!dfreqs && !dbias)) return r;
+  const size_t kb = align_up((size_t)d.B * d.Hk * d.Nk * d.R * sizeof(float));
+  const size_t qb = align_up((size_t)d.B * d.Hq * d.Nq * d.R * sizeof(float));
+  r.kpart = reinterpret_cast<float*>(base);
+  r.qpart = dfreqs ? reinterpret_cast<float*>(base + kb) : nullptr;
+  r.slices = reinterpret_cast<float*>(base + kb + qb);
+  return r;
+}
+
+hipError_t det_reduce(const pope_desc& d, const DetParts& dp, float* dfreqs, float* dbias, bool overwrite,
+                      hipStream_t s) {
+  if (!dp.kpart) return hipSuccess;
+  pope::PhaseGradParams g;
+  std::memset(&g, 0, sizeof g);
+  g.kpart = dp.kpart;
+  g.qpart = dp.qpart;
+  g.dfreqs = dfreqs;
+  g.dbias = dbias;
+  g.bslices = dp.slices;
+  g.B = d.B; g.Hq = d.Hq; g.Hk = d.Hk; g.Nq = d.Nq; g.Nk = d.Nk; g.R = d.R;
+  g.Bt = d.f_s[0] != 0 ? d.B : 1;
+  g.Ht = d.f_s[1] != 0 ? d.Hq : 1;   // per-head tables need Hq == Hk
+  g.Hb = d.bias_sh != 0 ? d.Hk : 1;
+  g.overwrite = overwrite ? 1 : 0;
+  g.df_s[0] = d.df_s[0]; g.df_s[1] = d.df_s[1]; g.df_s[2] = d.df_s[2];
+  g.bias_sh = d.bias_sh;
+  return pope::launch_phase_grad_reduce(g, s);
+}
+
 // Flash forward / backward workspace (the same layout for both, so the backward can reuse the
 // forward's preparation), each piece 256-byte aligned:
 //   cos/sin(F) (Bt, Ht, Nk, R) float2 | cos/sin(bias) (Hb, R) float2
@@ -139,7 +190,10 @@ FlashLayout flash_layout(const pope_desc& d) {
   return L;
 }
 
-size_t flash_ws(const pope_desc& d, int) { return flash_layout(d).total; }
+// The backward's workspace extends the forward's by the deterministic-mode region.
+size_t flash_ws(const pope_desc& d, int op) {
+  return flash_layout(d).total + (op == POPE_OP_FLASH_BWD ? det_bytes(d) : 0);
+}
 
 // The flash kernels address the rows of v and do inside one (batch, head) with 32-bit element
 // offsets, up to one tile past the padded length.
@@ -210,6 +264,7 @@ size_t sim_ws(const pope_desc& d, int op) {
       n += align_up((size_t)d.B * d.Hk * d.Nk * EP * sizeof(float));
     }
   }
+  if (op == POPE_OP_SIM_BWD) n += det_bytes(d);   // last: its offset is sim_ws - det_bytes
   return n;
 }
 
@@ -300,7 +355,8 @@ int check_sim_common(const pope_desc* d, const void* q, const void* k, const flo
   int rc = check_desc(d);
   if (rc) return rc;
   if (d->dtype != POPE_F32) return fail(POPE_ERR_UNSUPPORTED, "similarity kernels take fp32 (dtype %d)", d->dtype);
-  if (d->flags & ~POPE_FLAG_SPLIT_BF16) return fail(POPE_ERR_INVALID, "unknown flags 0x%x", (unsigned)d->flags);
+  if (d->flags & ~(POPE_FLAG_SPLIT_BF16 | POPE_FLAG_DETERMINISTIC))
+    return fail(POPE_ERR_INVALID, "unknown flags 0x%x", (unsigned)d->flags);
   if (d->D > 256) return fail(POPE_ERR_UNSUPPORTED, "similarity covers head dim <= 256 (got %d)", d->D);
   if (!q || !k) return fail(POPE_ERR_INVALID, "q, k must be non-NULL");
   if (!aligned16(q) || !aligned16(k)) return fail(POPE_ERR_INVALID, "q, k must be 16-byte aligned");
@@ -385,6 +441,7 @@ int pope_workspace_bytes(int op, const pope_desc* desc, size_t* bytes) {
     case POPE_OP_FLASH_FWD:
     case POPE_OP_FLASH_BWD: *bytes = flash_ws(*desc, op); return POPE_OK;
     case POPE_OP_FLASH_DECODE: *bytes = decode_ws(*desc); return POPE_OK;
+    case POPE_OP_POLAR_BWD: *bytes = det_bytes(*desc); return POPE_OK;
     default: return fail(POPE_ERR_INVALID, "unknown op %d", op);
   }
 }
@@ -436,10 +493,10 @@ int pope_flash_bwd(const pope_desc* d, const void* dout, const void* q, const vo
       (rc = check_strides16("dk", d->dk_s)) || (rc = check_strides16("dv", d->dv_s)))
     return rc;
   if (d->R == 0 && (dfreqs || dbias)) return fail(POPE_ERR_INVALID, "dfreqs/dbias requested with rotate dim 0");
-  if (d->flags & ~(POPE_FLAG_PREPARED | POPE_FLAG_ZERO_GRADS))
+  if (d->flags & ~(POPE_FLAG_PREPARED | POPE_FLAG_ZERO_GRADS | POPE_FLAG_DETERMINISTIC))
     return fail(POPE_ERR_INVALID, "unknown flags 0x%x", (unsigned)d->flags);
   const FlashLayout L = flash_layout(*d);
-  if ((rc = check_ws(L.total, workspace, workspace_bytes))) return rc;
+  if ((rc = check_ws(L.total + det_bytes(*d), workspace, workspace_bytes))) return rc;
   if ((rc = check_row_span("v", L.NkP, d->v_s[2])) || (rc = check_row_span("do", L.NqP, d->do_s[2]))) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
@@ -489,10 +546,15 @@ int pope_flash_bwd(const pope_desc* d, const void* dout, const void* q, const vo
   p.mask_sb = d->mask_sb;
   p.t_sb = L.Bt > 1 ? (int64_t)L.Ht * d->Nk * d->R : 0;
   p.t_sh = L.Ht > 1 ? (int64_t)d->Nk * d->R : 0;
+  const DetParts dp = det_parts(*d, ws + L.total, dfreqs, dbias);
+  p.kpart = dp.kpart;
+  p.qpart = dp.qpart;
   hipError_t e = pope::launch_flash_bwd(p, d->dtype, s);
   if (e == hipErrorInvalidValue)
     return fail(POPE_ERR_UNSUPPORTED, "no flash backward kernel for head dim %d, rotate dim %d", d->D, d->R);
   if (e != hipSuccess) return hip_fail(e, "flash backward launch");
+  e = det_reduce(*d, dp, dfreqs, dbias, (d->flags & POPE_FLAG_ZERO_GRADS) != 0, s);
+  if (e != hipSuccess) return hip_fail(e, "phase gradient reduction launch");
   return POPE_OK;
 }
 
@@ -624,11 +686,16 @@ int pope_sim_bwd(const pope_desc* d, const void* dsim, const void* q, const void
   const size_t off_u = sim_table_k(*d) + sim_table_q(*d);
   float* U = reinterpret_cast<float*>(ws + off_u);
   float* W = reinterpret_cast<float*>(ws + off_u + align_up((size_t)d->B * d->Hq * d->Nq * p.EP * sizeof(float)));
+  const DetParts dp = det_parts(*d, ws + sim_ws(*d, POPE_OP_SIM_BWD) - det_bytes(*d), dfreqs, dbias);
+  p.kpart = dp.kpart;
+  p.qpart = dp.qpart;
   if (d->flags & POPE_FLAG_SPLIT_BF16)
     e = pope::launch_sim_split_bwd(p, sim_split_planes(*d, ws, POPE_OP_SIM_BWD), U, W, s);
   else
     e = pope::launch_sim_bwd_ws(p, U, W, s);
   if (e != hipSuccess) return hip_fail(e, "similarity backward launch");
+  e = det_reduce(*d, dp, dfreqs, dbias, false, s);
+  if (e != hipSuccess) return hip_fail(e, "phase gradient reduction launch");
   return POPE_OK;
 }
 
@@ -650,7 +717,8 @@ int check_polar(const pope_desc* d, const void* q, const void* k, const float* f
     if (d->q_s[i] < 0 || d->q_s[i] % 4 || d->k_s[i] < 0 || d->k_s[i] % 4)
       return fail(POPE_ERR_INVALID, "q / k strides must be non-negative multiples of 4");
   if (d->R > 0 && d->bias_sh != 0 && d->bias_sh < d->R) return fail(POPE_ERR_INVALID, "bias row stride below R");
-  if (d->flags & ~POPE_FLAG_COMPLEX) return fail(POPE_ERR_INVALID, "unknown flags 0x%x", (unsigned)d->flags);
+  if (d->flags & ~(POPE_FLAG_COMPLEX | POPE_FLAG_DETERMINISTIC))
+    return fail(POPE_ERR_INVALID, "unknown flags 0x%x", (unsigned)d->flags);
   return check_pope_ptrs(d, freqs, bias);
 }
 
@@ -688,7 +756,7 @@ int pope_polar_fwd(const pope_desc* d, const void* q, const void* k, const float
 
 int pope_polar_bwd(const pope_desc* d, const float* dq_hat, const float* dk_hat, const void* q, const void* k,
                    const float* freqs, const float* bias, void* dq, void* dk, float* dfreqs, float* dbias,
-                   void* stream) {
+                   void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_polar(d, q, k, freqs, bias);
   if (rc) return rc;
   if (!dq_hat || !dk_hat || !aligned16(dq_hat) || !aligned16(dk_hat))
@@ -701,12 +769,19 @@ int pope_polar_bwd(const pope_desc* d, const float* dq_hat, const float* dk_hat,
       return fail(POPE_ERR_INVALID, "dq / dk strides must be non-negative multiples of 4");
   if (d->R == 0 && (dfreqs || dbias)) return fail(POPE_ERR_INVALID, "dfreqs/dbias requested with rotate dim 0");
   if (d->df_s[0] < 0 || d->df_s[1] < 0 || d->df_s[2] < 0) return fail(POPE_ERR_INVALID, "negative dfreqs stride");
+  if ((rc = check_ws(det_bytes(*d), workspace, workspace_bytes))) return rc;
   pope::PolarParams p;
   polar_params(d, q, k, freqs, bias, &p);
   p.gq = dq_hat; p.gk = dk_hat; p.dq = dq; p.dk = dk; p.dfreqs = dfreqs; p.dbias = dbias;
   copy3(p.dq_s, d->dq_s); copy3(p.dk_s, d->dk_s); copy3(p.df_s, d->df_s);
-  const hipError_t e = pope::launch_polar(p, polar_dtype(d), true, reinterpret_cast<hipStream_t>(stream));
+  const DetParts dp = det_parts(*d, static_cast<char*>(workspace), dfreqs, dbias);
+  p.kpart = dp.kpart;
+  p.qpart = dp.qpart;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e = pope::launch_polar(p, polar_dtype(d), true, s);
   if (e != hipSuccess) return hip_fail(e, "polar transform backward launch");
+  e = det_reduce(*d, dp, dfreqs, dbias, false, s);
+  if (e != hipSuccess) return hip_fail(e, "phase gradient reduction launch");
   return POPE_OK;
 }
 

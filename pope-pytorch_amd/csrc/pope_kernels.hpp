@@ -97,6 +97,7 @@ struct FlashBwdParams {
   int B, Hq, Hk, Nq, Nk, D, R, E, EP, DV, NqP, NkP, causal, has_mask;
   int Bt, Ht, Hb;            // extents of the cos/sin table and of the bias rows
   int zero_grads;            // clear dfreqs / dbias before accumulating
+  float* kpart; float* qpart;   // deterministic mode: per-row phase derivatives (PhaseGradParams), else null
   int n_kv_jobs, interleave; // dK/dV jobs of the fused launch; 1 = pair dK/dV and dQ jobs by cost
   float scale;
   int64_t q_s[3], k_s[3], v_s[3], o_s[3], do_s[3], dq_s[3], dk_s[3], dv_s[3], df_s[3];
@@ -112,6 +113,7 @@ struct SimParams {
   float* dq; float* dk; float* dfreqs; float* dbias;
   int B, Hq, Hk, Nq, Nk, D, R, E, EP;
   int g_vec;                 // dsim rows are 16-byte aligned: 4-wide loads allowed
+  float* kpart; float* qpart;   // deterministic mode: per-row phase derivatives (PhaseGradParams), else null
   int64_t q_s[3], k_s[3], sim_s[3], dq_s[3], dk_s[3], f_s[3], df_s[3];
   int64_t bias_sh, kt_sb, kt_sh, qt_sb, qt_sh;
 };
@@ -142,11 +144,28 @@ struct PolarParams {
   void* dq; void* dk; float* dfreqs; float* dbias;
   int B, Hq, Hk, Nq, Nk, D, R;
   int cplx;                             // rows of D (re, im) pairs (complex64 layout) instead of D + R
+  float* kpart; float* qpart;           // deterministic mode: per-row phase derivatives, else null
   int64_t q_s[3], k_s[3], dq_s[3], dk_s[3], f_s[3], df_s[3];
   int64_t bias_sh;
 };
 // dtype: 0 fp32, 1 fp16, 2 bf16 (of q, k, dq, dk)
 hipError_t launch_polar(const PolarParams& p, int dtype, bool bwd, hipStream_t s);
+
+// Deterministic phase gradients (phase_grad.hip): the backward kernels write every key-side phase
+// derivative dpsi once to kpart (B, Hk, Nk, R) and every query-side one dphi to qpart (B, Hq, Nq, R)
+// (query row i <-> phase row Nk - Nq + i); these sums add them in a fixed order into dfreqs
+// (Bt, Ht, Nk, R strides df_s) and dbias (Hb rows, bias_sh): `overwrite` replaces their contents,
+// otherwise the sums are added to them.  bslices: phase_grad_slices(Hb, R) floats of scratch.
+struct PhaseGradParams {
+  const float* kpart; const float* qpart;   // qpart may be null (no query-side derivatives)
+  float* dfreqs; float* dbias;              // null: not wanted
+  float* bslices;
+  int B, Hq, Hk, Nq, Nk, R, Bt, Ht, Hb, overwrite;
+  int64_t df_s[3];
+  int64_t bias_sh;
+};
+size_t phase_grad_slices(int Hb, int R);
+hipError_t launch_phase_grad_reduce(const PhaseGradParams& p, hipStream_t s);
 
 struct DecodeParams {
   const uint16_t* q; const uint16_t* k; const uint16_t* v;

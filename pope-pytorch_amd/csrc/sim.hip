@@ -394,13 +394,15 @@ __global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p,
         const float uc = arow[d] + (arow2 ? arow2[d] : 0.f), us = arow[R + d] + (arow2 ? arow2[R + d] : 0.f);
         out[(int64_t)n * os + d] = sigmoid_f(xv) * (cs.x * uc + cs.y * us);
         const float dph = softplus_f(xv) * (cs.x * us - cs.y * uc);
-        if (p.dfreqs) atomicAdd(p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)hh * p.df_s[1] + (int64_t)prow * p.df_s[2] + d, dph);
+        float* part = side == 0 ? p.qpart : p.kpart;   // deterministic mode: written once, summed later
+        if (part) part[((int64_t)bh * rows + n) * R + d] = dph;
+        else if (p.dfreqs) atomicAdd(p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)hh * p.df_s[1] + (int64_t)prow * p.df_s[2] + d, dph);
         dpsum += dph;
       } else {
         out[(int64_t)n * os + d] = arow[R + d] + (arow2 ? arow2[R + d] : 0.f);
       }
     }
-    if (side == 1 && p.dbias) {
+    if (side == 1 && p.dbias && !p.kpart) {
       red[rg][dl] = dpsum;
       __syncthreads();
       if (rg == 0 && d < R) {

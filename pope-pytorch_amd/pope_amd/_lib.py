@@ -14,11 +14,11 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpope_hip.so")
-ABI_VERSION = 2
-FLAG_PREPARED, FLAG_ZERO_GRADS, FLAG_SPLIT_BF16, FLAG_COMPLEX = 1, 2, 4, 8
+ABI_VERSION = 3
+FLAG_PREPARED, FLAG_ZERO_GRADS, FLAG_SPLIT_BF16, FLAG_COMPLEX, FLAG_DETERMINISTIC = 1, 2, 4, 8, 16
 
 POPE_F32, POPE_F16, POPE_BF16 = 0, 1, 2
-OP_SIM_FWD, OP_SIM_BWD, OP_FLASH_FWD, OP_FLASH_BWD, OP_FLASH_DECODE = range(5)
+OP_SIM_FWD, OP_SIM_BWD, OP_FLASH_FWD, OP_FLASH_BWD, OP_FLASH_DECODE, OP_POLAR_BWD = range(6)
 
 _DTYPE_CODE = {torch.float32: POPE_F32, torch.float16: POPE_F16, torch.bfloat16: POPE_BF16}
 
@@ -73,7 +73,7 @@ def _declare(lib):
     lib.pope_polar_fwd.restype = i32
     lib.pope_polar_fwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp]
     lib.pope_polar_bwd.restype = i32
-    lib.pope_polar_bwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.pope_polar_bwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     lib.pope_profile_enable.restype = i32
     lib.pope_profile_enable.argtypes = [i32]
     lib.pope_profile_read.restype = i32
@@ -163,6 +163,11 @@ def profile_read() -> dict:
         name, cnt, tot, mn, mx = line.split()
         out[name] = (int(cnt), float(tot), float(mn), float(mx))
     return out
+
+
+def deterministic_flag() -> int:
+    """FLAG_DETERMINISTIC when torch.use_deterministic_algorithms(True) is in effect."""
+    return FLAG_DETERMINISTIC if torch.are_deterministic_algorithms_enabled() else 0
 
 
 def dtype_code(dtype: torch.dtype) -> int:

@@ -77,6 +77,7 @@ def polar_bwd_op(gq: Tensor, gk: Tensor, q: Tensor, k: Tensor, freqs: Tensor, bi
     q, k = _rows4(q), _rows4(k)
     gq, gk = gq.float().contiguous(), gk.float().contiguous()
     d = _desc(q, k, freqs, bias, complex_out)
+    d.flags |= _lib.deterministic_flag()   # torch.use_deterministic_algorithms(True): no fp32 atomics
     dq, dk = torch.empty_like(q), torch.empty_like(k)
     d.dq_s[:], d.dk_s[:] = _lib.strides3(dq), _lib.strides3(dk)
     empty = q.new_empty(0, dtype=torch.float32)
@@ -84,10 +85,12 @@ def polar_bwd_op(gq: Tensor, gk: Tensor, q: Tensor, k: Tensor, freqs: Tensor, bi
     dbias = torch.zeros(bias.shape, device=q.device, dtype=torch.float32) if need_dbias else empty
     if need_dfreqs:
         d.df_s[:] = _freqs_strides(dfreqs)
+    ws = _lib.workspace(_lib.OP_POLAR_BWD, d, q.device)
     st = _lib.lib().pope_polar_bwd(ctypes.byref(d), _lib.ptr(gq), _lib.ptr(gk), _lib.ptr(q), _lib.ptr(k),
                                    _lib.ptr(freqs), _lib.ptr(bias), _lib.ptr(dq), _lib.ptr(dk),
                                    _lib.ptr(dfreqs) if need_dfreqs else None,
-                                   _lib.ptr(dbias) if need_dbias else None, _lib.stream_ptr(q.device))
+                                   _lib.ptr(dbias) if need_dbias else None, _lib.ptr(ws),
+                                   0 if ws is None else ws.numel(), _lib.stream_ptr(q.device))
     _lib.check(st, "polar transform backward")
     return dq, dk, dfreqs, dbias
 

@@ -89,6 +89,7 @@ def sim_bwd_op(dsim: Tensor, q: Tensor, k: Tensor, freqs: Tensor, bias: Tensor, 
     L = _lib.lib()
     q, k, dsim = _aligned(q), _aligned(k), _aligned(dsim.float())
     d = _desc(q, k, freqs, bias, split)
+    d.flags |= _lib.deterministic_flag()   # torch.use_deterministic_algorithms(True): no fp32 atomics
     d.sim_s[:] = _lib.strides3(dsim)
     dq, dk = torch.empty_like(q), torch.empty_like(k)
     d.dq_s[:], d.dk_s[:] = _lib.strides3(dq), _lib.strides3(dk)

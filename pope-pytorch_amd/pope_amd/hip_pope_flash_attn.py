@@ -24,7 +24,7 @@ Differences from the reference kernels, by design:
   * the backward skips key/query tiles past the causal diagonal (:167 visits all);
   * out-of-range keys are always masked (:152-199 leaves them in when the call is
     non-causal, unmasked and Nk % 32 != 0);
-  * fp32 inputs run the bf16 MFMA kernels on bf16-rounded q, k, v (the reference
+  * fp32 inputs run the fp16 MFMA kernels on fp16-rounded q, k, v, 10 significant bits (the reference
     runs tl.dot at TF32 for fp32, which is likewise a reduced-precision product).
 """
 from __future__ import annotations
@@ -251,7 +251,8 @@ def _bwd_impl(do, q, k, v, o, lse, freqs, bias, mask, causal, softmax_scale, nee
     alloc_df = torch.zeros if long_freqs else torch.empty
     dfreqs = alloc_df(freqs.shape, device=q.device, dtype=torch.float32) if need_dfreqs else q.new_empty(0, dtype=torch.float32)
     dbias = torch.empty(bias.shape, device=q.device, dtype=torch.float32) if need_dbias else q.new_empty(0, dtype=torch.float32)
-    key = ("bwd", q.shape, q.stride(), k.shape, k.stride(), v.shape, v.stride(), o.stride(), do.stride(),
+    deterministic = _lib.deterministic_flag()
+    key = ("bwd", deterministic, q.shape, q.stride(), k.shape, k.stride(), v.shape, v.stride(), o.stride(), do.stride(),
            dq.stride(), dk.stride(), dv.stride(), q.dtype, k.dtype, v.dtype, o.dtype, causal, softmax_scale,
            _opt_key(freqs), _opt_key(bias), _opt_key(mask), need_dfreqs, need_dbias)
 
@@ -266,7 +267,8 @@ def _bwd_impl(do, q, k, v, o, lse, freqs, bias, mask, causal, softmax_scale, nee
             d.df_s[:] = _freqs_strides(dfreqs)
         if exists(mask):
             d.mask_sb = mask.stride(0)
-        d.flags = _lib.FLAG_ZERO_GRADS
+        # torch.use_deterministic_algorithms(True): dfreqs / dbias summed in a fixed order
+        d.flags = _lib.FLAG_ZERO_GRADS | deterministic
         # the same descriptor with PREPARED set, for calls that bring the forward's workspace
         dp = _lib.PopeDesc.from_buffer_copy(d)
         dp.flags |= _lib.FLAG_PREPARED
@@ -384,7 +386,9 @@ def flash_attn_head_first(q: Tensor, k: Tensor, v: Tensor, freqs: Optional[Tenso
     mask = _prep_mask(mask, q.shape[0])
     out_dtype = q.dtype
     if q.dtype not in _MFMA_DTYPES:
-        q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+        # fp32 inputs: fp16 operands keep 10 significant bits, as the TF32 products of the
+        # reference's fp32 path do (triton_pope_flash_attn.py:80); |x| must stay below 65504
+        q, k, v = q.to(torch.float16), k.to(torch.float16), v.to(torch.float16)
     if k.dtype != q.dtype:
         k = k.to(q.dtype)
     if v.dtype != q.dtype:

@@ -63,3 +63,18 @@ def oracle_attention(inp, causal, scale=None, dtype=torch.float64, grads=True):
 
 def max_abs(a, b):
     return (a.detach().float().cpu() - b.detach().float().cpu()).abs().max().item()
+
+
+def excess_over(got, ref, atol):
+    """Largest |got - ref| - (atol + half an ulp of ref in got's dtype), elementwise; <= 0 means
+    every element is within atol of the exact value beyond the rounding of got's own format (a
+    bf16 output cannot be closer than half an ulp: 1.6e-2 at |x| in [4, 8), 3.1e-2 in [8, 16))."""
+    g = got.detach().double().cpu()
+    r = ref.detach().double().cpu()
+    if got.dtype in (torch.bfloat16, torch.float16):
+        mant = 7 if got.dtype == torch.bfloat16 else 10
+        e = torch.floor(torch.log2(r.abs().clamp_min(1e-30)))
+        half_ulp = torch.pow(2.0, e - mant - 1)
+    else:
+        half_ulp = torch.zeros_like(r)
+    return ((g - r).abs() - (atol + half_ulp)).max().item()

@@ -195,3 +195,21 @@ def test_noalloc_decode_rejects_sizes_beyond_its_scratch():
     d = _desc(B=64, Hq=64, Hk=64, Nq=1, Nk=32768, D=64, R=64)
     st = _lib.lib().pope_flash_decode_noalloc(ctypes.byref(d), _A, _A, _A, _A, _A, None, _A, _A, None)
     assert st == 3 and "scratch array" in _lib.last_error()
+
+
+def test_deterministic_mode_workspace():
+    """POPE_FLAG_DETERMINISTIC adds the per-row phase-derivative region to the backwards' workspaces:
+    dpsi (B, Hk, Nk, R) | dphi (B, Hq, Nq, R) | 64 dbias slices per (bias row, dim), fp32."""
+    al = lambda n: (n + 255) // 256 * 256
+    d = _desc()
+    base = _ws(_lib.OP_FLASH_BWD, d)[1]
+    assert _ws(_lib.OP_POLAR_BWD, d) == (0, 0)
+    d.flags = _lib.FLAG_DETERMINISTIC
+    det = al(2 * 8 * 256 * 32 * 4) + al(2 * 8 * 256 * 32 * 4) + al(8 * 32 * 64 * 4)
+    assert _ws(_lib.OP_FLASH_BWD, d) == (0, base + det)
+    assert _ws(_lib.OP_FLASH_FWD, d)[1] == base           # the forward's layout is unchanged
+    assert _ws(_lib.OP_POLAR_BWD, d) == (0, det)
+    ds = _desc(dtype=_lib.POPE_F32, R=64)
+    plain = _ws(_lib.OP_SIM_BWD, ds)[1]
+    ds.flags = _lib.FLAG_DETERMINISTIC
+    assert _ws(_lib.OP_SIM_BWD, ds)[1] == plain + al(2 * 8 * 256 * 64 * 4) * 2 + al(8 * 64 * 64 * 4)

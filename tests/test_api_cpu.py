@@ -200,3 +200,14 @@ def test_flash_torch_path_half_precision_casts_like_the_reference():
     assert o.dtype == torch.bfloat16
     want = orc.flash_nonfused(qb.double(), kb.double(), vb.double(), freqs, bias, mask=mask, causal=True)
     assert (o.double() - want).abs().max().item() < 2e-2
+
+
+def test_format_aware_bound_helper():
+    """gpu_common.excess_over (the GPU tests' bound for bf16 outputs): exact values rounded to bf16
+    are within 0 beyond the format's half ulp; a 3e-2 error on values near 1 exceeds 2e-2."""
+    from gpu_common import excess_over
+    ref = torch.randn(4096, dtype=torch.float64) * 10
+    assert excess_over(ref.to(torch.bfloat16), ref, 0.0) <= 0
+    small = torch.rand(4096, dtype=torch.float64) * 0.5 + 0.5
+    assert excess_over((small + 0.03).to(torch.bfloat16), small, 2e-2) > 0
+    assert excess_over(small.float(), small, 0.0) <= 1e-7

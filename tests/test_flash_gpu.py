@@ -142,17 +142,16 @@ def test_lse_and_raw_forward(cuda):
 
 
 def test_fp32_inputs_and_custom_scale(cuda):
-    """fp32 inputs run the bf16 MFMA kernels on bf16-rounded q, k, v: against the oracle on those
-    rounded inputs the bf16 tolerance holds; against the fp32 oracle on the unrounded inputs the
-    reference's own fp32 tolerance for its reduced-precision (TF32) fused path holds, 5e-2 absolute
-    (test_flash_attn.py:63-76 uses 5e-2 for half types and 2e-2 for fp32 at TF32)."""
+    """fp32 inputs run the fp16 MFMA kernels on fp16-rounded q, k, v (10 significant bits, as the
+    reference's TF32 products keep): against the oracle on those rounded inputs the half-precision
+    tolerance holds; against the fp32 oracle on the unrounded inputs the reference's own fp32
+    tolerance holds, 2e-2 absolute (test_flash_attn.py:63-76: 5e-2 for half types, 2e-2 for fp32)."""
     inp = make_pope_inputs(5, 1, 4, 4, 128, 128, 64, 32, torch.float32, "prefix")
     res = _run(inp, True, need_grads=True, scale=0.2)
     assert res["o"].dtype == torch.float32
-    rounded = dict(inp, **{n: inp[n].to(torch.bfloat16).float() for n in ("q", "k", "v")})
+    rounded = dict(inp, **{n: inp[n].to(torch.float16).float() for n in ("q", "k", "v")})
     _check(res, oracle_attention(rounded, True, scale=0.2), ["o", "dq", "dk", "dv", "dbias"])
-    _check(res, oracle_attention(inp, True, scale=0.2), ["o", "dq", "dk", "dv", "dbias"],
-           tol_fn=lambda n, r: 5e-2 * (max(1.0, r.abs().max().item()) if n in SUMMED else 1.0))
+    _check(res, oracle_attention(inp, True, scale=0.2), ["o", "dq", "dk", "dv", "dbias"])
 
 
 @pytest.mark.parametrize("seq_len_q", [1, 1024])
@@ -170,8 +169,10 @@ def test_consistent_with_similarity_path(cuda, seq_len_q):
     attn = (sim * 64 ** -0.5).softmax(-1)
     out_sim = torch.einsum("bhij,bhjd->bhid", attn, v.transpose(1, 2)).transpose(1, 2)
     out = pope_amd.flash_attn_with_pope(q, k, v, pos_emb=pope, head_dimension_at_first=False)
-    # bf16 MFMA for fp32 inputs: the bound is the bf16 tolerance, not the reference's TF32 5e-4
-    assert max_abs(out, out_sim) <= TOL
+    # fp32 inputs run on fp16 operands (TF32's 10 significant bits): the reference's bound holds
+    err = max_abs(out, out_sim)
+    print(f"flash vs softmax(sim * scale) v: {err:.2e}")
+    assert err < 5e-4
 
 
 def test_readme_fused_flash_attn(cuda):
