@@ -312,6 +312,18 @@ def axial_bench(steps: int, warmup: int):
     }
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (the `model name` line lscpu reports, read from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(min_seconds: float = 10.0, max_reps: int = 10):
     """The CPU oracle fwd+bwd over the whole C3 workload (every batch and head, two heads per
     call), fp32 after the bf16 cast (the reference's PyTorch path promotes after softplus,
@@ -321,8 +333,9 @@ def cpu_baseline(min_seconds: float = 10.0, max_reps: int = 10):
 
     from oracle import pope_oracle as orc
 
-    # the host share this process is given (OMP_NUM_THREADS), else every core
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
+    # the host share this process is given (OMP_NUM_THREADS, capped by the CPU affinity mask)
+    avail = len(os.sched_getaffinity(0))
+    threads = min(int(os.environ.get("OMP_NUM_THREADS", "0")) or avail, avail)
     torch.set_num_threads(threads)
     q, k, v, do, mask, _ = make_inputs("cpu")
     hs = 2
@@ -349,6 +362,8 @@ def cpu_baseline(min_seconds: float = 10.0, max_reps: int = 10):
         "value": round(STEP_FLOPS / med / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
+        "cpu_model": _cpu_model(),
+        "cpus_in_affinity_mask": avail,
         "kind": "port",
         "sample": f"the whole workload: oracle fwd+bwd (torch fp32, CPU) over B={B} x H={H} heads, "
                   f"N={N}, D={D}, causal, mask, two heads per call; median of {len(times)} passes "
