@@ -18,6 +18,11 @@ for p in (os.path.join(ROOT, "pope-pytorch_amd"), ROOT):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an AMD Instinct MI355X (runs the HIP kernels)")
+    # the host-sanitizer run of the C ABI tests (test_abi_asan.py) points the binding at its build
+    lib_override = os.environ.get("POPE_AMD_TEST_LIB")
+    if lib_override:
+        from pope_amd import _lib
+        _lib.LIB_PATH = lib_override
 
 
 @pytest.fixture
