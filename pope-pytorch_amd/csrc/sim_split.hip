@@ -25,6 +25,7 @@ namespace pope {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kGPre = 3;   // steps of G in flight in the U pass
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
@@ -248,6 +249,13 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p,
 // blocks, so each G value is loaded and split once.  A = G rows (lane = row, 8 consecutive
 // keys, 32 bytes, split on the fly); B = the transposed K_hat planes (128 columns e x 32 keys)
 // through LDS, loaded once per workgroup and double-buffered.
+// G is the stream (dS, read once from HBM): its rows are loaded kGPre steps ahead into a ring of
+// registers.  With VEC (16-byte aligned rows, Nk a multiple of 8) the steps of the unrolled main loop issue
+// the same loads every time (addresses clamped, elements past Nk zeroed after the load), the
+// K_hat^T tile's loads before the step's G loads: the wait for the tile at the end of a step
+// (vmcnt counts in issue order) then leaves kGPre steps of G in flight.  Steps left over after
+// whole rounds of kGPre take a guarded tail loop.
+template <bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void sim_split_u_kernel(SimParams p, SimSplit sp, float* U, int nib, int nec) {
   __shared__ __attribute__((aligned(16))) uint16_t ts[2][kTile];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
@@ -269,13 +277,18 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_u_kernel(SimParams p, S
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[y][r] = 0.f;
 
-  // G of 32 keys: sub-step u covers keys j0 + 16 u + 8 hf .. + 8
-  auto load_g = [&](int j0, float* g) {
-    if (p.g_vec && j0 + 32 <= Nk) {
+  // G of the 32 keys of step st (clamped into [s0, s1)): sub-step u covers keys
+  // j0 + 16 u + 8 hf .. + 8
+  auto load_g = [&](int st, float* g) {
+    const int j0 = 32 * min(max(st, s0), s1 - 1);
+    if constexpr (VEC) {
+      // a valid, 16-byte aligned chunk; a step reaching past Nk zeroes its extra entries when it
+      // is consumed (`step`), so nothing here waits for the load
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const float4 a = *reinterpret_cast<const float4*>(grow + j0 + 16 * u + 8 * hf);
-        const float4 c = *reinterpret_cast<const float4*>(grow + j0 + 16 * u + 8 * hf + 4);
+        const int jl = min(j0 + 16 * u + 8 * hf, Nk - 8);
+        const float4 a = *reinterpret_cast<const float4*>(grow + jl);
+        const float4 c = *reinterpret_cast<const float4*>(grow + jl + 4);
         g[8 * u + 0] = a.x; g[8 * u + 1] = a.y; g[8 * u + 2] = a.z; g[8 * u + 3] = a.w;
         g[8 * u + 4] = c.x; g[8 * u + 5] = c.y; g[8 * u + 6] = c.z; g[8 * u + 7] = c.w;
       }
@@ -289,23 +302,26 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_u_kernel(SimParams p, S
         }
     }
   };
-  float g[16];
-  u32x4 vb[4];
-  if (s0 < s1) {
-    load_g(32 * s0, g);
-    tile_load(sp.kh + bo, sp.kl + bo, sp.NkP, 32 * s0, erows, vb, tid);
-    tile_store(ts[0], vb, tid);
-  }
-  __syncthreads();
-  for (int st = s0; st < s1; ++st) {
+  // one step: split the step's G, issue the next tile's loads and step st + kGPre's G loads, the
+  // products on the current tile, the next tile into the other LDS buffer
+  auto step = [&](int st, float* g) {
     const int buf = (st - s0) & 1;
+    if (VEC && 32 * st + 32 > Nk) {   // the last, partial step: keys past Nk read as zero
+      POPE_COLD_PATH();
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int j = 32 * st + 16 * u + 8 * hf + t;
+          if (j >= Nk) g[8 * u + t] = 0.f;
+        }
+    }
     u32x4 ah[2], al[2];
     split8(g, ah[0], al[0]);
     split8(g + 8, ah[1], al[1]);
-    if (st + 1 < s1) {
-      load_g(32 * (st + 1), g);
-      tile_load(sp.kh + bo, sp.kl + bo, sp.NkP, 32 * (st + 1), erows, vb, tid);
-    }
+    u32x4 vb[4];
+    tile_load(sp.kh + bo, sp.kl + bo, sp.NkP, 32 * min(st + 1, s1 - 1), erows, vb, tid);
+    load_g(st + kGPre, g);
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -314,8 +330,27 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_u_kernel(SimParams p, S
         tile_frag(ts[buf], 32 * y, u, lr, hf, bh16, bl16);
         acc[y] = mfma3(ah[u], al[u], bh16, bl16, acc[y]);
       }
-    if (st + 1 < s1) tile_store(ts[buf ^ 1], vb, tid);
+    tile_store(ts[buf ^ 1], vb, tid);   // the last step's copy is never read
     __syncthreads();
+  };
+  float g[kGPre][16];
+  if (s0 < s1) {
+    {
+      u32x4 vb[4];
+      tile_load(sp.kh + bo, sp.kl + bo, sp.NkP, 32 * s0, erows, vb, tid);
+#pragma unroll
+      for (int k = 0; k < kGPre; ++k) load_g(s0 + k, g[k]);
+      tile_store(ts[0], vb, tid);
+    }
+    __syncthreads();
+    const int nmain = s0 + ((s1 - s0) / kGPre) * kGPre;
+    for (int sb = s0; sb < nmain; sb += kGPre) {
+#pragma unroll
+      for (int k = 0; k < kGPre; ++k) step(sb + k, g[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < kGPre - 1; ++k)
+      if (nmain + k < s1) step(nmain + k, g[k]);
   }
 
   float* ub = (half ? sp.U2 : U) + (int64_t)bh * Nq * EP;
@@ -476,8 +511,12 @@ hipError_t launch_sim_split_bwd(const SimParams& p, const SimSplit& sp, float* U
   if (e != hipSuccess) return e;
   const int nec = (p.EP + 127) / 128;
   const int nib = (p.Nq + 127) / 128, njb = (p.Nk + 127) / 128;
-  e = launch_named("sim_split_u", sim_split_u_kernel, dim3(2 * nib * nec * p.B * p.Hq), dim3(kThreads), s, p, sp, U,
-                   nib, nec);
+  const dim3 ugrid(2 * nib * nec * p.B * p.Hq);
+  // VEC needs Nk % 8 == 0: every 8-key chunk then lies wholly inside or wholly past the row, so a
+  // clamped chunk is only ever one whose entries are all zeroed
+  e = p.g_vec && p.Nk % 8 == 0
+          ? launch_named("sim_split_u", sim_split_u_kernel<true>, ugrid, dim3(kThreads), s, p, sp, U, nib, nec)
+          : launch_named("sim_split_u", sim_split_u_kernel<false>, ugrid, dim3(kThreads), s, p, sp, U, nib, nec);
   if (e != hipSuccess) return e;
   e = launch_named("sim_split_w", sim_split_w_kernel, dim3(2 * njb * nec * p.B * p.Hk), dim3(kThreads), s, p, sp, W,
                    njb, nec);
