@@ -7,7 +7,9 @@ defaults, layouts (``head_dimension_at_first``), asserts and return values.
 
 Dispatch (reference :21-26, :63-71, :86): GPU tensors go to the HIP kernels of
 libpope_hip.so; if that library is missing the call raises -- there is no silent
-fallback.  The torch path (``fused=False`` or CPU tensors) is the reference's own
+fallback.  Flash attention with heads wider than the flash kernels cover (128) runs
+with the polar transform materialised on the device (the polar transform kernel) and
+the attention products in fp32 (``_attend_materialised``).  The torch path (``fused=False`` or CPU tensors) is the reference's own
 non-fused computation, with the key-padding and causal masks combined into one
 explicit boolean mask so the result does not depend on the torch version's
 handling of ``attn_mask`` together with ``is_causal`` (reference :133-138).
@@ -40,9 +42,55 @@ def _to_head_first(*ts):
     return tuple(t.transpose(1, 2) for t in ts)
 
 
+# widest (padded) head dim of the fused flash kernels; flash_attn_with_pope takes wider heads
+# through its materialising path
+FLASH_MAX_HEAD_DIM = 128
+
+
+def _flash_width(D, pos_emb):
+    """Head dim the flash kernels would see: D, or its padded width when D or the rotate dim
+    is not a multiple of 8 (pope_amd._pad)."""
+    from ._pad import pad_plan
+    R = pos_emb[0].shape[-1] if exists(pos_emb) and exists(pos_emb[0]) else 0
+    plan = pad_plan(D, R)
+    return D if plan is None else plan.Dp
+
+
 def _repeat_heads(t, groups):
     """'b h ... -> b (g h) ...': query head i reads kv head i % Hk."""
     return t.repeat(1, groups, *([1] * (t.ndim - 2))) if groups > 1 else t
+
+
+def _keep_mask(mask, causal, Nq, Nk, device):
+    keep = None
+    if exists(mask):
+        keep = mask.bool()[:, None, None, :]
+    if causal:
+        tri = torch.ones(Nq, Nk, dtype=torch.bool, device=device).tril()
+        keep = tri if keep is None else keep & tri
+    return keep
+
+
+def _attend_materialised(q, k, v, pos_emb, mask, causal, softmax_scale):
+    """Head-first PoPE attention for heads wider than the flash kernels cover: q_hat, k_hat from
+    apply_pope_to_qk (the polar transform kernel for GPU tensors), then the masked softmax
+    attention of attention.py:106-145 with the scores and the value product in fp32 (explicit
+    products with contiguous right operands).  A row with every key masked gives 0."""
+    out_dtype = v.dtype
+    if exists(pos_emb):
+        q, k = apply_pope_to_qk(pos_emb, q, k, to_magnitude=F.softplus)
+    groups = q.shape[1] // k.shape[1]
+    k, v = _repeat_heads(k, groups), _repeat_heads(v, groups)
+    qf, kf, vf = q.float(), k.float(), v.float()
+    s = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) * softmax_scale
+    keep = _keep_mask(mask, causal, q.shape[-2], k.shape[-2], q.device)
+    if exists(keep):
+        s = s.masked_fill(~keep, float("-inf"))
+        row_any = keep.any(-1, keepdim=True)
+        p = torch.softmax(s.masked_fill(~row_any, 0.0), dim=-1) * row_any
+    else:
+        p = torch.softmax(s, dim=-1)
+    return torch.matmul(p, vf).to(out_dtype)
 
 
 def compute_attn_similarity_non_fused(q, k, pope, head_dimension_at_first=True):
@@ -73,6 +121,14 @@ def flash_attn_with_pope(q, k, v, pos_emb=None, mask=None, causal=False, softmax
                          head_dimension_at_first=True):
     fused = default(fused, q.is_cuda)
     softmax_scale = default(softmax_scale, q.shape[-1] ** -0.5)
+    wide = fused and _flash_width(q.shape[-1], pos_emb) > FLASH_MAX_HEAD_DIM
+
+    if wide:
+        # heads wider than the flash kernels cover: the polar transform materialised on the device
+        if not head_dimension_at_first:
+            q, k, v = _to_head_first(q, k, v)
+        out = _attend_materialised(q, k, v, pos_emb, mask, causal, softmax_scale)
+        return out.transpose(1, 2) if not head_dimension_at_first else out
 
     if fused:
         from .hip_pope_flash_attn import flash_attn_head_first
@@ -96,12 +152,7 @@ def flash_attn_with_pope(q, k, v, pos_emb=None, mask=None, causal=False, softmax
     if q.dtype != v.dtype:
         v = v.to(q.dtype)
 
-    keep = None
-    if exists(mask):
-        keep = mask.bool()[:, None, None, :]
-    if causal:
-        tri = torch.ones(q.shape[-2], k.shape[-2], dtype=torch.bool, device=q.device).tril()
-        keep = tri if keep is None else keep & tri
+    keep = _keep_mask(mask, causal, q.shape[-2], k.shape[-2], q.device)
     out = F.scaled_dot_product_attention(q, k, v, attn_mask=keep, scale=softmax_scale)
     if exists(keep):
         # rows with every key masked give 0, as the fused kernels do

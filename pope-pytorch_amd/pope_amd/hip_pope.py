@@ -29,6 +29,7 @@ import torch
 from torch import Tensor
 
 from . import _lib
+from ._pad import pad_last, pad_plan, pad_qk
 from .hip_pope_flash_attn import _freqs_strides
 
 
@@ -171,5 +172,10 @@ def hip_compute_qk_similarity(q, k, freqs, bias, rotate_dim=None, allow_tf32=Tru
         raise ValueError(f"freqs has {freqs.shape[-2]} positions, keys need {k.shape[2]}")
     out_dtype = q.dtype
     qf, kf = q.float(), k.float()
+    # head / rotate dims that are not multiples of 8: padded on the device (pope_amd._pad)
+    plan = pad_plan(q.shape[-1], R)
+    if plan is not None:
+        qf, kf = pad_qk(qf, plan), pad_qk(kf, plan)
+        freqs, bias = pad_last(freqs, plan.R8), pad_last(bias, plan.R8)
     sim = sim_fwd_op(qf, kf, freqs, bias, bool(allow_tf32))
     return sim.to(out_dtype) if out_dtype != torch.float32 else sim

@@ -36,6 +36,7 @@ import torch
 from torch import Tensor
 
 from . import _lib
+from ._pad import pad_last, pad_plan, pad_qk, unpad_qk
 
 _MFMA_DTYPES = (torch.bfloat16, torch.float16)
 
@@ -393,7 +394,14 @@ def flash_attn_head_first(q: Tensor, k: Tensor, v: Tensor, freqs: Optional[Tenso
         k = k.to(q.dtype)
     if v.dtype != q.dtype:
         v = v.to(q.dtype)
+    # head / rotate dims that are not multiples of 8: padded on the device (pope_amd._pad)
+    plan = pad_plan(q.shape[-1], freqs.shape[-1] if exists(freqs) else 0)
+    if plan is not None:
+        q, k, v = pad_qk(q, plan), pad_qk(k, plan), pad_last(v, plan.Dp)
+        freqs, pope_bias = pad_last(freqs, plan.R8), pad_last(pope_bias, plan.R8)
     o = _flash(q, k, v, freqs, pope_bias, mask, causal, float(scale))
+    if plan is not None:
+        o = o[..., :plan.D]
     return o.to(out_dtype) if o.dtype != out_dtype else o
 
 
@@ -407,7 +415,13 @@ def flash_attn_forward(q, k, v, freqs=None, pope_bias=None, mask=None, causal=Fa
     qh, kh, vh = (t.transpose(1, 2) for t in (q, k, v))
     if exists(freqs) and freqs.ndim == 4:
         freqs = freqs.transpose(1, 2)   # (B, N, H, R) -> (B, H, N, R) view
+    plan = pad_plan(q.shape[-1], freqs.shape[-1] if exists(freqs) else 0)
+    if plan is not None:
+        qh, kh, vh = pad_qk(qh, plan), pad_qk(kh, plan), pad_last(vh, plan.Dp)
+        freqs, pope_bias = pad_last(freqs, plan.R8), pad_last(pope_bias, plan.R8)
     o, lse, _ = flash_fwd_op(qh, kh, vh, freqs, pope_bias, mask, causal, float(scale))
+    if plan is not None:
+        o = o[..., :plan.D]
     return o.transpose(1, 2), lse
 
 
@@ -423,8 +437,18 @@ def flash_attn_backward(do, q, k, v, o, lse, dq, dk, dv, dfreqs=None, dpope_bias
     mask = _prep_mask(mask, q.shape[0])
     tr = lambda t: t.transpose(1, 2)
     f = freqs.transpose(1, 2) if exists(freqs) and freqs.ndim == 4 else freqs
-    gq, gk, gv, gf, gb = flash_bwd_op(tr(do), tr(q), tr(k), tr(v), tr(o), lse, f, pope_bias, mask, causal,
+    tq, tk, tv, to, tdo = tr(q), tr(k), tr(v), tr(o), tr(do)
+    plan = pad_plan(q.shape[-1], freqs.shape[-1] if exists(freqs) else 0)
+    if plan is not None:
+        tq, tk = pad_qk(tq, plan), pad_qk(tk, plan)
+        tv, to, tdo = pad_last(tv, plan.Dp), pad_last(to, plan.Dp), pad_last(tdo, plan.Dp)
+        f, pope_bias = pad_last(f, plan.R8), pad_last(pope_bias, plan.R8)
+    gq, gk, gv, gf, gb = flash_bwd_op(tdo, tq, tk, tv, to, lse, f, pope_bias, mask, causal,
                                       float(scale), exists(dfreqs), exists(dpope_bias))
+    if plan is not None:
+        gq, gk, gv = unpad_qk(gq, plan), unpad_qk(gk, plan), gv[..., :plan.D]
+        gf = gf[..., :plan.R] if exists(dfreqs) else gf
+        gb = gb[..., :plan.R] if exists(dpope_bias) else gb
     dq.add_(tr(gq))
     dk.copy_(tr(gk))
     dv.copy_(tr(gv))
