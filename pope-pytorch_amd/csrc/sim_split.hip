@@ -387,8 +387,11 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_w_kernel(SimParams p, S
   const int nst = groups * nis, hst = (nst + 1) / 2;
   const int s0 = half * hst, s1 = min(nst, s0 + hst);
   const int erows = min(128, EP - ec * 128);
-  // G tile loader: thread -> key quad c (keys 4 c .. 4 c + 3), rows 4 rg .. 4 rg + 3 of the step
-  const int c = tid & 31, rg = tid >> 5;
+  // G tile loader: thread -> key quad c (keys 4 c .. 4 c + 3), rows 4 rg .. 4 rg + 3 of the step.
+  // rg runs fastest so that the eight lanes of one key quad write one 64-byte LDS row segment:
+  // a 16-lane group of 8-byte stores then covers every bank once (80-dword row stride); a wave's
+  // global load reads eight 128-byte row segments.
+  const int c = tid >> 3, rg = tid & 7;
   const int jq = jb * 128 + 4 * c;
   const bool vec = p.g_vec && jq + 3 < Nk;
 
