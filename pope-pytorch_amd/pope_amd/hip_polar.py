@@ -22,6 +22,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from . import _lib
+from ._pad import pad_last, pad_plan, pad_qk
 from .hip_pope_flash_attn import _freqs_strides
 
 
@@ -141,7 +142,8 @@ def fits(q: Tensor, k: Tensor, freqs: Tensor, bias: Tensor, to_magnitude, return
         return False
     B, Hq, Nq, D = q.shape
     R = freqs.shape[-1]
-    if k.shape[0] != B or k.shape[-1] != D or D % 8 or R % 8 or D > 512 or R > D or Nq > k.shape[2] or R == 0:
+    plan = pad_plan(D, R)   # head / rotate dims not multiples of 8: padded in polar()
+    if k.shape[0] != B or k.shape[-1] != D or (plan.Dp if plan else D) > 512 or R > D or Nq > k.shape[2] or R == 0:
         return False
     if bias.shape[-1] != R or bias.shape[0] not in (1, k.shape[1]) or bias.stride(-1) != 1:
         return False
@@ -149,9 +151,21 @@ def fits(q: Tensor, k: Tensor, freqs: Tensor, bias: Tensor, to_magnitude, return
 
 
 def polar(q: Tensor, k: Tensor, freqs: Tensor, bias: Tensor, return_complex: bool = False) -> tuple[Tensor, Tensor]:
+    D, R = q.shape[-1], freqs.shape[-1]
+    plan = pad_plan(D, R)
+    if plan is not None:
+        # rows padded on the device (pope_amd._pad); the padded dims' output columns are dropped
+        q, k = pad_qk(q, plan), pad_qk(k, plan)
+        freqs, bias = pad_last(freqs, plan.R8), pad_last(bias, plan.R8)
     qh, kh = polar_fwd_op(q, k, freqs, bias, return_complex)
     if return_complex:
-        D = q.shape[-1]
-        qh = torch.view_as_complex(qh.view(*qh.shape[:-1], D, 2))
-        kh = torch.view_as_complex(kh.view(*kh.shape[:-1], D, 2))
+        W = q.shape[-1]
+        qh = torch.view_as_complex(qh.view(*qh.shape[:-1], W, 2))
+        kh = torch.view_as_complex(kh.view(*kh.shape[:-1], W, 2))
+        if plan is not None:   # complex dims: R rotated, then D - R pass-through
+            keep = lambda t: torch.cat([t[..., :R], t[..., plan.R8:plan.R8 + D - R]], -1)
+            qh, kh = keep(qh), keep(kh)
+    elif plan is not None:     # real columns: 2 R interleaved (cos, sin) pairs, then D - R pass-through
+        keep = lambda t: torch.cat([t[..., :2 * R], t[..., 2 * plan.R8:2 * plan.R8 + D - R]], -1)
+        qh, kh = keep(qh), keep(kh)
     return qh, kh

@@ -23,6 +23,9 @@ CASES = [
     (2, 2, 2, 64, 64, 48, 16, torch.float16, True, 2),        # D = 48, per-batch positions
     (1, 2, 2, 33, 33, 128, 128, torch.float32, True, 1),      # one bias row broadcast over the heads
     (1, 3, 3, 40, 40, 96, 96, torch.bfloat16, False, 3),      # D = 96 (12 units per row)
+    (2, 4, 2, 50, 70, 20, 3, torch.float32, False, 2),        # D, R not multiples of 8 (padded rows)
+    (1, 2, 2, 33, 33, 44, 12, torch.bfloat16, True, 1),       # ragged pass-through part
+    (1, 2, 2, 40, 40, 23, 23, torch.float32, False, 2),       # every dim rotated, odd count
 ]
 
 
@@ -82,8 +85,9 @@ def test_polar_forward_backward(cuda, cfg):
         assert e <= tol, f"{name}: {e:.3e} > {tol:.3e}"
 
 
-@pytest.mark.parametrize("cfg", [(1, 2, 2, 16, 16, 32, 16, False), (2, 4, 2, 40, 72, 64, 64, True)],
-                         ids=["partial", "full-f3"])
+@pytest.mark.parametrize("cfg", [(1, 2, 2, 16, 16, 32, 16, False), (2, 4, 2, 40, 72, 64, 64, True),
+                                 (1, 2, 2, 24, 24, 20, 3, False)],
+                         ids=["partial", "full-f3", "odd-dims"])
 def test_polar_complex_output(cuda, cfg):
     """return_complex=True on the kernels: complex64 rows of (a cos, a sin) pairs with pass-through
     dims as (x, 0) (pope.py:49-51,66-67,74-75), forward and backward vs the oracle's torch.polar."""
