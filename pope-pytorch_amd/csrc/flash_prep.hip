@@ -1,14 +1,21 @@
 // Shared preparation of the PoPE flash forward and backward (gfx950).
 //
 // The polar transform of the reference (pope.py:30-86, triton_pope_flash_attn.py:52-57,73-79)
-// is applied once per call and the expanded rows are kept in the caller's workspace:
-//   flash_setup  cos/sin(F[n, d]) for n < Nk (accurate sincosf, fp32 pairs), cos/sin(bias[hb, d])
-//                and the key visibility words (bit j of word w: key 64 w + j < Nk and
-//                mask[b, key] != 0, the reference's keep convention, attention.py:129-131);
-//   flash_prep   K_hat, Q_hat (pre-scaled by softmax_scale * log2 e) and, per batch, one past
-//                the last visible key.
-// The forward reads K_hat / Q_hat tiles straight into LDS; the backward reuses them (and the
-// cos/sin table for its chain rule) when the forward's workspace is handed to it.
+// is applied once per call and the expanded rows are kept in the caller's workspace.  One
+// launch, four kinds of blocks:
+//   K_hat items   8 dims of one key row: cos/sin(F[n, d]) (FMA-split reduction to revolutions and
+//                 the hardware sine / cosine, sincos_rev), the row's cos and sin chunks of K_hat
+//                 and, from the items of the first batch / head that own a table row, the
+//                 cos/sin table (fp32 pairs, n < Nk) that the backward's chain rule reads;
+//   Q_hat items   the same for a query row at phase F[Nk - Nq + i] - bias, pre-scaled by
+//                 softmax_scale * log2 e;
+//   mask words    bit j of word w: key 64 w + j < Nk and mask[b, key] != 0 (the reference's keep
+//                 convention, attention.py:129-131), one wave per word;
+//   batch blocks  one past the last visible key of each batch, from the mask bytes directly;
+//                 the first one also writes cos/sin(bias) for the backward.
+// No block reads what another writes, so nothing orders them.  The forward reads K_hat / Q_hat
+// tiles straight into LDS; the backward reuses them (and the tables) when the forward's
+// workspace is handed to it.
 #include "pope_common.hpp"
 #include "pope_kernels.hpp"
 
@@ -19,84 +26,11 @@ namespace {
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(uint16_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
-constexpr int kSetupBlocksMax = 2048;
-
-// Block ranges of flash_setup: [table | bias table | mask words (4 per block, one per wave)].
-struct SetupGrid {
-  int64_t n_tab;
-  int b_tab, b_bias, b_mask;
-};
-SetupGrid setup_grid(const FlashPrep& p) {
-  SetupGrid g;
-  g.n_tab = (int64_t)p.Bt * p.Ht * p.Nk * p.R;
-  const int64_t bt = (g.n_tab / 4 + 255) / 256;   // four entries per thread
-  g.b_tab = (int)(bt > kSetupBlocksMax ? kSetupBlocksMax : bt);
-  g.b_bias = p.R > 0 ? (p.Hb * p.R + 255) / 256 : 0;
-  g.b_mask = (p.B * p.NW + 3) / 4;
-  return g;
-}
-
-__global__ __launch_bounds__(256) void flash_setup_kernel(FlashPrep p, SetupGrid g) {
-  const int blk = blockIdx.x;
-  if (blk < g.b_tab) {
-    // cos/sin(F) rows, grid-stride over (bt, ht, n, d): four consecutive entries of one row per
-    // thread (R is a multiple of 8), four independent loads, two 16-byte stores; the index is
-    // decomposed in 32 bits when the table allows
-    for (int64_t i4 = 4 * ((int64_t)blk * 256 + threadIdx.x); i4 < g.n_tab; i4 += 4 * (int64_t)g.b_tab * 256) {
-      int d, n, ht, bt;
-      if (g.n_tab < INT32_MAX) {
-        const int i = (int)i4;
-        d = i % p.R;
-        int rest = i / p.R;
-        n = rest % p.Nk;
-        rest /= p.Nk;
-        ht = rest % p.Ht;
-        bt = rest / p.Ht;
-      } else {
-        d = (int)(i4 % p.R);
-        int64_t rest = i4 / p.R;
-        n = (int)(rest % p.Nk);
-        rest /= p.Nk;
-        ht = (int)(rest % p.Ht);
-        bt = (int)(rest / p.Ht);
-      }
-      const float* f = p.freqs + (int64_t)bt * p.f_s[0] + (int64_t)ht * p.f_s[1] + (int64_t)n * p.f_s[2] + d;
-      float x[4], sn[4], cs[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) x[t] = f[t];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) sincos_acc(x[t], &sn[t], &cs[t]);
-      float4* dst = reinterpret_cast<float4*>(p.table + i4);
-      dst[0] = make_float4(cs[0], sn[0], cs[1], sn[1]);
-      dst[1] = make_float4(cs[2], sn[2], cs[3], sn[3]);
-    }
-    return;
-  }
-  if (blk < g.b_tab + g.b_bias) {   // cos/sin(bias)
-    const int idx = (blk - g.b_tab) * 256 + threadIdx.x;
-    if (idx < p.Hb * p.R) {
-      const int hb = idx / p.R, d = idx % p.R;
-      float sn, cs;
-      sincos_acc(p.bias[(int64_t)hb * p.bias_sh + d], &sn, &cs);
-      p.btab[idx] = make_float2(cs, sn);
-    }
-    return;
-  }
-  // key visibility words: one wave per word, one lane per key
-  const int wi = (blk - g.b_tab - g.b_bias) * 4 + (threadIdx.x >> 6);
-  if (wi >= p.B * p.NW) return;
-  const int b = wi / p.NW, w = wi % p.NW, lane = threadIdx.x & 63;
-  const int key = 64 * w + lane;
-  const bool vis = key < p.Nk && (!p.has_mask || p.mask[(int64_t)b * p.mask_sb + key] != 0);
-  const uint64_t bits = __ballot(vis);
-  if (lane == 0) p.mwords[wi] = bits;
-}
-
-// Block ranges of flash_prep: [K_hat items | Q_hat items | kend (one block per batch)].
+// Block ranges of flash_prep: [K_hat items | Q_hat items | mask words (4 per block) | batches].
 struct PrepGrid {
   int nitem;            // work items per row: R/8 rotated chunks, (D-R)/8 pass-through, (EP-E)/8 zero
   int64_t n_k, n_q;     // items of the K_hat and Q_hat parts
-  int b_k, b_q;
+  int b_k, b_q, b_mask;
 };
 PrepGrid prep_grid(const FlashPrep& p) {
   PrepGrid g;
@@ -105,6 +39,7 @@ PrepGrid prep_grid(const FlashPrep& p) {
   g.n_q = (int64_t)p.B * p.Hq * p.NqP * g.nitem;
   g.b_k = (int)((g.n_k + 255) / 256);
   g.b_q = (int)((g.n_q + 255) / 256);
+  g.b_mask = (p.B * p.NW + 3) / 4;
   return g;
 }
 
@@ -138,21 +73,53 @@ template <typename T>
 __global__ __launch_bounds__(256) void flash_prep_kernel(FlashPrep p, PrepGrid g) {
   const int blk = blockIdx.x;
   const int D = p.D, R = p.R, EP = p.EP, E = D + R;
-  if (blk >= g.b_k + g.b_q) {   // kend: 1 + last visible key of batch b
-    const int b = blk - g.b_k - g.b_q;
+  if (blk >= g.b_k + g.b_q + g.b_mask) {   // batch b: 1 + last visible key; cos/sin(bias)
+    const int b = blk - g.b_k - g.b_q - g.b_mask;
+    if (b == 0)
+      for (int i = threadIdx.x; i < p.Hb * R; i += 256) {
+        const int hb = i / R, d = i % R;
+        float sn, cs;
+        sincos_rev(p.bias[(int64_t)hb * p.bias_sh + d], &sn, &cs);
+        p.btab[i] = make_float2(cs, sn);
+      }
     int last = 0;
-    for (int w = threadIdx.x; w < p.NW; w += 256) {
-      const uint64_t bits = p.mwords[(int64_t)b * p.NW + w];
-      if (bits) last = max(last, 64 * w + 64 - (int)__builtin_clzll(bits));
+    if (!p.has_mask) {
+      last = p.Nk;
+    } else {
+      const uint8_t* mrow = p.mask + (int64_t)b * p.mask_sb;
+      int j = threadIdx.x;   // each thread's keys ascend: its last hit is its maximum
+      if ((reinterpret_cast<uintptr_t>(mrow) & 15) == 0) {
+        // 16 mask bytes per load; the highest nonzero byte of a word (little-endian) is its last key
+        const int n16 = p.Nk / 16;
+        for (int c = threadIdx.x; c < n16; c += 256) {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(mrow + 16 * c);
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            if (w[t]) last = 16 * c + 4 * t + (31 - (int)__builtin_clz(w[t])) / 8 + 1;
+        }
+        j = 16 * n16 + threadIdx.x;
+      }
+      for (; j < p.Nk; j += 256)
+        if (mrow[j]) last = j + 1;
     }
     __shared__ int red[256];
     red[threadIdx.x] = last;
     __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-      if ((int)threadIdx.x < s) red[threadIdx.x] = max(red[threadIdx.x], red[threadIdx.x + s]);
+    for (int st = 128; st > 0; st >>= 1) {
+      if ((int)threadIdx.x < st) red[threadIdx.x] = max(red[threadIdx.x], red[threadIdx.x + st]);
       __syncthreads();
     }
     if (threadIdx.x == 0) p.kend[b] = red[0];
+    return;
+  }
+  if (blk >= g.b_k + g.b_q) {   // key visibility words: one wave per word, one lane per key
+    const int wi = (blk - g.b_k - g.b_q) * 4 + (threadIdx.x >> 6);
+    if (wi >= p.B * p.NW) return;
+    const int b = wi / p.NW, w = wi % p.NW, lane = threadIdx.x & 63;
+    const int key = 64 * w + lane;
+    const bool vis = key < p.Nk && (!p.has_mask || p.mask[(int64_t)b * p.mask_sb + key] != 0);
+    const uint64_t bits = __ballot(vis);
+    if (lane == 0) p.mwords[wi] = bits;
     return;
   }
   const bool is_k = blk < g.b_k;
@@ -192,25 +159,33 @@ __global__ __launch_bounds__(256) void flash_prep_kernel(FlashPrep p, PrepGrid g
   const u32x4 raw = ld16(src + d0);
   float cs[8], sn[8];
   if (d0 < R) {
-    // phase row: keys use F[j]; queries F[Nk - Nq + i] rotated by -bias of their kv head
+    // phase row: keys use F[j]; queries F[Nk - Nq + i] rotated by -bias of their kv head.  The
+    // table and the freqs rows share their (batch, head) selection (Bt, Ht of 1 broadcast).
     const int pos = is_k ? n : p.Nk - p.Nq + n;
-    const float2* t = p.table + (int64_t)b * p.t_sb + (int64_t)h * p.t_sh + (int64_t)pos * R + d0;
+    const int bt = p.Bt > 1 ? b : 0, ht = p.Ht > 1 ? h : 0;
+    const float* f = p.freqs + (int64_t)bt * p.f_s[0] + (int64_t)ht * p.f_s[1] + (int64_t)pos * p.f_s[2] + d0;
+    float x[8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const float2 f = t[s];
-      cs[s] = f.x;
-      sn[s] = f.y;
+    for (int t = 0; t < 8; ++t) x[t] = f[t];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) sincos_rev(x[t], &sn[t], &cs[t]);
+    if (is_k && (p.Bt > 1 || b == 0) && (p.Ht > 1 || h == 0)) {   // one writer per table row
+      float4* tdst = reinterpret_cast<float4*>(p.table + (int64_t)bt * p.t_sb + (int64_t)ht * p.t_sh +
+                                               (int64_t)n * R + d0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) tdst[t] = make_float4(cs[2 * t], sn[2 * t], cs[2 * t + 1], sn[2 * t + 1]);
     }
     if (!is_k) {
       const int hb = p.Hb > 1 ? h % p.Hk : 0;
-      const float2* bt = p.btab + hb * R + d0;
+      const float* bb = p.bias + (int64_t)hb * p.bias_sh + d0;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const float2 c = bt[s];   // cos(F - b) = cF cb + sF sb,  sin(F - b) = sF cb - cF sb
-        const float c2 = fmaf(cs[s], c.x, sn[s] * c.y);
-        const float s2 = fmaf(sn[s], c.x, -cs[s] * c.y);
-        cs[s] = c2;
-        sn[s] = s2;
+      for (int t = 0; t < 8; ++t) {
+        float sb, cb;   // cos(F - b) = cF cb + sF sb,  sin(F - b) = sF cb - cF sb
+        sincos_rev(bb[t], &sb, &cb);
+        const float c2 = fmaf(cs[t], cb, sn[t] * sb);
+        const float s2 = fmaf(sn[t], cb, -cs[t] * sb);
+        cs[t] = c2;
+        sn[t] = s2;
       }
     }
   }
@@ -220,12 +195,8 @@ __global__ __launch_bounds__(256) void flash_prep_kernel(FlashPrep p, PrepGrid g
 }  // namespace
 
 hipError_t launch_flash_prep(const FlashPrep& p, int dtype, hipStream_t s) {
-  const SetupGrid sg = setup_grid(p);
-  const int sblocks = sg.b_tab + sg.b_bias + sg.b_mask;
-  hipError_t e = launch_named("flash_setup", flash_setup_kernel, dim3(sblocks), dim3(256), s, p, sg);
-  if (e != hipSuccess) return e;
   const PrepGrid pg = prep_grid(p);
-  const dim3 grid(pg.b_k + pg.b_q + p.B);
+  const dim3 grid(pg.b_k + pg.b_q + pg.b_mask + p.B);
   return dtype == 2 ? launch_named("flash_prep", flash_prep_kernel<BF16>, grid, dim3(256), s, p, pg)
                     : launch_named("flash_prep", flash_prep_kernel<F16>, grid, dim3(256), s, p, pg);
 }

@@ -43,11 +43,10 @@ struct TableParams {
 };
 hipError_t launch_phase_table(const TableParams& p, hipStream_t s);
 
-// Shared preparation of the flash forward and backward (flash_prep.hip), written into the
-// caller's workspace once per forward call and reused by the backward:
-//   flash_setup: cos/sin(F) rows n < Nk (fp32 pairs), cos/sin(bias) per (bias row, dim), key
-//                visibility words;
-//   flash_prep : K_hat and the pre-scaled Q_hat rows, 1 + last visible key per batch.
+// Shared preparation of the flash forward and backward (flash_prep.hip, one launch), written
+// into the caller's workspace once per forward call and reused by the backward: K_hat and the
+// pre-scaled Q_hat rows, cos/sin(F) rows n < Nk (fp32 pairs), cos/sin(bias) per (bias row, dim),
+// the key visibility words and 1 + last visible key per batch.
 // The expanded rows (16-bit, EP columns, zero past E and past Nq / Nk) are
 //   K_hat[b, hk, j] = [c cos F_j | c sin F_j | k_rest],                c = softplus(k_j)
 //   Q_hat[b, h, i]  = s [a cos(F_i' - bias) | a sin(F_i' - bias) | q_rest],  a = softplus(q_i),
