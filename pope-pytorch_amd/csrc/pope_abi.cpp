@@ -364,7 +364,8 @@ int check_sim_common(const pope_desc* d, const void* q, const void* k, const flo
   return check_pope_ptrs(d, freqs, bias);
 }
 
-// Builds the key table (with bias) and the query table (without) and fills the shared parameters.
+// Builds the key table (with bias) and the query table (without) for the fp32 kernels (the
+// split-bf16 kernels compute the phases in place) and fills the shared parameters.
 hipError_t sim_setup(const pope_desc& d, const void* q, const void* k, const float* freqs, const float* bias,
                      char* ws, hipStream_t s, pope::SimParams* out) {
   pope::SimParams& p = *out;
@@ -373,7 +374,9 @@ hipError_t sim_setup(const pope_desc& d, const void* q, const void* k, const flo
   const int Hqt = d.f_s[1] != 0 ? d.Hq : 1;
   float2* ktab = reinterpret_cast<float2*>(ws);
   float2* qtab = reinterpret_cast<float2*>(ws + sim_table_k(d));
-  if (d.R > 0) {
+  // the fp32 kernels read the phases from tables; the split-bf16 kernels compute them in place
+  const bool tables = d.R > 0 && !(d.flags & POPE_FLAG_SPLIT_BF16);
+  if (tables) {
     hipError_t e = build_table(d, freqs, bias, Bt, d.Hk, ktab, s);
     if (e != hipSuccess) return e;
     e = build_table(d, freqs, nullptr, Bt, Hqt, qtab, s);  // query phases never carry the bias
@@ -383,8 +386,8 @@ hipError_t sim_setup(const pope_desc& d, const void* q, const void* k, const flo
   p.k = static_cast<const float*>(k);
   p.freqs = d.R > 0 ? freqs : nullptr;
   p.bias = d.R > 0 ? bias : nullptr;
-  p.ktab = d.R > 0 ? ktab : nullptr;
-  p.qtab = d.R > 0 ? qtab : nullptr;
+  p.ktab = tables ? ktab : nullptr;
+  p.qtab = tables ? qtab : nullptr;
   p.B = d.B; p.Hq = d.Hq; p.Hk = d.Hk; p.Nq = d.Nq; p.Nk = d.Nk; p.D = d.D; p.R = d.R;
   p.E = d.D + d.R;
   p.EP = round_up(p.E, 32);

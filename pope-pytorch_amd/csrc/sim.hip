@@ -21,6 +21,7 @@
 // (_bwd_kernel_dbias_optimized): both are the derivative of S by the key phase.
 #include "pope_common.hpp"
 #include "pope_kernels.hpp"
+#include "sim_phase.hpp"
 
 namespace pope {
 
@@ -351,15 +352,23 @@ __global__ __launch_bounds__(kThreads, 2) void sim_bwd_w_kernel(SimParams p, flo
   }
 }
 
-// Finalize: chain rule of the polar transform for one side.
-//   side 0: rows = queries of (b, h), acc = U, out = dq, phase row = q_off + i, no bias
-//   side 1: rows = keys of (b, hk), acc = W, out = dk, phase row = j, dbias accumulated
-// one workgroup = 32 rows of one (b, head); thread -> (dim lane, row group).
-__global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p, const float* acc, const float* acc2,
-                                                                     int side, int nrb) {
+// Finalize: chain rule of the polar transform, both sides in one launch.
+//   side 0 (blocks [0, nqb)): rows = queries of (b, h), acc = U, out = dq, phase row = q_off + i,
+//                             no bias
+//   side 1 (the rest):        rows = keys of (b, hk), acc = W, out = dk, phase row = j, dbias
+//                             accumulated
+// one workgroup = 32 rows of one (b, head); thread -> (dim lane, row group).  The phases come from
+// the tables when present, else are computed in place (sim_phase).
+__global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p, const float* U, const float* U2,
+                                                                     const float* W, const float* W2, int nqb) {
   __shared__ float red[4][256];
   const int tid = threadIdx.x;
-  const int rb = blockIdx.x % nrb, bh = blockIdx.x / nrb;
+  const int side = (int)blockIdx.x < nqb ? 0 : 1;
+  const float* acc = side == 0 ? U : W;
+  const float* acc2 = side == 0 ? U2 : W2;
+  const int nrb = side == 0 ? (p.Nq + 31) / 32 : (p.Nk + 31) / 32;
+  const int blk = side == 0 ? (int)blockIdx.x : (int)blockIdx.x - nqb;
+  const int rb = blk % nrb, bh = blk / nrb;
   const int heads = side == 0 ? p.Hq : p.Hk;
   const int b = bh / heads, hh = bh % heads;
   const int R = p.R, D = p.D, EP = p.EP;
@@ -372,8 +381,9 @@ __global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p,
                          : p.dk + (int64_t)b * p.dk_s[0] + (int64_t)hh * p.dk_s[1];
   const int64_t os = side == 0 ? p.dq_s[2] : p.dk_s[2];
   const float2* tab = nullptr;
-  if (R) tab = side == 0 ? p.qtab + (int64_t)b * p.qt_sb + (int64_t)hh * p.qt_sh
-                         : p.ktab + (int64_t)b * p.kt_sb + (int64_t)hh * p.kt_sh;
+  if (R && (side == 0 ? p.qtab : p.ktab))
+    tab = side == 0 ? p.qtab + (int64_t)b * p.qt_sb + (int64_t)hh * p.qt_sh
+                    : p.ktab + (int64_t)b * p.kt_sb + (int64_t)hh * p.kt_sh;
   const float* ab = acc + (int64_t)bh * rows * EP;
   // a second partial sum (split reduction of the split-bf16 path), added when present
   const float* ab2 = acc2 ? acc2 + (int64_t)bh * rows * EP : nullptr;
@@ -389,7 +399,7 @@ __global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p,
       const float* arow2 = ab2 ? ab2 + (int64_t)n * EP : nullptr;
       if (d < R) {
         const int prow = side == 0 ? q_off + n : n;
-        const float2 cs = tab[(int64_t)prow * R + d];
+        const float2 cs = tab ? tab[(int64_t)prow * R + d] : sim_phase(p, side, b, hh, prow, d);
         const float xv = x[(int64_t)n * xs + d];
         const float uc = arow[d] + (arow2 ? arow2[d] : 0.f), us = arow[R + d] + (arow2 ? arow2[R + d] : 0.f);
         out[(int64_t)n * os + d] = sigmoid_f(xv) * (cs.x * uc + cs.y * us);
@@ -437,13 +447,10 @@ hipError_t launch_sim_bwd_ws(const SimParams& p, float* U, float* W, hipStream_t
 
 hipError_t launch_sim_finalize(const SimParams& p, const float* U, const float* U2, const float* W, const float* W2,
                                hipStream_t s) {
-  hipError_t e;
   const int nrq = (p.Nq + 31) / 32, nrk = (p.Nk + 31) / 32;
-  e = launch_named("sim_bwd_finalize_q", sim_bwd_finalize_kernel, dim3(nrq * p.B * p.Hq), dim3(kThreads), s, p,
-                   U, U2, 0, nrq);
-  if (e != hipSuccess) return e;
-  return launch_named("sim_bwd_finalize_k", sim_bwd_finalize_kernel, dim3(nrk * p.B * p.Hk), dim3(kThreads), s, p,
-                      W, W2, 1, nrk);
+  const int nqb = nrq * p.B * p.Hq;
+  return launch_named("sim_bwd_finalize", sim_bwd_finalize_kernel, dim3(nqb + nrk * p.B * p.Hk), dim3(kThreads), s,
+                      p, U, U2, W, W2, nqb);
 }
 
 }  // namespace pope

@@ -19,6 +19,7 @@
 // The chain rule of the polar transform then runs in sim.hip's finalize kernel on U and W.
 #include "pope_common.hpp"
 #include "pope_kernels.hpp"
+#include "sim_phase.hpp"
 
 namespace pope {
 
@@ -47,8 +48,9 @@ __device__ __forceinline__ f32x16 mfma3(u32x4 ah, u32x4 al, u32x4 bh, u32x4 bl, 
 }
 
 // Expanded 8 columns [e0, e0 + 8) of one row (zeros past the row count or past E); the same
-// transform as the fp32 path (sim.hip).
-__device__ __forceinline__ void expand_row8(const float* x, const float2* tab, int e0, int R, int E, bool valid,
+// transform as the fp32 path (sim.hip).  cs8: the (cos, sin) pairs of the rotated dims the
+// columns belong to (dims e0 .. e0 + 7 for cos columns, e0 - R .. for sin columns).
+__device__ __forceinline__ void expand_row8(const float* x, const float2* cs8, int e0, int R, int E, bool valid,
                                             float* out) {
   if (!valid || e0 >= E) {
 #pragma unroll
@@ -62,26 +64,30 @@ __device__ __forceinline__ void expand_row8(const float* x, const float2* tab, i
   const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
   if (is_cos || is_sin) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const float2 cs = tab[d0 + s];
-      out[s] = softplus_f(xv[s]) * (is_cos ? cs.x : cs.y);
-    }
+    for (int s = 0; s < 8; ++s) out[s] = softplus_f(xv[s]) * (is_cos ? cs8[s].x : cs8[s].y);
   } else {
 #pragma unroll
     for (int s = 0; s < 8; ++s) out[s] = xv[s];
   }
 }
 
-// One thread per (row, 8 expanded columns).  side 0: query rows of (b, h) (phase row
-// q_off + i, no bias); side 1: key rows of (b, hk) (phase fl(F_j + bias)).  transposed = 0:
-// planes (heads, NP, EP); 1: planes (heads, EP, NP), rows fastest over threads so that each
-// 2-byte store of a wave covers 64 consecutive rows.
-__global__ __launch_bounds__(kThreads) void sim_split_prep_kernel(SimParams p, SimSplit sp, int side, int transposed) {
+// Work items per row of the split planes: R / 8 rotated dim groups (each a cos and a sin chunk of
+// 8 columns, one phase evaluation for both), then one item per other 8-column chunk (pass-through
+// dims, zero padding up to EP).
+__host__ __device__ __forceinline__ int prep_items(int EP, int R) { return EP / 8 - R / 8; }
+
+// One thread per (row, item); blocks [0, nb0) take side 0 (query rows of (b, h), phase row
+// q_off + i, no bias), the rest side 1 (key rows of (b, hk), phase fl(F_j + bias)).  The phases
+// come from the tables when present, else are computed in place (sim_phase).
+// transposed = 0: planes (heads, NP, EP); 1: planes (heads, EP, NP), rows fastest over threads so
+// that each 2-byte store of a wave covers 64 consecutive rows.
+__global__ __launch_bounds__(kThreads) void sim_split_prep_kernel(SimParams p, SimSplit sp, int nb0, int transposed) {
+  const int side = (int)blockIdx.x < nb0 ? 0 : 1;
   const int heads = side == 0 ? p.B * p.Hq : p.B * p.Hk;
   const int N = side == 0 ? p.Nq : p.Nk, NP = side == 0 ? sp.NqP : sp.NkP;
-  const int nch = p.EP / 8;
+  const int R = p.R, nch = prep_items(p.EP, R);
   const int64_t total = (int64_t)heads * NP * nch;
-  const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t idx = (int64_t)(side == 0 ? blockIdx.x : blockIdx.x - nb0) * kThreads + threadIdx.x;
   if (idx >= total) return;
   int bh, n, ch;
   if (total < INT32_MAX) {   // the usual case: 32-bit index decomposition
@@ -108,36 +114,65 @@ __global__ __launch_bounds__(kThreads) void sim_split_prep_kernel(SimParams p, S
     n = (int)(r % NP);
     bh = (int)(r / NP);
   }
-  const int R = p.R, q_off = p.Nk - p.Nq;
+  const int q_off = p.Nk - p.Nq;
   const int nn = min(n, N - 1);
-  const float* x;
-  const float2* tab = nullptr;
-  if (side == 0) {
-    const int b = bh / p.Hq, h = bh % p.Hq;
-    x = p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + (int64_t)nn * p.q_s[2];
-    if (R) tab = p.qtab + (int64_t)b * p.qt_sb + (int64_t)h * p.qt_sh + (int64_t)(q_off + nn) * R;
-  } else {
-    const int b = bh / p.Hk, hk = bh % p.Hk;
-    x = p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1] + (int64_t)nn * p.k_s[2];
-    if (R) tab = p.ktab + (int64_t)b * p.kt_sb + (int64_t)hk * p.kt_sh + (int64_t)nn * R;
-  }
-  float v[8];
-  expand_row8(x, tab, 8 * ch, R, p.E, n < N, v);
-  u32x4 hi, lo;
-  split8(v, hi, lo);
+  const int hh = side == 0 ? bh % p.Hq : bh % p.Hk, b = side == 0 ? bh / p.Hq : bh / p.Hk;
+  const float* x = side == 0 ? p.q + (int64_t)b * p.q_s[0] + (int64_t)hh * p.q_s[1] + (int64_t)nn * p.q_s[2]
+                             : p.k + (int64_t)b * p.k_s[0] + (int64_t)hh * p.k_s[1] + (int64_t)nn * p.k_s[2];
   uint16_t* ph = side == 0 ? sp.qh : sp.kh;
   uint16_t* pl = side == 0 ? sp.ql : sp.kl;
-  if (!transposed) {
-    const int64_t o = ((int64_t)bh * NP + n) * p.EP + 8 * ch;
-    *reinterpret_cast<u32x4*>(ph + o) = hi;
-    *reinterpret_cast<u32x4*>(pl + o) = lo;
-  } else {
-    const int64_t o = ((int64_t)bh * p.EP + 8 * ch) * NP + n;
+  auto store = [&](int e0, const float* v) {   // split 8 columns [e0, e0 + 8) of the row
+    u32x4 hi, lo;
+    split8(v, hi, lo);
+    if (!transposed) {
+      const int64_t o = ((int64_t)bh * NP + n) * p.EP + e0;
+      *reinterpret_cast<u32x4*>(ph + o) = hi;
+      *reinterpret_cast<u32x4*>(pl + o) = lo;
+    } else {
+      const int64_t o = ((int64_t)bh * p.EP + e0) * NP + n;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      ph[o + (int64_t)s * NP] = (uint16_t)((s & 1) ? hi[s >> 1] >> 16 : hi[s >> 1] & 0xffffu);
-      pl[o + (int64_t)s * NP] = (uint16_t)((s & 1) ? lo[s >> 1] >> 16 : lo[s >> 1] & 0xffffu);
+      for (int s = 0; s < 8; ++s) {
+        ph[o + (int64_t)s * NP] = (uint16_t)((s & 1) ? hi[s >> 1] >> 16 : hi[s >> 1] & 0xffffu);
+        pl[o + (int64_t)s * NP] = (uint16_t)((s & 1) ? lo[s >> 1] >> 16 : lo[s >> 1] & 0xffffu);
+      }
     }
+  };
+  if (8 * ch < R) {   // rotated dims d0 .. d0 + 7: cos chunk at column d0, sin chunk at R + d0
+    const int d0 = 8 * ch;
+    float vc[8], vs[8];
+    if (n < N) {
+      const int prow = side == 0 ? q_off + nn : nn;
+      float2 cs8[8];
+      const float2* tab = side == 0 ? p.qtab : p.ktab;
+      if (tab) {
+        const float2* t = tab + (int64_t)b * (side == 0 ? p.qt_sb : p.kt_sb) +
+                          (int64_t)hh * (side == 0 ? p.qt_sh : p.kt_sh) + (int64_t)prow * R + d0;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) cs8[s] = t[s];
+      } else {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) cs8[s] = sim_phase(p, side, b, hh, prow, d0 + s);
+      }
+      const float4 x0 = *reinterpret_cast<const float4*>(x + d0);
+      const float4 x1 = *reinterpret_cast<const float4*>(x + d0 + 4);
+      const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const float a = softplus_f(xv[s]);
+        vc[s] = a * cs8[s].x;
+        vs[s] = a * cs8[s].y;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) vc[s] = vs[s] = 0.f;
+    }
+    store(d0, vc);
+    store(R + d0, vs);
+  } else {            // pass-through dims (columns < E) or zero padding
+    const int e0 = 8 * ch + R;
+    float v[8];
+    expand_row8(x, nullptr, e0, R, p.E, n < N, v);
+    store(e0, v);
   }
 }
 
@@ -491,14 +526,14 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_w_kernel(SimParams p, S
 }  // namespace
 
 hipError_t launch_sim_split_prep(const SimParams& p, const SimSplit& sp, int transposed, hipStream_t s) {
+  int64_t blocks[2];
   for (int side = 0; side < 2; ++side) {
     const int heads = side == 0 ? p.B * p.Hq : p.B * p.Hk;
-    const int64_t total = (int64_t)heads * (side == 0 ? sp.NqP : sp.NkP) * (p.EP / 8);
-    const hipError_t e = launch_named("sim_split_prep", sim_split_prep_kernel, dim3((unsigned)((total + kThreads - 1) / kThreads)),
-                                      dim3(kThreads), s, p, sp, side, transposed);
-    if (e != hipSuccess) return e;
+    const int64_t total = (int64_t)heads * (side == 0 ? sp.NqP : sp.NkP) * prep_items(p.EP, p.R);
+    blocks[side] = (total + kThreads - 1) / kThreads;
   }
-  return hipSuccess;
+  return launch_named("sim_split_prep", sim_split_prep_kernel, dim3((unsigned)(blocks[0] + blocks[1])), dim3(kThreads),
+                      s, p, sp, (int)blocks[0], transposed);
 }
 
 hipError_t launch_sim_split_fwd(const SimParams& p, const SimSplit& sp, hipStream_t s) {
