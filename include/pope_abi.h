@@ -83,7 +83,12 @@ enum pope_flags {
  * f[b*f_s[0] + h*f_s[1] + n*f_s[2] + r] (0 strides broadcast); the key phase is
  * freqs[j] + bias, the query phase freqs[Nk - Nq + i] (right-aligned,
  * pope.py:64, triton_pope_flash_attn.py:54).  R == 0 means no PoPE (plain
- * attention / plain q k^T).  bias: (Hb, R) with Hb in {1, Hk}, row stride
+ * attention / plain q k^T).  D and R are multiples of 8 (rows move in 16-byte
+ * chunks); flash takes D <= 128, the similarity D <= 256.  The reference takes
+ * any D and R (triton_pope.py:58-60, triton_pope_flash_attn.py:44,252); other
+ * shapes are padded by the caller first: rotated dims with a value whose
+ * softplus is 0 (-1e4), pass-through dims, v, freqs and bias with zeros (the
+ * Python layer does this, pope_amd/_pad.py).  bias: (Hb, R) with Hb in {1, Hk}, row stride
  * bias_sh (0 when Hb == 1); it must already be clamped to [-2*pi, 0]
  * (pope.py:145).  mask: (B, Nk) bytes, nonzero = keep (attention.py:129-131).
  */
