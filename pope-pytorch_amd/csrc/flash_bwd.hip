@@ -379,6 +379,12 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
         s[r] = pv;
         dp[r] = pv * dp[r];
       }
+      // The two waves of a SIMD run this loop in step between the barriers, so their product
+      // bursts and their exponentials would coincide.  Raised priority for the dV / dK burst lets
+      // the wave that reaches it first keep the matrix pipe; the other wave's exponentials and
+      // packs then run beside it, and the two drift half a sub-tile apart (8-wave workgroups only:
+      // with one wave per SIMD there is nothing to arbitrate).
+      if constexpr (C::NW == 8) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int g2 = 0; g2 < 2; ++g2) {
         const vec8 ap = as_vec8<vec8>(pack8<T>(s, g2));
@@ -393,6 +399,7 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
           dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_tr8_at(qa.lo_at(eb) + 2 * r0 * EP, qa.hi_at(eb) + 2 * r0 * EP)),
                               dka[eb]);
       }
+      if constexpr (C::NW == 8) __builtin_amdgcn_s_setprio(0);
     }
   }
   __syncthreads();   // every wave is done with the slots
