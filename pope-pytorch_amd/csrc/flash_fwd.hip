@@ -331,6 +331,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
         __builtin_amdgcn_sched_group_barrier(kSchedValu, (6 * KB * 16 / 2) / (KB * KS), 0);
       }
+      // the packed probabilities are complete here, before the mask branch: otherwise their
+      // exponentials sink past it into the P V block, away from the score products they overlap
+#pragma unroll
+      for (int i = 0; i < 2 * KB; ++i) asm volatile("" : "+v"(pw[i]));
       if (!full) {
         POPE_COLD_PATH();
         apply_mask(t + 1, mb, nxt);
