@@ -117,7 +117,8 @@ class PoPE(Module):
             pos = pos_or_seq_len
         else:
             pos = torch.arange(pos_or_seq_len, device=self.device, dtype=self.inv_freqs.dtype)
-        pos = pos + offset
+        if is_tensor(offset) or offset != 0:   # adding an integer 0 would only copy pos (one launch)
+            pos = pos + offset
         freqs = pos.unsqueeze(-1) * self.inv_freqs          # '... i, j -> ... i j'
         bias = self.bias.clamp(-2.0 * pi, 0.0)
         return PolarEmbedReturn(freqs, bias)
