@@ -41,6 +41,13 @@ def test_pope_module_matches_closed_form():
     f3 = m(pos).freqs
     assert f3.shape == (2, 16, 32)
     torch.testing.assert_close(f3, orc.pope_freqs(pos, orc.inv_freqs(32)), rtol=0, atol=0)
+    # offsets: an explicit integer 0 (no add), a tensor offset, tensor positions shifted by an integer;
+    # the returned freqs never alias the positions passed in
+    torch.testing.assert_close(m(1024, offset=0).freqs, freqs, rtol=0, atol=0)
+    torch.testing.assert_close(m(1000, offset=torch.tensor(24.0)).freqs, freqs[24:], rtol=0, atol=0)
+    torch.testing.assert_close(m(pos, offset=3).freqs, orc.pope_freqs(pos + 3, orc.inv_freqs(32)), rtol=0, atol=0)
+    p1 = torch.arange(8).float()
+    assert m(p1).freqs.data_ptr() != p1.data_ptr()
     # the bias gradient passes where the clamp is inactive (and at its bounds)
     m.bias.grad = None
     m(8).bias.sum().backward()
