@@ -88,6 +88,23 @@ def apply_pope_to_qk(pope: PolarEmbedReturn, q: Tensor, k: Tensor, to_magnitude=
     return q, k
 
 
+class _ClampBias(torch.autograd.Function):
+    """bias.clamp(lo, hi) with the gradient of torch's clamp (passed where lo <= bias <= hi, bounds included;
+    zero outside and for NaN), in three launches per forward + backward instead of five: the forward saves
+    the keep mask (clamped == bias) and the backward is one multiply."""
+
+    @staticmethod
+    def forward(ctx, bias, lo, hi):
+        out = bias.clamp(lo, hi)
+        ctx.save_for_backward(out == bias)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        (keep,) = ctx.saved_tensors
+        return grad * keep, None, None
+
+
 class PoPE(Module):
     """Frequencies ``theta ** -(j / dim)`` for j < dim (pope.py:106-107) and a learned
     per-head key phase bias clamped to [-2 pi, 0] (pope.py:113,145)."""
@@ -120,5 +137,5 @@ class PoPE(Module):
         if is_tensor(offset) or offset != 0:   # adding an integer 0 would only copy pos (one launch)
             pos = pos + offset
         freqs = pos.unsqueeze(-1) * self.inv_freqs          # '... i, j -> ... i j'
-        bias = self.bias.clamp(-2.0 * pi, 0.0)
+        bias = _ClampBias.apply(self.bias, -2.0 * pi, 0.0) if self.bias.requires_grad else self.bias.clamp(-2.0 * pi, 0.0)
         return PolarEmbedReturn(freqs, bias)

@@ -16,7 +16,7 @@ from torch import Tensor
 from torch.amp import autocast
 from torch.nn import Module, Parameter, ParameterList
 
-from .pope import PolarEmbedReturn, apply_pope_to_qk
+from .pope import PolarEmbedReturn, _ClampBias, apply_pope_to_qk
 
 
 class AxialPoPE(Module):
@@ -57,5 +57,5 @@ class AxialPoPE(Module):
             pos = pos_or_dims
         assert pos.shape[-1] == len(self.axial_dims)
         freqs = torch.cat([pos[..., i, None] * inv for i, inv in enumerate(self.inv_freqs)], dim=-1)
-        bias = self.bias.clamp(-2.0 * pi, 0.0)
+        bias = _ClampBias.apply(self.bias, -2.0 * pi, 0.0) if self.bias.requires_grad else self.bias.clamp(-2.0 * pi, 0.0)
         return PolarEmbedReturn(freqs, bias)

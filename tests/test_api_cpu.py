@@ -55,6 +55,25 @@ def test_pope_module_matches_closed_form():
     assert torch.equal(m.bias.grad, inside.float())
 
 
+def test_bias_clamp_matches_torch_clamp():
+    """The modules' bias clamp (a fused-backward autograd function) against torch's clamp: values and
+    gradients at the exact bounds, inside, outside and for NaN, for PoPE and AxialPoPE."""
+    vals = torch.tensor([-7.0, -2 * math.pi, -3.0, 0.0, 0.5, float("nan"), -1.0, 2.0])
+    g = torch.randn(4, 16, generator=torch.Generator().manual_seed(5))
+    for m in (pope_amd.PoPE(16, heads=4), pope_amd.AxialPoPE(16, heads=4, axial_dims=(8, 8))):
+        with torch.no_grad():
+            m.bias.copy_(vals.repeat(8).view(4, 16))
+        ref = m.bias.detach().clone().requires_grad_(True)
+        out = m(8).bias if isinstance(m, pope_amd.PoPE) else m((2, 4)).bias
+        (out * g).sum().backward()
+        want = ref.clamp(-2 * math.pi, 0.0)
+        (want * g).sum().backward()
+        assert torch.equal(torch.nan_to_num(out.detach(), 9.0), torch.nan_to_num(want.detach(), 9.0))
+        assert torch.equal(m.bias.grad, ref.grad)
+        # a planted mistake: a gradient blocked at the bounds must differ
+        assert not torch.equal(m.bias.grad, g * ((ref > -2 * math.pi) & (ref < 0)))
+
+
 def test_pope_state_dict_round_trip_and_options():
     src = pope_amd.PoPE(64, heads=4, bias_uniform_init=True)      # the reference raises here
     assert src.bias.min() >= -2 * math.pi and src.bias.max() <= 0 and src.bias.abs().sum() > 0
