@@ -84,7 +84,7 @@ enum pope_flags {
  * freqs[j] + bias, the query phase freqs[Nk - Nq + i] (right-aligned,
  * pope.py:64, triton_pope_flash_attn.py:54).  R == 0 means no PoPE (plain
  * attention / plain q k^T).  D and R are multiples of 8 (rows move in 16-byte
- * chunks); flash takes D <= 128, the similarity D <= 256.  The reference takes
+ * chunks); flash takes D <= 128, the similarity D <= 512.  The reference takes
  * any D and R (triton_pope.py:58-60, triton_pope_flash_attn.py:44,252); other
  * shapes are padded by the caller first: rotated dims with a value whose
  * softplus is 0 (-1e4), pass-through dims, v, freqs and bias with zeros (the

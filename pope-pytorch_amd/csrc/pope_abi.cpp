@@ -357,7 +357,7 @@ int check_sim_common(const pope_desc* d, const void* q, const void* k, const flo
   if (d->dtype != POPE_F32) return fail(POPE_ERR_UNSUPPORTED, "similarity kernels take fp32 (dtype %d)", d->dtype);
   if (d->flags & ~(POPE_FLAG_SPLIT_BF16 | POPE_FLAG_DETERMINISTIC))
     return fail(POPE_ERR_INVALID, "unknown flags 0x%x", (unsigned)d->flags);
-  if (d->D > 256) return fail(POPE_ERR_UNSUPPORTED, "similarity covers head dim <= 256 (got %d)", d->D);
+  if (d->D > 512) return fail(POPE_ERR_UNSUPPORTED, "similarity covers head dim <= 512 (got %d)", d->D);
   if (!q || !k) return fail(POPE_ERR_INVALID, "q, k must be non-NULL");
   if (!aligned16(q) || !aligned16(k)) return fail(POPE_ERR_INVALID, "q, k must be 16-byte aligned");
   if ((rc = check_strides32("q", d->q_s)) || (rc = check_strides32("k", d->k_s))) return rc;

@@ -86,6 +86,7 @@ def _compare(S, grads, S_ref, grads_ref, names=("dq", "dk", "dfreqs", "dbias")):
     (1, 4, 2, 100, 300, 64, 32),     # GQA, ragged, Nq < Nk
     (1, 2, 2, 64, 64, 256, 128),     # E = 384: several expanded-column chunks
     (1, 2, 2, 33, 33, 48, 16),       # D = 48
+    (1, 2, 1, 40, 72, 256, 253),     # D = 256 with a ragged rotate dim: padded to 264 wide
 ], ids=lambda c: "x".join(map(str, c)))
 @pytest.mark.parametrize("allow_tf32", [True, False], ids=["split_bf16", "fp32"])
 def test_similarity_multi_config(cuda, cfg, allow_tf32):
