@@ -80,8 +80,10 @@ def _attend_materialised(q, k, v, pos_emb, mask, causal, softmax_scale):
     if exists(pos_emb):
         q, k = apply_pope_to_qk(pos_emb, q, k, to_magnitude=F.softplus)
     groups = q.shape[1] // k.shape[1]
-    k, v = _repeat_heads(k, groups), _repeat_heads(v, groups)
+    # repeated after the fp32 conversion, so the group heads' dk / dv are summed in fp32 and
+    # rounded to the input dtype once
     qf, kf, vf = q.float(), k.float(), v.float()
+    kf, vf = _repeat_heads(kf, groups), _repeat_heads(vf, groups)
     s = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) * softmax_scale
     keep = _keep_mask(mask, causal, q.shape[-2], k.shape[-2], q.device)
     if exists(keep):

@@ -96,6 +96,7 @@ def test_reference_operator_api_dims_not_multiple_of_8(cuda):
 @pytest.mark.parametrize("cfg", [
     (1, 2, 1, 96, 96, 160, 32, True, "prefix"),
     (1, 2, 2, 64, 64, 256, 64, False, "none"),
+    (2, 8, 1, 59, 60, 129, 88, True, "none"),   # 8 query heads per kv head: dv summed over the group in fp32
 ], ids=lambda c: "x".join(map(str, c)))
 def test_flash_heads_wider_than_kernels(cuda, cfg):
     *shape, causal, mask = cfg
