@@ -800,11 +800,16 @@ __global__ __launch_bounds__((BwdCfg<EP, DV>::THREADS), 1) void bwd_main_kernel(
   if (p.interleave) {
     // pairs of equal cost, heaviest first: dK/dV block r with dQ block nqb - 1 - r; the
     // batch * head index is fastest so that one head's jobs share an XCD (workgroup ids are
-    // dealt round-robin over the 8 XCDs)
+    // dealt round-robin over the 8 XCDs).  Workgroups are dispatched in id order, and inside an
+    // XCD the ids go round-robin to its shader engines: with the kind fixed by one id bit, each
+    // engine held jobs of one kind only, the dQ engines' CUs finished their first jobs 30 us
+    // earlier and then waited, because the next id in line belonged to a dK/dV engine without a
+    // free CU.  The kind therefore flips with the parity of the head index and of the level, so
+    // that every run of ids mixes both kinds.
     const int BH = p.B * p.Hq;
     const int r = id / (2 * BH), rem = id % (2 * BH);
-    kind = rem / BH;
     head = rem % BH;
+    kind = (rem / BH) ^ (__builtin_popcount(head) & 1) ^ (r & 1);
     blk = kind == 0 ? r : nqb - 1 - r;
   } else if (id < p.n_kv_jobs) {
     const int BHk = p.B * p.Hk;
