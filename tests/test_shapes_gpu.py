@@ -104,7 +104,7 @@ def test_flash_heads_wider_than_kernels(cuda, cfg):
     _check(_api(inp, causal), oracle_attention(inp, causal), ALL)
 
 
-@pytest.mark.parametrize("D,R", [(20, 12), (44, 3), (24, 0)])
+@pytest.mark.parametrize("D,R", [(20, 12), (44, 3), (24, 0), (300, 37), (512, 256)])   # the C ABI takes D <= 512
 @pytest.mark.parametrize("allow_tf32", [True, False], ids=["split_bf16", "fp32"])
 def test_similarity_dims_not_multiple_of_8(cuda, D, R, allow_tf32):
     from pope_amd.hip_pope import hip_compute_qk_similarity
