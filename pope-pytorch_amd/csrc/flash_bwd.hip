@@ -29,8 +29,8 @@
 //   bwd_main   : one launch holding two kinds of jobs, one per workgroup
 //     dK/dV job: 32 keys per wave (256 keys in 8 waves when D + R and D are small,
 //                128 in 4 waves otherwise) of one (batch, kv head); loops over the
-//                query heads of its group and the query steps (128 or 64 rows)
-//                that can see its keys (steps before the causal diagonal are
+//                query heads of its group and the query steps (128 rows; 64 for
+//                the widest rows) that can see its keys (steps before the causal diagonal are
 //                skipped); the epilogue applies the key-side chain rule and sums
 //                dbias.
 //     dQ job   : 32 queries per wave, the same job sizes; loops over the key
@@ -40,8 +40,9 @@
 //                input dtype, triton_pope_flash_attn.py:215).
 //   Causal dK/dV job r and dQ job (blocks - 1 - r) cost the same; the launch
 //   orders the pairs heaviest first, so the triangle's work balances over the
-//   CUs.  Streamed tiles go straight from global memory into a ring of three LDS
-//   slots (global_load_lds_dwordx4), two steps ahead of the step computed.
+//   CUs.  Streamed tiles go straight from global memory into a ring of LDS slots
+//   (global_load_lds_dwordx4): three slots, two steps ahead of the step computed, or,
+//   for wide rows whose 128-row slots only fit twice, two slots one step ahead.
 //   The row terms enter the MFMAs as initial accumulators: the score product
 //   starts from -lse (so it returns s - lse and P = exp2 of it) and dO V^T from
 //   -delta (so it returns dP - delta).
@@ -60,8 +61,6 @@
 namespace pope {
 
 namespace {
-
-constexpr int kSlots = 3;
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
@@ -177,12 +176,16 @@ template <int EP, int DV>
 struct BwdCfg {
   // Small rows: 8 waves (256 keys per dK/dV job, 256 queries per dQ job) and 128-row steps, one
   // workgroup per CU (two waves per SIMD).  Wide rows need up to 512 registers per lane: 4 waves,
-  // one per SIMD, 64-row steps.
+  // one per SIMD; 128-row steps in a two-slot ring where two such slots fit (C4's E = 192, D = 96:
+  // 326 against 331 us with 64-row steps in three slots), else 64-row steps in three.
   static constexpr bool kBig = EP + DV > 160;
   static constexpr int NW = kBig ? 4 : 8;                    // waves per workgroup
   static constexpr int THREADS = 64 * NW;
   static constexpr int JOB = 32 * NW;                        // keys (dK/dV) or queries (dQ) per job
-  static constexpr int BM = kBig ? 64 : 128;                 // query rows per dK/dV step, keys per dQ step
+  // wide rows: 128-row steps in a two-slot ring when two such slots fit the LDS, else 64-row steps in three
+  static constexpr bool kWide128 = kBig && 2 * ((128 * EP + 128 * DV) * 2 + 64 * 16) <= 150 * 1024;
+  static constexpr int BM = (kBig && !kWide128) ? 64 : 128;  // query rows per dK/dV step, keys per dQ step
+  static constexpr int SLOTS = kWide128 ? 2 : 3;
   static constexpr int KS = EP / 16, DS = DV / 16, EB = EP / 32, DB = DV / 32;
   static constexpr int EPU = EP / 8, DVU = DV / 8;
   static constexpr int XT = BM * EP, YT = BM * DV;            // elements of the two tiles of a slot
@@ -196,7 +199,7 @@ struct BwdCfg {
   static constexpr int KV_LMIN = (KV_UNITS - (THREADS - 64) + THREADS - 1) / THREADS;   // loads of the last wave
   static constexpr int Q_LMIN = (Q_UNITS - (THREADS - 64) + THREADS - 1) / THREADS;
   static constexpr int EPI = 32 * (EP + 1) * 4;
-  static constexpr int LDS = kSlots * SLOT > EPI ? kSlots * SLOT : EPI;
+  static constexpr int LDS = SLOTS * SLOT > EPI ? SLOTS * SLOT : EPI;
   static_assert(XU % 64 == 0 && YU % 64 == 0, "tile regions must split at wave boundaries");
   static_assert(LDS <= 160 * 1024, "LDS budget");
 };
@@ -292,7 +295,7 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
   const int do_last = (Nq - 1) * do_rs + D - 8;   // start of the last chunk of the last row
   auto issue = [&](int st) {
     const int g = st / per_head, i0 = (qt0 + st % per_head) * BM;
-    char* slot = smem + (st % kSlots) * C::SLOT;
+    char* slot = smem + (st % C::SLOTS) * C::SLOT;
     const uint16_t* qg = qh_job + g * qh_hstride + (int64_t)i0 * EP;
     const uint16_t* dg = do_job + g * do_hstride;
     const float* lg = nl_job + g * nl_hstride + i0;
@@ -321,16 +324,21 @@ __device__ __forceinline__ void dkdv_job(const FlashBwdParams& p, char* smem, fl
   const TileOffsets<EPU> qo(lane);
   const TileOffsets<DVU> doo(lane);
 
+  constexpr int PD = C::SLOTS - 1;   // steps in flight ahead of the one computed
   if (nsteps > 0) issue(0);
-  if (nsteps > 1) issue(1);
+  if (PD > 1 && nsteps > 1) issue(1);
   for (int st = 0; st < nsteps; ++st) {
-    if (st + 1 < nsteps) wait_vmcnt<C::KV_LMIN>();   // this thread's loads of step st landed
-    else wait_vmcnt<0>();
+    if constexpr (PD > 1) {
+      if (st + 1 < nsteps) wait_vmcnt<C::KV_LMIN>();   // this thread's loads of step st landed
+      else wait_vmcnt<0>();
+    } else {
+      wait_vmcnt<0>();
+    }
     __syncthreads();                                // ... everyone's; step st - 1's slot is free
-    if (st + 2 < nsteps) issue(st + 2);
+    if (st + PD < nsteps) issue(st + PD);
     const int i0 = (qt0 + st % per_head) * BM;
     // byte addresses in the step's slot: Q_hat tile | dO tile | -lse rows | -delta rows
-    const uint32_t sb = lds_addr(smem + (st % kSlots) * C::SLOT);
+    const uint32_t sb = lds_addr(smem + (st % C::SLOTS) * C::SLOT);
     const TileAddr<EPU> qa(qo, sb);
     const TileAddr<DVU> da(doo, sb + 2 * C::XT);
     const uint32_t nla = opaque_u32(sb + 2 * (C::XT + C::YT) + 16 * hf);
@@ -597,7 +605,7 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
   const int v_last = (Nk - 1) * vs2 + D - 8;   // start of the last chunk of the last row
   auto issue = [&](int kt) {
     const int j0 = kt * BN;
-    char* slot = smem + (kt % kSlots) * C::SLOT;
+    char* slot = smem + (kt % C::SLOTS) * C::SLOT;
     const uint16_t* kg = kh_g + j0 * EP;   // K_hat rows are padded to NkP
     const int vrow0 = j0 * vs2;
 #pragma unroll
@@ -618,15 +626,20 @@ __device__ __forceinline__ void dq_job(const FlashBwdParams& p, char* smem, int 
   const TileOffsets<EPU> ko(lane);
   const TileOffsets<DVU> vo(lane);
 
+  constexpr int PD = C::SLOTS - 1;
   if (nt > 0) issue(0);
-  if (nt > 1) issue(1);
+  if (PD > 1 && nt > 1) issue(1);
   for (int kt = 0; kt < nt; ++kt) {
-    if (kt + 1 < nt) wait_vmcnt<C::Q_LMIN>();
-    else wait_vmcnt<0>();
+    if constexpr (PD > 1) {
+      if (kt + 1 < nt) wait_vmcnt<C::Q_LMIN>();
+      else wait_vmcnt<0>();
+    } else {
+      wait_vmcnt<0>();
+    }
     __syncthreads();
-    if (kt + 2 < nt) issue(kt + 2);
+    if (kt + PD < nt) issue(kt + PD);
     const int j0 = kt * BN;
-    const uint32_t sb = lds_addr(smem + (kt % kSlots) * C::SLOT);   // K_hat tile | V tile
+    const uint32_t sb = lds_addr(smem + (kt % C::SLOTS) * C::SLOT);   // K_hat tile | V tile
     const TileAddr<EPU> ka(ko, sb);
     const TileAddr<DVU> va(vo, sb + 2 * C::XT);
 #pragma unroll
