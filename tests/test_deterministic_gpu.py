@@ -45,6 +45,7 @@ FLASH_CASES = [
     (2, 4, 4, 384, 64, 32, True, "prefix", False, False),
     (2, 8, 2, 256, 64, 32, True, "random", False, True),
     (2, 2, 2, 300, 96, 96, False, "none", True, False),
+    (1, 2, 2, 520, 96, 64, True, "prefix", False, False),   # wide rows, causal: 128-row steps in two slots
 ]
 
 
