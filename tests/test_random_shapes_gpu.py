@@ -9,8 +9,8 @@ product paths) and the polar transform: ragged sizes, grouped heads, odd dims.
 
 Tolerances, as in the other GPU tests: flash and decode 2e-2 absolute beyond the rounding of the exact value to
 the output format (gpu_common.excess_over) for O, dq, dk, dv and 2e-2 * max(1, ||ref||_inf) for the summed dbias /
-dfreqs; the fp32 similarity 1e-4 relative to ||ref||_inf; the fp32 polar transform 1e-5 relative for outputs, dq,
-dk and 1e-4 for dfreqs / dbias.  The shapes stay where bf16 operand rounding keeps within the bf16 bound: head
+dfreqs; the fp32 similarity 1e-4 relative to ||ref||_inf; the fp32 polar transform 1e-5 + 2^-23 max|F + beta|
+relative (one ulp of the largest fp32 phase on top) for outputs, dq, dk and 1e-4 for dfreqs / dbias.  The shapes stay where bf16 operand rounding keeps within the bf16 bound: head
 dims of at least 8 (a softmax scale of at most 0.35; at D = 1 the logits reach 12 and rounding q_hat / k_hat to bf16
 alone moves them by 0.03), and at most 8 * 700 query rows summed into one dk element.
 """
@@ -87,10 +87,10 @@ def _cid(c):
     return "-".join(f"{k}{str(v).replace('torch.', '')}" for k, v in c.items() if k != "seed")
 
 
-FLASH = [_flash_case(i) for i in range(40)]
-DECODE = [_decode_case(i) for i in range(16)]
-SIM = [_sim_case(i) for i in range(16)]
-POLAR = [_polar_case(i) for i in range(16)]
+FLASH = [_flash_case(i) for i in range(200)]
+DECODE = [_decode_case(i) for i in range(64)]
+SIM = [_sim_case(i) for i in range(64)]
+POLAR = [_polar_case(i) for i in range(64)]
 
 
 def _batch_freqs(B, N, R, seed):
@@ -200,8 +200,12 @@ def test_random_polar(cuda, c):
     r = [x.double().requires_grad_(True) for x in (q, k, freqs, bias)]
     qr, kr = orc.apply_pope_to_qk(r[2], r[3], r[0], r[1])
     ((qr * gq.double()).sum() + (kr * gk.double()).sum()).backward()
-    for n, a, b, tol in (("q_hat", qh, qr, 1e-5), ("k_hat", kh, kr, 1e-5), ("dq", t[0].grad, r[0].grad, 1e-5),
-                         ("dk", t[1].grad, r[1].grad, 1e-5), ("dfreqs", t[2].grad, r[2].grad, 1e-4),
+    # an fp32 phase F + beta carries up to one ulp of itself (2^-23 |F + beta|) of error before its cos / sin, as
+    # the reference's own fp32 `freqs + bias` does; the float64 oracle has none, so the bound on the outputs and
+    # on dq / dk grows with the largest phase
+    ph = 1e-5 + 2.0 ** -23 * (freqs.abs().max().item() + bias.abs().max().item())
+    for n, a, b, tol in (("q_hat", qh, qr, ph), ("k_hat", kh, kr, ph), ("dq", t[0].grad, r[0].grad, ph),
+                         ("dk", t[1].grad, r[1].grad, ph), ("dfreqs", t[2].grad, r[2].grad, 1e-4),
                          ("dbias", t[3].grad, r[3].grad, 1e-4)):
         rel = max_abs(a, b) / max(1e-30, b.abs().max().item())
         print(f"{n}={rel:.1e}", end=" ")
