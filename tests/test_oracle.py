@@ -93,6 +93,88 @@ def test_axial_grid_reversed_order_and_shapes():
     assert orc.axial_freqs(orc.axial_grid_positions(32, 32), orc.axial_inv_freqs((32, 32))).shape == (1024, 64)
 
 
+# ---- axial tables against closed forms, and mistakes planted in copies of them ----
+
+def _axial_closed_form(dims, axial_dims):
+    """Float64 table built from scalars alone (pope_nd.py:48-52,65-68,84-100): token n of the
+    row-major grid ``dims`` has coordinates (c_0, ..., c_{k-1}) with the last axis fastest;
+    column block i holds the coordinate of axis k-1-i times 10000 ** -(j / axial_dims[i])."""
+    k = len(dims)
+    ntok = int(np.prod(dims))
+    width = sum(axial_dims)
+    out = np.zeros((ntok, width))
+    for n in range(ntok):
+        coords, rem = [0] * k, n
+        for ax in reversed(range(k)):
+            coords[ax], rem = rem % dims[ax], rem // dims[ax]
+        col = 0
+        for i, d in enumerate(axial_dims):
+            p = coords[k - 1 - i]
+            for j in range(d):
+                out[n, col] = p * 10000.0 ** (-j / d)
+                col += 1
+    return out
+
+
+# (grid, per-axis widths): unequal widths so that a denominator of sum(widths) or of another axis's
+# width changes every block but the first entry; distinct grid sizes so that a wrong axis shows
+AXIAL_PIN_CASES = [((3, 5, 7), (4, 2, 8)), ((8, 16, 16), (32, 32, 32)), ((6, 10), (8, 16)), ((9,), (12,))]
+
+
+def _check_axial(inv_fn, grid_fn, freqs_fn):
+    # fp32 pow: a few ulp (2^-23 = 1.2e-7) of relative error; every planted mistake is off by > 1e-2
+    # per-axis inverse frequencies at widths where 10000 ** -(j / d) has short decimal forms
+    exact = {1: [1.0], 2: [1.0, 1e-2], 4: [1.0, 1e-1, 1e-2, 1e-3], 8: [10.0 ** (-j / 2) for j in range(8)]}
+    invs = inv_fn(tuple(exact))
+    for inv, (d, want) in zip(invs, exact.items()):
+        np.testing.assert_allclose(inv.double().numpy(), want, rtol=5e-7, atol=0)
+    for dims, axial_dims in AXIAL_PIN_CASES:
+        invs = inv_fn(axial_dims)
+        for inv, d in zip(invs, axial_dims):
+            np.testing.assert_allclose(inv.double().numpy(), 10000.0 ** (-np.arange(d) / d), rtol=5e-7, atol=0)
+        got = freqs_fn(grid_fn(*dims), invs)
+        np.testing.assert_allclose(got.double().numpy(), _axial_closed_form(dims, axial_dims),
+                                   rtol=1e-6, atol=0)
+
+
+def test_axial_tables_match_closed_form():
+    """Every per-axis inverse frequency and every column block of the axial table, against
+    float64 values computed from scalars (not from the oracle's own tensors)."""
+    _check_axial(orc.axial_inv_freqs, orc.axial_grid_positions, orc.axial_freqs)
+
+
+def _mutant_axial(kind):
+    def inv_fn(axial_dims):
+        if kind == "denominator_sum":
+            s = sum(axial_dims)
+            return [10000.0 ** -(torch.arange(d).float() / s) for d in axial_dims]
+        if kind == "arange_step_two":                     # RoPE's arange(0, d, 2) / d, repeated
+            return [(10000.0 ** -(torch.arange(0, d, 2).float() / d)).repeat_interleave(2)[:d]
+                    for d in axial_dims]
+        return orc.axial_inv_freqs(axial_dims)
+
+    def grid_fn(*dims):
+        if kind == "grid_not_reversed":
+            grid = torch.meshgrid(*[torch.arange(d).float() for d in dims], indexing="ij")
+            return torch.stack([g.flatten() for g in grid], dim=-1)
+        return orc.axial_grid_positions(*dims)
+
+    def freqs_fn(pos, invs):
+        if kind == "first_axis_everywhere":
+            return torch.cat([pos[..., 0, None] * inv for inv in invs], dim=-1)
+        if kind == "blocks_reversed":
+            return torch.cat([pos[..., i, None] * inv for i, inv in reversed(list(enumerate(invs)))], dim=-1)
+        return orc.axial_freqs(pos, invs)
+    return inv_fn, grid_fn, freqs_fn
+
+
+@pytest.mark.parametrize("kind", ["denominator_sum", "arange_step_two", "grid_not_reversed",
+                                  "first_axis_everywhere", "blocks_reversed"])
+def test_planted_axial_mistakes_are_caught(kind):
+    with pytest.raises(AssertionError):
+        _check_axial(*_mutant_axial(kind))
+
+
 @pytest.mark.parametrize("partial", [False, True])
 def test_transform_layout_and_shapes(partial):
     torch.manual_seed(0)
