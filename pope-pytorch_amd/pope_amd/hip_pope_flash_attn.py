@@ -51,7 +51,8 @@ def _freqs_strides(freqs: Tensor, head_first: bool = True) -> tuple:
     2-D (N, R): shared; 3-D (B, N, R): per batch; 4-D: (B, H, N, R) head-first
     or (B, N, H, R) when the caller works in (batch, seq, heads) layout
     (triton_pope_flash_attn.py:237-245)."""
-    s = freqs.stride()
+    # a batch or head extent of 1 broadcasts: stride 0, so the library sees one shared table
+    s = [0 if n == 1 else st for n, st in zip(freqs.shape, freqs.stride())]
     if freqs.ndim == 2:
         return (0, 0, s[0])
     if freqs.ndim == 3:
@@ -66,8 +67,12 @@ def _prep_pope(freqs: Optional[Tensor], bias: Optional[Tensor]):
         return None, None
     if freqs.dtype != torch.float32:
         freqs = freqs.float()
-    if freqs.stride(-1) != 1:
-        freqs = freqs.contiguous()
+    # rows of 16-byte vectors: unit feature stride, row / batch / head strides and the view's
+    # offset in whole 4-float units (storage_offset, not data_ptr, so fake tensors decide alike)
+    # (rotate dims that are not multiples of 8 are padded into a fresh table later)
+    if freqs.stride(-1) != 1 or (freqs.shape[-1] % 8 == 0 and (
+            freqs.storage_offset() % 4 or any(s % 4 for s in freqs.stride()[:-1]))):
+        freqs = freqs.clone(memory_format=torch.contiguous_format)
     if bias.dtype != torch.float32:
         bias = bias.float()
     if bias.ndim == 1:
@@ -142,6 +147,25 @@ def _check_dtypes(q, *others):
             raise TypeError(f"pope_amd flash: operand of dtype {t.dtype} next to q of dtype {q.dtype}")
 
 
+_FP16_MAX = 65504.0
+
+
+def _check_fp16_range(*ts):
+    """fp32 flash inputs run on fp16 operands: a finite value beyond fp16's range would become inf
+    silently, so such inputs raise instead.  The check reads one flag back to the host (fp32 flash
+    is the compatibility path; the bf16 / fp16 paths never synchronise); under torch.compile
+    tracing it is skipped."""
+    if torch.compiler.is_compiling():
+        return
+    bad = torch.zeros((), dtype=torch.bool, device=ts[0].device)
+    for t in ts:
+        bad |= ((t.abs() > _FP16_MAX) & t.isfinite()).any()
+    if bool(bad):
+        raise ValueError("pope_amd flash: fp32 q / k / v run on fp16 operands (10-bit mantissa, as the "
+                         "reference's TF32 products) and must stay within fp16's range |x| <= 65504; "
+                         "scale the inputs or pass bf16")
+
+
 _INT32_MAX = 2 ** 31 - 1
 _DECODE_QUERY_WORDS = 4096   # decode_max_query_words() of the library
 
@@ -156,12 +180,10 @@ def _decode_eligible(q, k, v, freqs, causal) -> bool:
     R = freqs.shape[-1] if exists(freqs) else 0
     if Nq != 1 or causal or Nk < 1024 or D > 128:
         return False
-    if exists(freqs) and freqs.ndim == 4 and freqs.shape[1] > 1:
-        return False   # per-head phase tables: the general forward covers them
     if Hq * D > _DECODE_QUERY_WORDS:
         return False   # the kernel stages Hq * D query weights in LDS
-    if R and (freqs.data_ptr() % 16 or any(s % 4 for s in freqs.stride()[:-1])):
-        return False   # freqs rows are read as 16-byte vectors
+    if R and (_freqs_strides(freqs)[1] != 0 or any(st % 4 for st in _freqs_strides(freqs))):
+        return False   # per-head tables, or rows that are not whole 16-byte vectors
     return (Nk - 1) * max(k.stride(2), v.stride(2)) + D < _INT32_MAX
 
 
@@ -198,13 +220,24 @@ def _data(t):
     return None if t is None else t.data_ptr()
 
 
+def _fwd_ws_bytes(d, deterministic: int) -> int:
+    """The forward's workspace: the preparation the backward reuses and, under deterministic mode,
+    the backward's phase-derivative region after it, so that the backward takes the buffer as is."""
+    if not deterministic:
+        return _lib.workspace_bytes(_lib.OP_FLASH_FWD, d)
+    dd = _lib.PopeDesc.from_buffer_copy(d)
+    dd.flags = deterministic
+    return _lib.workspace_bytes(_lib.OP_FLASH_BWD, dd)
+
+
 def _fwd_impl(q, k, v, freqs, bias, mask, causal, softmax_scale):
     q, k, v = _unit_feature(q), _unit_feature(k), _unit_feature(v)
     o = torch.empty_like(q)
     lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
     _check_views(q, k, v, mask)
-    key = ("fwd", q.shape, q.stride(), k.shape, k.stride(), v.shape, v.stride(), o.stride(), q.dtype,
-           k.dtype, v.dtype, causal, softmax_scale, _opt_key(freqs), _opt_key(bias), _opt_key(mask))
+    deterministic = _lib.deterministic_flag()
+    key = ("fwd", deterministic, q.shape, q.stride(), k.shape, k.stride(), v.shape, v.stride(), o.stride(),
+           q.dtype, k.dtype, v.dtype, causal, softmax_scale, _opt_key(freqs), _opt_key(bias), _opt_key(mask))
 
     def build():
         _check_dtypes(q, k, v)
@@ -217,7 +250,7 @@ def _fwd_impl(q, k, v, freqs, bias, mask, causal, softmax_scale):
         # one non-causal query row against a long cache: the split-K decode kernel
         decode = _decode_eligible(q, k, v, freqs, causal)
         dec_bytes = _lib.workspace_bytes(_lib.OP_FLASH_DECODE, d) if decode else -1
-        return d, dec_bytes, _lib.workspace_bytes(_lib.OP_FLASH_FWD, d)
+        return d, dec_bytes, _fwd_ws_bytes(d, deterministic)
 
     d, dec_bytes, fwd_bytes = _plan(key, build)
     L = _lib.lib()
@@ -225,6 +258,13 @@ def _fwd_impl(q, k, v, freqs, bias, mask, causal, softmax_scale):
             o.data_ptr(), lse.data_ptr())
     stream = _stream(q)
     if dec_bytes >= 0:
+        if exists(freqs) and freqs.data_ptr() % 16:
+            # a table in memory torch did not allocate (its base is not 16-byte aligned): run on an
+            # aligned dense copy, with a descriptor for the copy's strides
+            freqs = freqs.clone(memory_format=torch.contiguous_format)
+            args = args[:3] + (freqs.data_ptr(),) + args[4:]
+            d = _lib.PopeDesc.from_buffer_copy(d)
+            d.f_s[:] = _freqs_strides(freqs)
         dws = torch.empty(dec_bytes, dtype=torch.uint8, device=q.device) if dec_bytes else None
         _lib.check(L.pope_flash_decode(ctypes.byref(d), *args, _data(dws), dec_bytes, stream), "flash decode")
         return o, lse, q.new_empty(0, dtype=torch.uint8)
@@ -232,6 +272,10 @@ def _fwd_impl(q, k, v, freqs, bias, mask, causal, softmax_scale):
     ws = torch.empty(fwd_bytes, dtype=torch.uint8, device=q.device)
     _lib.check(L.pope_flash_fwd(ctypes.byref(d), *args, ws.data_ptr(), fwd_bytes, stream), "flash forward")
     return o, lse, ws
+
+
+# whether the last backward reused its forward's preparation (read by tests)
+_LAST_BWD_PREPARED = False
 
 
 def _bwd_impl(do, q, k, v, o, lse, freqs, bias, mask, causal, softmax_scale, need_dfreqs, need_dbias,
@@ -276,7 +320,9 @@ def _bwd_impl(do, q, k, v, o, lse, freqs, bias, mask, causal, softmax_scale, nee
         return d, dp, _lib.workspace_bytes(_lib.OP_FLASH_BWD, d)
 
     d, dprep, need = _plan(key, build)
-    if exists(fwd_ws) and fwd_ws.numel() == need:
+    global _LAST_BWD_PREPARED
+    _LAST_BWD_PREPARED = exists(fwd_ws) and fwd_ws.numel() == need
+    if _LAST_BWD_PREPARED:
         ws, d = fwd_ws, dprep
     else:
         ws = torch.empty(need, dtype=torch.uint8, device=q.device)
@@ -305,7 +351,7 @@ def _(q, k, v, freqs, bias, mask, causal, softmax_scale):
     if _decode_eligible(q, k, v, freqs, causal):
         n = 0   # the decode kernel keeps nothing for the backward
     else:
-        n = _lib.workspace_bytes(_lib.OP_FLASH_FWD, _desc(q, k, freqs, bias, causal, softmax_scale))
+        n = _fwd_ws_bytes(_desc(q, k, freqs, bias, causal, softmax_scale), _lib.deterministic_flag())
     return torch.empty_like(q), q.new_empty(q.shape[:3], dtype=torch.float32), q.new_empty(n, dtype=torch.uint8)
 
 
@@ -388,7 +434,8 @@ def flash_attn_head_first(q: Tensor, k: Tensor, v: Tensor, freqs: Optional[Tenso
     out_dtype = q.dtype
     if q.dtype not in _MFMA_DTYPES:
         # fp32 inputs: fp16 operands keep 10 significant bits, as the TF32 products of the
-        # reference's fp32 path do (triton_pope_flash_attn.py:80); |x| must stay below 65504
+        # reference's fp32 path do (triton_pope_flash_attn.py:80), but not TF32's exponent range
+        _check_fp16_range(q, k, v)
         q, k, v = q.to(torch.float16), k.to(torch.float16), v.to(torch.float16)
     if k.dtype != q.dtype:
         k = k.to(q.dtype)

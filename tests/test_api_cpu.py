@@ -237,3 +237,32 @@ def test_format_aware_bound_helper():
     small = torch.rand(4096, dtype=torch.float64) * 0.5 + 0.5
     assert excess_over((small + 0.03).to(torch.bfloat16), small, 2e-2) > 0
     assert excess_over(small.float(), small, 0.0) <= 1e-7
+
+
+def test_flash_host_predicates_use_shapes_not_pointers():
+    """The decode choice and the freqs strides the library sees depend on shapes, strides and
+    storage offsets only (so the fake implementation decides as the real one does): extents of 1
+    broadcast with stride 0, per-head tables and rows that are not whole 16-byte vectors leave the
+    decode kernel, and tables whose view starts mid-vector are copied before any kernel sees them."""
+    from pope_amd import hip_pope_flash_attn as fa
+    B, H, Nk, D, R = 2, 4, 2048, 64, 64
+    q, k = torch.zeros(B, H, 1, D), torch.zeros(B, H, Nk, D)
+    F = torch.zeros(Nk, R)
+    assert fa._freqs_strides(F) == (0, 0, R)
+    assert fa._freqs_strides(F[None]) == (0, 0, R)                       # (1, N, R): one table
+    assert fa._freqs_strides(torch.zeros(B, 1, Nk, R)) == (Nk * R, 0, R)  # (B, 1, N, R): per batch
+    assert fa._freqs_strides(torch.zeros(B, Nk, 1, R), head_first=False) == (Nk * R, 0, R)
+    assert fa._decode_eligible(q, k, k, F, False)
+    assert fa._decode_eligible(q, k, k, torch.zeros(B, 1, Nk, R), False)
+    assert not fa._decode_eligible(q, k, k, torch.zeros(B, H, Nk, R), False)      # per-head table
+    assert not fa._decode_eligible(q, k, k, torch.zeros(Nk, R + 2)[:, :R], False)  # rows of 66 floats
+    assert not fa._decode_eligible(q, k, k, F, True)
+    # a view starting one float into its storage is copied; a whole-vector offset is kept
+    flat = torch.zeros(Nk * R + 4)
+    odd = flat[1:1 + Nk * R].view(Nk, R)
+    even = flat[4:].view(Nk, R)
+    bias = torch.zeros(H, R)
+    f_odd, _ = fa._prep_pope(odd, bias)
+    f_even, _ = fa._prep_pope(even, bias)
+    assert f_odd.storage_offset() == 0 and f_odd.data_ptr() != odd.data_ptr()
+    assert f_even.data_ptr() == even.data_ptr()

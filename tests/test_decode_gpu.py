@@ -113,3 +113,52 @@ def test_decode_backward(cuda):
         t = TOL * (max(1.0, ref[n].abs().max().item()) if n == "dbias" else 1.0)
         print(f"{n}={e:.2e}")
         assert e <= t, n
+
+
+@pytest.mark.parametrize("view", ["offset_rows", "batch_one", "heads_one", "odd_offset"])
+def test_decode_freqs_views(cuda, view):
+    """freqs tables that are views the decode kernel cannot read as given: rows starting past the
+    table's first element (a KV-cache continuation), a (1, N, R) table broadcast over the batch,
+    a (B, N, 1, R) table with one head, and a view whose start is not a whole 16-byte vector.
+    Each must give the oracle's result (the kernel choice may differ, the result may not)."""
+    import pope_amd
+    B, H, Nk, D, R = 2, 4, 2048, 64, 64
+    inp = _decode_inputs(61, B, H, H, Nk, D, R, torch.bfloat16)
+    F = inp["freqs"]
+    if view == "offset_rows":
+        big = orc_freqs(Nk + 100, R).to("cuda")
+        fv = big[100:]
+        want = big[100:].cpu()
+    elif view == "batch_one":
+        fv = F[None]
+        want = F.cpu()
+    elif view == "heads_one":
+        fv = F[None, None].expand(B, 1, Nk, R).contiguous()      # (B, H = 1, N, R), head-first
+        want = F.cpu()
+    else:
+        flat = torch.zeros(Nk * R + 1, device="cuda")
+        flat[1:] = F.reshape(-1)
+        fv = flat[1:].view(Nk, R)
+        want = F.cpu()
+    ref_inp = dict(inp, freqs=want.to("cuda"))
+    ref = oracle_attention(ref_inp, False, grads=False)
+    o = pope_amd.flash_attn_with_pope(inp["q"], inp["k"], inp["v"], pos_emb=(fv, inp["bias"]), mask=inp["mask"])
+    err = max_abs(o, ref["o"])
+    print(f"{view}: o={err:.2e}")
+    assert err <= TOL
+
+
+def orc_freqs(n, R):
+    from oracle import pope_oracle as orc
+    return orc.pope_freqs(n, orc.inv_freqs(R))
+
+
+def test_fp32_flash_rejects_values_beyond_fp16(cuda):
+    """fp32 q / k / v run on fp16 operands; a finite value beyond 65504 raises instead of
+    silently becoming inf."""
+    import pope_amd
+    inp = make_pope_inputs(3, 1, 2, 2, 64, 64, 64, 32, torch.float32)
+    q = inp["q"].clone()
+    q[0, 0, 0, 0] = 7.0e4
+    with pytest.raises(ValueError, match="fp16"):
+        pope_amd.flash_attn_with_pope(q, inp["k"], inp["v"], pos_emb=(inp["freqs"], inp["bias"]))

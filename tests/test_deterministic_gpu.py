@@ -33,10 +33,13 @@ def deterministic():
 
 def _flash_grads(inp, causal):
     import pope_amd
+    from pope_amd import hip_pope_flash_attn as fa
     t = [inp[n].detach().clone().requires_grad_(True) for n in ("q", "k", "v", "freqs", "bias")]
     o = pope_amd.flash_attn_with_pope(t[0], t[1], t[2], pos_emb=(t[3], t[4]), mask=inp["mask"], causal=causal)
     o.backward(inp["do"])
     torch.cuda.synchronize()
+    # the backward took the forward's workspace (its preparation) as is, in either mode
+    assert fa._LAST_BWD_PREPARED
     return dict(o=o.detach(), dq=t[0].grad, dk=t[1].grad, dv=t[2].grad, dfreqs=t[3].grad, dbias=t[4].grad)
 
 
