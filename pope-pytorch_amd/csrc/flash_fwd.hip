@@ -207,15 +207,24 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
             : "+v"(s[kb][r]) : "v"(-INFINITY), "v"((int)ok) : "vcc");
       }
   };
-  // S^T - m for the group's tile of pair pr (the accumulators start from the -m block)
+  // S^T - m for the group's tile of pair pr (the accumulators start from the -m block).
+  constexpr int NQK = KB * KS;
+  // Rows of up to 128 expanded features run the step's two bursts in the fenced order below,
+  // with six K_hat operand reads in flight, so that an operand read's LDS latency overlaps the
+  // products before it instead of preceding each product (C3 forward 55.0 -> 53.5 us).  Wider
+  // rows keep the compiler's interleave (sched_group_barrier), which was faster there (C4 86.9
+  // against 88.5 us).
+  constexpr bool kFenced = EP <= 128;
+  constexpr int kPF = 6;   // K_hat operand reads in flight ahead of the products (fenced order)
+  auto k_operand = [&](const uint16_t* kt, int i) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(kt + 32 * (i / KS) * EP + ko.row_at(i % KS));
+  };
   auto qk = [&](int pr, f32x16* s) {
     const uint16_t* kt = kh_tile(pr);
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      s[kb] = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt + 32 * kb * EP + ko.row_at(0))), qreg[0], negm);
-#pragma unroll
-      for (int kk = 1; kk < KS; ++kk)
-        s[kb] = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt + 32 * kb * EP + ko.row_at(kk))), qreg[kk], s[kb]);
+    for (int i = 0; i < NQK; ++i) {
+      const int kb = i / KS, kk = i % KS;
+      s[kb] = T::mfma32(as_vec8<vec8>(k_operand(kt, i)), qreg[kk], kk == 0 ? negm : s[kb]);
     }
   };
   auto rowmax = [&](const f32x16* s) -> float {
@@ -264,6 +273,70 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
           pw[2 * kb + g][q] = w;
           l_run = T::dot2(w, ones, l_run);
         }
+  };
+  // The pipelined step's two product bursts, each in an explicit order: a fence
+  // (sched_barrier) after every product pins, next to that product, the operand reads of a later
+  // product (so an LDS read has several products' time to land, instead of preceding each
+  // product) and an even share of the VALU work the burst overlaps.
+  //   scores of tile t + 1  with  the probabilities and row sum of tile t
+  //   P V of tile t          with  the row maximum of tile t + 1
+  constexpr int NPU = 2 * KB * 4;   // probability units: 2 exponentials, a pack, a row-sum dot
+  auto prob_unit = [&](const f32x16* s, u32x4* pw, int u) {
+    const int kb = u / 8, g = (u / 4) % 2, q = u % 4;
+    const uint32_t w = T::pack2(__builtin_amdgcn_exp2f(s[kb][8 * g + 2 * q]),
+                                __builtin_amdgcn_exp2f(s[kb][8 * g + 2 * q + 1]));
+    pw[2 * kb + g][q] = w;
+    l_run = T::dot2(w, T::pack2(1.f, 1.f), l_run);
+    // pinned here (a volatile statement stays between the fences around it): otherwise the
+    // packs and the row sum drift past the fences into a later block
+    asm volatile("" : "+v"(pw[2 * kb + g][q]), "+v"(l_run));
+  };
+  auto qk_probs = [&](int pr, f32x16* s, const f32x16* cur, u32x4* pw) {
+    const uint16_t* kt = kh_tile(pr);
+    u32x4 fk[NQK];
+#pragma unroll
+    for (int i = 0; i < kPF && i < NQK; ++i) fk[i] = k_operand(kt, i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NQK; ++i) {
+      const int kb = i / KS, kk = i % KS;
+      s[kb] = T::mfma32(as_vec8<vec8>(fk[i]), qreg[kk], kk == 0 ? negm : s[kb]);
+      if (i + kPF < NQK) fk[i + kPF] = k_operand(kt, i + kPF);
+#pragma unroll
+      for (int u = i * NPU / NQK; u < (i + 1) * NPU / NQK; ++u) prob_unit(cur, pw, u);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  constexpr int NPV = (BN / 16) * NDB, kVPF = 2;
+  auto pv_rowmax = [&](int pr, const u32x4* pw, const f32x16* s) -> float {
+    const uint32_t vb = lds_addr(v_tile(pr));
+    uint32_t alo[NDB], ahi[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      alo[db] = opaque_u32(vb + 2 * vo.lo_at(db));
+      ahi[db] = opaque_u32(vb + 2 * vo.hi_at(db));
+    }
+    auto v_operand = [&](int i) -> u32x4 {
+      const int g16 = i / NDB, db = i % NDB;
+      const uint32_t off = 2 * 16 * g16 * DV;
+      return lds_tr8_at(alo[db] + off, ahi[db] + off);
+    };
+    u32x4 fv[NPV];
+#pragma unroll
+    for (int i = 0; i < kVPF && i < NPV; ++i) fv[i] = v_operand(i);
+    __builtin_amdgcn_sched_barrier(0);
+    float mt = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NPV; ++i) {
+      const int g16 = i / NDB, db = i % NDB;
+      oacc[db] = T::mfma32(as_vec8<vec8>(fv[i]), as_vec8<vec8>(pw[g16]), oacc[db]);
+      if (i + kVPF < NPV) fv[i + kVPF] = v_operand(i + kVPF);
+#pragma unroll
+      for (int x = i * 16 * KB / NPV; x < (i + 1) * 16 * KB / NPV; ++x) mt = fmaxf(mt, s[x / 16][x % 16]);
+      asm volatile("" : "+v"(mt));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return half_swap_max(mt);
   };
   // O^T += V^T P^T over the tile's 16-key groups
   auto pv = [&](int pr, const u32x4* pw) {
@@ -323,13 +396,17 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
       // keep the exponentials of tile t below the barrier, next to the MFMAs they overlap
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) asm volatile("" : "+v"(cur[kb]));
-      qk(t + 1, nxt);
-      probs(cur, pw);
+      if constexpr (kFenced) {
+        qk_probs(t + 1, nxt, cur, pw);
+      } else {
+        qk(t + 1, nxt);
+        probs(cur, pw);
 #pragma unroll
-      for (int i = 0; i < KB * KS; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedValu, (6 * KB * 16 / 2) / (KB * KS), 0);
+        for (int i = 0; i < NQK; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedValu, (6 * KB * 16 / 2) / NQK, 0);
+        }
       }
       // the packed probabilities are complete here, before the mask branch: otherwise their
       // exponentials sink past it into the P V block, away from the score products they overlap
@@ -339,13 +416,17 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
         POPE_COLD_PATH();
         apply_mask(t + 1, mb, nxt);
       }
-      pv(t, pw);
-      mt = rowmax(nxt);
+      if constexpr (kFenced) {
+        mt = pv_rowmax(t, pw, nxt);
+      } else {
+        pv(t, pw);
+        mt = rowmax(nxt);
 #pragma unroll
-      for (int i = 0; i < (BN / 16) * NDB; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
-        __builtin_amdgcn_sched_group_barrier(kSchedValu, 2, 1);
+        for (int i = 0; i < NPV; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
+          __builtin_amdgcn_sched_group_barrier(kSchedValu, 2, 1);
+        }
       }
     };
     auto last = [&](int t, f32x16* cur) {
