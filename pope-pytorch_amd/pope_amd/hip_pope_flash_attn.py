@@ -69,9 +69,13 @@ def _prep_pope(freqs: Optional[Tensor], bias: Optional[Tensor]):
         freqs = freqs.float()
     # rows of 16-byte vectors: unit feature stride, row / batch / head strides and the view's
     # offset in whole 4-float units (storage_offset, not data_ptr, so fake tensors decide alike)
-    # (rotate dims that are not multiples of 8 are padded into a fresh table later)
-    if freqs.stride(-1) != 1 or (freqs.shape[-1] % 8 == 0 and (
-            freqs.storage_offset() % 4 or any(s % 4 for s in freqs.stride()[:-1]))):
+    # (rotate dims that are not multiples of 8 are padded into a fresh table later; under
+    # torch.compile tracing the offset is not inspected, and the forward copies a misaligned
+    # table itself where the decode kernel needs it)
+    misaligned = freqs.shape[-1] % 8 == 0 and any(s % 4 for s in freqs.stride()[:-1])
+    if not torch.compiler.is_compiling() and freqs.shape[-1] % 8 == 0:
+        misaligned = misaligned or freqs.storage_offset() % 4 != 0
+    if freqs.stride(-1) != 1 or misaligned:
         freqs = freqs.clone(memory_format=torch.contiguous_format)
     if bias.dtype != torch.float32:
         bias = bias.float()
