@@ -34,7 +34,9 @@ stream it runs on; the events stay out of the timed pass).  Its ``traffic`` is
 the HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
 summary (profiles/flash_c3_traffic.md), calibrated against a copy kernel.
 ``cpu_baseline`` times the CPU oracle (the restatement of the reference's
-PyTorch path) fwd+bwd on the whole workload on this host's cores.
+PyTorch path) fwd+bwd on the whole workload on this host's cores; its ``configs``
+object times the same oracle on C1, C2, C4 and C5 (forward, and forward + backward
+where the config has one) on the GPU lines' seeded inputs.
 """
 from __future__ import annotations
 
@@ -406,6 +408,108 @@ def cpu_baseline(min_seconds: float = 10.0, max_reps: int = 10):
     }
 
 
+def _time_cpu(fn, min_seconds: float, max_reps: int, min_reps: int = 3):
+    """Median wall time of fn() over at least ``min_reps`` passes (after one warm-up pass),
+    repeated until about ``min_seconds`` of CPU work or ``max_reps`` passes."""
+    fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < max_reps and (len(times) < min_reps or time.perf_counter() - t_start < min_seconds):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_configs(min_seconds: float = 3.0, max_reps: int = 5) -> dict:
+    """The CPU oracle on the other BASELINE configs, on the same seeded inputs as the GPU lines
+    (C1 from seed 1001): forward, and forward + backward where the config has a backward, over
+    the whole workload of each config in fp32 (bf16 inputs cast first, as the reference's
+    PyTorch path promotes them, pope.py:60,69-70).  Each figure is the median of at least three
+    passes; the value is in the unit the config's GPU figure uses."""
+    import torch
+
+    from oracle import pope_oracle as orc
+
+    out = {}
+    # C1: PoPE(64, heads=8), pope(1024), q, k, v (1, 8, 1024, 64) fp32: similarity and attention
+    g = torch.Generator().manual_seed(1001)
+    q1, k1, v1 = (torch.randn(1, 8, 1024, 64, generator=g) for _ in range(3))
+    f1, b1 = orc.pope_freqs(1024, orc.inv_freqs(64)), torch.zeros(8, 64)
+
+    def c1():
+        orc.sim_nonfused(q1, k1, f1, b1)
+        orc.flash_nonfused(q1, k1, v1, f1, b1)
+
+    t, n = _time_cpu(c1, min_seconds, max_reps)
+    c1_flops = 2 * 8 * 1024 * 1024 * (64 + 64) * 2 + 2 * 8 * 1024 * 1024 * 64
+    out["C1"] = {"fwd_ms": round(t * 1e3, 2), "value": round(c1_flops / t / 1e12, 5), "unit": "TFLOP/s",
+                 "passes": n, "sample": "whole workload: similarity (1,8,1024,1024) and attention output, fp32"}
+
+    # C2: similarity fwd + bwd, q, k (2, 8, 2048, 64) fp32, dS N(0, 1) (the GPU line's seed and draws)
+    g = torch.Generator().manual_seed(SIM_SEED)
+    q2 = torch.randn(SIM_B, SIM_H, SIM_N, SIM_D, generator=g)
+    k2 = torch.randn(SIM_B, SIM_H, SIM_N, SIM_D, generator=g)
+    ds2 = torch.randn(SIM_B, SIM_H, SIM_N, SIM_N, generator=g)
+    f2, b2 = orc.pope_freqs(SIM_N, orc.inv_freqs(SIM_D)), torch.zeros(SIM_H, SIM_D)
+    qg, kg, bg = q2.clone().requires_grad_(True), k2.clone().requires_grad_(True), b2.clone().requires_grad_(True)
+    tf, _ = _time_cpu(lambda: orc.sim_nonfused(q2, k2, f2, b2), min_seconds, max_reps)
+
+    def c2():
+        orc.sim_nonfused(qg, kg, f2, bg).backward(ds2)
+
+    t, n = _time_cpu(c2, min_seconds, max_reps)
+    c2_bytes = 2 * 4 * SIM_B * SIM_H * SIM_N * SIM_N + 2 * 4 * 2 * SIM_B * SIM_H * SIM_N * SIM_D + 4 * SIM_N * SIM_D
+    out["C2"] = {"fwd_ms": round(tf * 1e3, 2), "fwd_bwd_ms": round(t * 1e3, 2),
+                 "value": round(c2_bytes / t / 1e9, 3), "unit": "GB/s", "passes": n,
+                 "sample": "whole workload: sim (2,8,2048,2048), dq, dk, dbias; bytes as the GPU line"}
+
+    # C4: axial flash fwd + bwd, (4, 8, 2048, 96) bf16 -> fp32, AxialPoPE(96, 8, (32, 32, 32)) on (8, 16, 16)
+    g = torch.Generator().manual_seed(AX_SEED)
+    q4, k4, v4, do4 = (torch.randn(4, 8, 2048, 96, generator=g).to(torch.bfloat16).float() for _ in range(4))
+    f4 = orc.axial_freqs(orc.axial_grid_positions(8, 16, 16), orc.axial_inv_freqs((32, 32, 32)))
+    b4 = torch.zeros(8, 96)
+
+    def c4(bwd):   # sample: batch 0 of 4 (a quarter of the workload), four heads per call
+        def run():
+            for b in range(1):
+                for h0 in range(0, 8, 4):
+                    sl = lambda t: t[b:b + 1, h0:h0 + 4].clone().requires_grad_(bwd)
+                    o = orc.flash_nonfused(sl(q4), sl(k4), sl(v4), f4, b4[h0:h0 + 4])
+                    if bwd:
+                        o.backward(do4[b:b + 1, h0:h0 + 4])
+        return run
+
+    tf, _ = _time_cpu(c4(False), min_seconds, max_reps, 2)
+    t, n = _time_cpu(c4(True), min_seconds, max_reps, 2)
+    c4_flops = 3.5 * 4 * 1 * 8 * 2048 * 2048 * 96
+    out["C4"] = {"fwd_ms": round(tf * 1e3, 2), "fwd_bwd_ms": round(t * 1e3, 2),
+                 "value": round(c4_flops / t / 1e12, 5), "unit": "TFLOP/s", "passes": n,
+                 "sample": "batch 0 of 4 (8 heads, a quarter of the workload), four heads per call; "
+                           "times are for the sample, the value uses the sample's FA flops"}
+
+    # C5: decode, q (8, 16, 1, 64) against K / V (8, 16, 32768, 64) bf16 -> fp32, valid lengths U{4096..32768}
+    g = torch.Generator().manual_seed(DEC_SEED)
+    q5 = torch.randn(DEC_B, DEC_H, 1, DEC_D, generator=g).to(torch.bfloat16).float()
+    k5 = torch.randn(DEC_B, DEC_H, DEC_N, DEC_D, generator=g).to(torch.bfloat16)
+    v5 = torch.randn(DEC_B, DEC_H, DEC_N, DEC_D, generator=g).to(torch.bfloat16)
+    lens = torch.randint(4096, DEC_N + 1, (DEC_B,), generator=g)
+    mask5 = torch.arange(DEC_N)[None, :] < lens[:, None]
+    f5, b5 = orc.pope_freqs(DEC_N, orc.inv_freqs(DEC_D)), torch.zeros(DEC_H, DEC_D)
+
+    def c5():   # sample: sequences 0 and 1 of 8, one per call
+        for b in range(2):
+            orc.flash_nonfused(q5[b:b + 1], k5[b:b + 1].float(), v5[b:b + 1].float(), f5, b5, mask=mask5[b:b + 1])
+
+    t, n = _time_cpu(c5, min_seconds, max_reps, 2)
+    valid = int(lens[:2].sum()) * DEC_H * DEC_D * 2 * 2
+    out["C5"] = {"fwd_ms": round(t * 1e3, 2), "value": round(valid / t / 1e9, 3), "unit": "GB/s", "passes": n,
+                 "sample": f"sequences 0 and 1 of 8 (valid lengths {int(lens[0])}, {int(lens[1])}), one "
+                           "per call; GB/s of their valid bf16 K and V rows, as the GPU line counts"}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -461,6 +565,7 @@ def main():
     }
     if not a.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
+        line["cpu_baseline"]["configs"] = cpu_configs()
     print(json.dumps(line), flush=True)
 
 
