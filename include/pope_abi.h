@@ -166,8 +166,12 @@ int pope_flash_bwd(const pope_desc* desc, const void* dout, const void* q, const
 /*
  * Bandwidth-bound forward for a single non-causal query row against a long KV
  * cache (decode): split-K over the keys plus an LSE merge.  Same contract as
- * pope_flash_fwd; returns POPE_ERR_UNSUPPORTED for Nq != 1, causal, or head dim
- * above 128 (callers then use pope_flash_fwd).  Replaces flash_attn_forward at
+ * pope_flash_fwd; returns
+ * POPE_ERR_UNSUPPORTED (callers then use pope_flash_fwd) for: Nq != 1; causal; head
+ * dim above 128; per-head freqs tables (f_s[1] != 0); query heads x head dim above
+ * 4096 (the query weights are staged in LDS); freqs rows that are not 16-byte
+ * aligned (pointer, f_s[0] or f_s[2] not a multiple of 4 floats); K / V row offsets
+ * within a (batch, head) beyond 32 bits.  Replaces flash_attn_forward at
  * seqlen_q = 1 (triton_pope_flash_attn.py:222-271 with grid (1, B*H)).
  */
 int pope_flash_decode(const pope_desc* desc, const void* q, const void* k, const void* v,

@@ -875,4 +875,11 @@ hipError_t launch_flash_bwd(const FlashBwdParams& p, int dtype, hipStream_t s) {
   return dtype == 2 ? dispatch<BF16>(p, s) : dispatch<F16>(p, s);
 }
 
+hipError_t launch_flash_bwd_delta(const FlashBwdParams& p, int dtype, hipStream_t s) {
+  const int64_t nrows = (int64_t)p.B * p.Hq * p.NqP;
+  const dim3 grid((unsigned)((8 * nrows + 255) / 256));
+  return dtype == 2 ? launch_named("flash_bwd_delta", bwd_delta_kernel<BF16>, grid, dim3(256), s, p)
+                    : launch_named("flash_bwd_delta", bwd_delta_kernel<F16>, grid, dim3(256), s, p);
+}
+
 }  // namespace pope

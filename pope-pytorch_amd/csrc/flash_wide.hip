@@ -1,0 +1,493 @@
+// Flash attention with PoPE for wide heads: head dims of 136 to 256 (after padding to a multiple
+// of 8), expanded rows up to 512 features (gfx950, bf16 / fp16 MFMA).
+//
+// Reference semantics: triton_pope_flash_attn.py:23-117 (forward), :119-218 (backward), whose
+// Triton kernels take any head dim (BD = next_pow2(D), :252-254); PyTorch path
+// attention.py:106-145.
+//
+// The rows of these heads do not fit the register tiling of flash_fwd.hip / flash_bwd.hip (the
+// backward's dK_hat accumulator alone is 256 registers per lane at E = 512), so the wide path
+// trades speed for a plain structure: one wave per workgroup, 32 rows per wave, the
+// accumulators of the backward split over kChunks column chunks (each chunk recomputes the
+// scores), and the polar transform's chain rule in a separate pass.  Memory stays linear in the
+// sequence length: no score matrix is stored.  Same workspace preparation as the narrow path
+// (flash_prep.hip: K_hat, Q_hat pre-scaled by softmax_scale * log2 e, key visibility words,
+// phase tables), with EP = E rounded up to 128 and DV = 256.
+//   wide_fwd   one wave per (32 queries, batch * head): S^T = K_hat Q_hat^T (K_hat rows from
+//              global memory), online softmax in log2 units, O^T += V^T P^T with V staged in LDS
+//              and read transposed (ds_read_b64_tr_b16).
+//   wide_kv    one wave per (32 keys, column chunk, batch * kv head): S = Q_hat K_hat^T - lse,
+//              dP = dO V^T - delta (Q_hat and dO tiles staged in LDS), P = exp2 S, dS = P dP;
+//              dV (its chunk of D columns) += P^T dO and dK_hat (its chunk of E columns) +=
+//              dS^T Q_hat; writes dV and the raw dK_hat chunk (fp32 workspace).
+//   wide_q     one wave per (32 queries, column chunk, batch * head): S^T, dP^T with the K_hat
+//              tile in LDS, dQ_hat^T (its chunk) += K_hat^T dS^T; writes the raw dQ_hat chunk.
+//   wide_chain the chain rule of the polar transform from the raw rows: dk, dq, dfreqs, dbias
+//              (deterministic mode: the per-row phase derivatives, summed later in a fixed order).
+#include "pope_common.hpp"
+#include "pope_kernels.hpp"
+
+namespace pope {
+
+namespace {
+
+constexpr int kChunks = 4;   // column chunks of the backward's accumulators
+
+__device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
+
+typedef const __attribute__((address_space(4))) uint64_t cu64;
+typedef const __attribute__((address_space(4))) int ci32;
+
+// Registers [8 g, 8 g + 8) of an MFMA result, packed as an 8-element operand.
+template <typename T>
+__device__ __forceinline__ u32x4 pack8w(const f32x16& x, int g) {
+  u32x4 w;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) w[s] = T::pack2(x[8 * g + 2 * s], x[8 * g + 2 * s + 1]);
+  return w;
+}
+
+__device__ __forceinline__ f32x16 splat16(float x) {
+  f32x16 c;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) c[r] = x;
+  return c;
+}
+
+// Row offset within a 32-row block of register r of a 32x32 MFMA result in lane half hf.
+__device__ __forceinline__ int res_row(int r, int hf) { return 8 * (r >> 2) + 4 * hf + (r & 3); }
+
+// Stages rows [r0, r0 + 32) of a 16-bit row-major source (row stride rs elements) into a
+// row-major LDS tile of `cols` columns: rows past row_last repeat it, 8-column chunks at or past
+// `dlim` are zero (head columns past D).  One wave.
+template <int COLS>
+__device__ __forceinline__ void stage32(uint16_t* lds, const uint16_t* src, int64_t rs, int r0, int row_last,
+                                        int dlim) {
+  constexpr int U = COLS / 8;
+  for (int c = threadIdx.x; c < 32 * U; c += 64) {
+    const int r = c / U, d0 = 8 * (c % U);
+    const u32x4 v = d0 < dlim ? ld16(src + (int64_t)min(r0 + r, row_last) * rs + d0) : zero4();
+    *reinterpret_cast<u32x4*>(lds + r * COLS + d0) = v;
+  }
+}
+
+// ---- forward ---------------------------------------------------------------------------
+template <typename T, int EP, int DV>
+__global__ __launch_bounds__(64) void wide_fwd_kernel(FlashFwdParams p) {
+  constexpr int KS = EP / 16, NDB = DV / 32;
+  typedef typename T::vec8 vec8;
+  __shared__ __attribute__((aligned(16))) uint16_t vt[32 * DV];
+
+  const int lane = threadIdx.x, lr = lane & 31, hf = lane >> 5;
+  const int BH = p.B * p.Hq, nqb = p.NqP / 32;
+  const int bh = blockIdx.x % BH;
+  const int q0 = 32 * (nqb - 1 - (int)(blockIdx.x / BH));   // heaviest causal blocks first
+  if (q0 >= p.Nq) return;
+  const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
+  const int Nk = p.Nk, D = p.D, qi = q0 + lr;
+
+  vec8 qreg[KS];
+  {
+    const uint16_t* qrow = p.qh + ((int64_t)bh * p.NqP + qi) * EP + 8 * hf;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) qreg[kk] = as_vec8<vec8>(ld16(qrow + 16 * kk));
+  }
+  int nkeys = min(((ci32*)p.kend)[b], Nk);
+  if (p.causal) nkeys = min(nkeys, q0 + 32);
+  const uint16_t* khb = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;
+  const uint16_t* vb = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
+  cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
+  const TrLane tl = tr_lane<false>(DV, lane);
+
+  f32x16 oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) oacc[db] = splat16(0.f);
+  float m = -INFINITY, l = 0.f;
+  const uint32_t ones = T::pack2(1.f, 1.f);
+  for (int j0 = 0; j0 < nkeys; j0 += 32) {
+    stage32<DV>(vt, vb, p.v_s[2], j0, Nk - 1, D);
+    // S^T (rows = keys, lane = query), log2 units
+    f32x16 s = splat16(0.f);
+    const uint16_t* kr = khb + (int64_t)(j0 + lr) * EP + 8 * hf;   // rows padded to NkP
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) s = T::mfma32(as_vec8<vec8>(ld16(kr + 16 * kk)), qreg[kk], s);
+    const uint32_t wv = (uint32_t)(mw[j0 >> 6] >> (j0 & 32));
+    float mt = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr_ = res_row(r, hf);
+      const bool ok = ((wv >> kr_) & 1u) && (!p.causal || j0 + kr_ <= qi);
+      s[r] = ok ? s[r] : -INFINITY;
+      mt = fmaxf(mt, s[r]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mn = fmaxf(m, mt);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m - mu);
+    u32x4 pw[2];
+    float ls = 0.f;
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t w = T::pack2(__builtin_amdgcn_exp2f(s[8 * g + 2 * q] - mu),
+                                    __builtin_amdgcn_exp2f(s[8 * g + 2 * q + 1] - mu));
+        pw[g][q] = w;
+        ls = T::dot2(w, ones, ls);   // the row sum of the probabilities the products use
+      }
+    l = l * alpha + ls + __shfl_xor(ls, 32, 64);
+    m = mn;
+    __syncthreads();   // the V tile's stores are complete
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+        oacc[db] = T::mfma32(as_vec8<vec8>(lds_operand_tr(vt, tl, DV, 16 * g, 32 * db)), as_vec8<vec8>(pw[g]),
+                             oacc[db]);
+    }
+    __syncthreads();   // every V read of this tile is done before the next tile is staged
+  }
+  if (qi >= p.Nq) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1] + (int64_t)qi * p.o_s[2];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * db + 8 * g + 4 * hf;
+      if (d0 < D) {
+        u32x2 w;
+        w[0] = T::pack2(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv);
+        w[1] = T::pack2(oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + d0) = w;
+      }
+    }
+  if (hf == 0)
+    p.lse[((int64_t)b * p.Hq + h) * p.Nq + qi] = m == -INFINITY ? -INFINITY : (m + __builtin_amdgcn_logf(l)) * kLn2;
+}
+
+// ---- backward: dK_hat / dV --------------------------------------------------------------
+template <typename T, int EP, int DV>
+__global__ __launch_bounds__(64) void wide_kv_kernel(FlashBwdParams p, float* wk) {
+  constexpr int KS = EP / 16, DS = DV / 16, EBC = EP / 32 / kChunks, DBC = DV / 32 / kChunks;
+  typedef typename T::vec8 vec8;
+  __shared__ __attribute__((aligned(16))) uint16_t qt[32 * EP];
+  __shared__ __attribute__((aligned(16))) uint16_t dt[32 * DV];
+
+  const int lane = threadIdx.x, lr = lane & 31, hf = lane >> 5;
+  const int nkb = p.NkP / 32;
+  const int ec = blockIdx.x % kChunks, rest = blockIdx.x / kChunks;
+  const int k0 = 32 * (rest % nkb), bhk = rest / nkb;   // key block 0 (the heaviest causal one) first
+  const int b = bhk / p.Hk, hk = bhk % p.Hk;
+  const int Nk = p.Nk, Nq = p.Nq, D = p.D, NqP = p.NqP;
+  if (k0 >= Nk) return;
+  const int kj = k0 + lr;
+  cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
+  const bool kvis = (mw[kj >> 6] >> (kj & 63)) & 1ull;
+
+  vec8 kreg[KS], vreg[DS];
+  {
+    const uint16_t* khr = p.kh + ((int64_t)bhk * p.NkP + kj) * EP + 8 * hf;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) kreg[kk] = as_vec8<vec8>(ld16(khr + 16 * kk));
+    const uint16_t* vr = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1] + (int64_t)min(kj, Nk - 1) * p.v_s[2];
+#pragma unroll
+    for (int kk = 0; kk < DS; ++kk) {
+      const int d0 = 16 * kk + 8 * hf;
+      vreg[kk] = as_vec8<vec8>((kj < Nk && d0 < D) ? ld16(vr + d0) : zero4());
+    }
+  }
+  f32x16 dka[EBC], dva[DBC];
+#pragma unroll
+  for (int x = 0; x < EBC; ++x) dka[x] = splat16(0.f);
+#pragma unroll
+  for (int x = 0; x < DBC; ++x) dva[x] = splat16(0.f);
+  const TrLane tq = tr_lane<false>(EP, lane), td = tr_lane<false>(DV, lane);
+
+  if (__any(kvis)) {
+    const int groups = p.Hq / p.Hk;
+    for (int g = 0; g < groups; ++g) {
+      const int h = g * p.Hk + hk, bh = b * p.Hq + h;
+      const uint16_t* qhb = p.qh + (int64_t)bh * NqP * EP;
+      const uint16_t* dob = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1];
+      const float* nlb = p.nl + (int64_t)bh * NqP;
+      const float* ndb = p.nd + (int64_t)bh * NqP;
+      for (int q0 = p.causal ? k0 : 0; q0 < Nq; q0 += 32) {
+        stage32<EP>(qt, qhb, EP, q0, NqP - 1, EP);
+        stage32<DV>(dt, dob, p.do_s[2], q0, Nq - 1, D);
+        // -lse and -delta of the result rows (queries q0 + res_row(r, hf); padded rows give P = 0)
+        f32x16 nl16, nd16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 a = *reinterpret_cast<const f32x4*>(nlb + q0 + 8 * q + 4 * hf);
+          const f32x4 c = *reinterpret_cast<const f32x4*>(ndb + q0 + 8 * q + 4 * hf);
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            nl16[4 * q + x] = a[x];
+            nd16[4 * q + x] = c[x];
+          }
+        }
+        __syncthreads();   // the tiles' stores are complete
+        // S = Q_hat K_hat^T - lse and dP = dO V^T - delta (rows = queries, lane = key)
+        f32x16 s = nl16, dp = nd16;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+          s = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(qt + lr * EP + 16 * kk + 8 * hf)), kreg[kk], s);
+#pragma unroll
+        for (int kk = 0; kk < DS; ++kk)
+          dp = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(dt + lr * DV + 16 * kk + 8 * hf)), vreg[kk], dp);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const bool ok = kvis && (!p.causal || kj <= q0 + res_row(r, hf));
+          const float pv = ok ? __builtin_amdgcn_exp2f(s[r]) : 0.f;
+          s[r] = pv;
+          dp[r] = pv * dp[r];
+        }
+#pragma unroll
+        for (int g2 = 0; g2 < 2; ++g2) {
+          const vec8 ap = as_vec8<vec8>(pack8w<T>(s, g2)), ads = as_vec8<vec8>(pack8w<T>(dp, g2));
+#pragma unroll
+          for (int db = 0; db < DBC; ++db)
+            dva[db] = T::mfma32(ap, as_vec8<vec8>(lds_operand_tr(dt, td, DV, 16 * g2, 32 * (ec * DBC + db))), dva[db]);
+#pragma unroll
+          for (int eb = 0; eb < EBC; ++eb)
+            dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_operand_tr(qt, tq, EP, 16 * g2, 32 * (ec * EBC + eb))), dka[eb]);
+        }
+        __syncthreads();   // every tile read is done before the next tiles are staged
+      }
+    }
+  }
+  // dV (lane = d column, registers = keys); the raw dK_hat chunk, times ln 2 (Q_hat carries log2 e)
+  uint16_t* dvb = p.dv + (int64_t)b * p.dv_s[0] + (int64_t)hk * p.dv_s[1];
+#pragma unroll
+  for (int db = 0; db < DBC; ++db) {
+    const int d = 32 * (ec * DBC + db) + lr;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = k0 + res_row(r, hf);
+      if (key < Nk && d < D) dvb[(int64_t)key * p.dv_s[2] + d] = T::bits(dva[db][r]);
+    }
+  }
+  float* wkb = wk + (int64_t)bhk * p.NkP * EP;
+#pragma unroll
+  for (int eb = 0; eb < EBC; ++eb) {
+    const int e = 32 * (ec * EBC + eb) + lr;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) wkb[(int64_t)(k0 + res_row(r, hf)) * EP + e] = dka[eb][r] * kLn2;
+  }
+}
+
+// ---- backward: dQ_hat -------------------------------------------------------------------
+template <typename T, int EP, int DV>
+__global__ __launch_bounds__(64) void wide_q_kernel(FlashBwdParams p, float* wq) {
+  constexpr int KS = EP / 16, DS = DV / 16, EBC = EP / 32 / kChunks;
+  typedef typename T::vec8 vec8;
+  __shared__ __attribute__((aligned(16))) uint16_t kt[32 * EP];
+
+  const int lane = threadIdx.x, lr = lane & 31, hf = lane >> 5;
+  const int nqb = p.NqP / 32;
+  const int ec = blockIdx.x % kChunks, rest = blockIdx.x / kChunks;
+  const int q0 = 32 * (nqb - 1 - rest % nqb), bh = rest / nqb;   // heaviest causal blocks first
+  const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
+  const int Nk = p.Nk, Nq = p.Nq, D = p.D;
+  if (q0 >= Nq) return;
+  const int qi = q0 + lr;
+
+  vec8 qreg[KS], doreg[DS];
+  {
+    const uint16_t* qhr = p.qh + ((int64_t)bh * p.NqP + qi) * EP + 8 * hf;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) qreg[kk] = as_vec8<vec8>(ld16(qhr + 16 * kk));
+    const uint16_t* dr = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1] + (int64_t)min(qi, Nq - 1) * p.do_s[2];
+#pragma unroll
+    for (int kk = 0; kk < DS; ++kk) {
+      const int d0 = 16 * kk + 8 * hf;
+      doreg[kk] = as_vec8<vec8>((qi < Nq && d0 < D) ? ld16(dr + d0) : zero4());
+    }
+  }
+  const float nls = p.nl[(int64_t)bh * p.NqP + qi], nds = p.nd[(int64_t)bh * p.NqP + qi];
+  f32x16 dqa[EBC];
+#pragma unroll
+  for (int x = 0; x < EBC; ++x) dqa[x] = splat16(0.f);
+  int nkeys = min(((ci32*)p.kend)[b], Nk);
+  if (p.causal) nkeys = min(nkeys, q0 + 32);
+  const uint16_t* khb = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;
+  const uint16_t* vb = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
+  cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
+  const TrLane tk = tr_lane<false>(EP, lane);
+  for (int j0 = 0; j0 < nkeys; j0 += 32) {
+    stage32<EP>(kt, khb, EP, j0, p.NkP - 1, EP);
+    __syncthreads();   // the tile's stores are complete
+    // S^T = K_hat Q_hat^T - lse and dP^T = V dO^T - delta (rows = keys, lane = query)
+    f32x16 s = splat16(nls), dp = splat16(nds);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
+      s = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt + lr * EP + 16 * kk + 8 * hf)), qreg[kk], s);
+    const uint16_t* vr = vb + (int64_t)min(j0 + lr, Nk - 1) * p.v_s[2] + 8 * hf;
+#pragma unroll
+    for (int kk = 0; kk < DS; ++kk) {
+      const u32x4 va = 16 * kk + 8 * hf < D ? ld16(vr + 16 * kk) : zero4();
+      dp = T::mfma32(as_vec8<vec8>(va), doreg[kk], dp);
+    }
+    const uint32_t wv = (uint32_t)(mw[j0 >> 6] >> (j0 & 32));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr_ = res_row(r, hf);
+      const bool ok = ((wv >> kr_) & 1u) && (!p.causal || j0 + kr_ <= qi);
+      dp[r] = ok ? __builtin_amdgcn_exp2f(s[r]) * dp[r] : 0.f;
+    }
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) {
+      const vec8 bds = as_vec8<vec8>(pack8w<T>(dp, g2));
+#pragma unroll
+      for (int eb = 0; eb < EBC; ++eb)
+        dqa[eb] = T::mfma32(as_vec8<vec8>(lds_operand_tr(kt, tk, EP, 16 * g2, 32 * (ec * EBC + eb))), bds, dqa[eb]);
+    }
+    __syncthreads();   // every tile read is done before the next tile is staged
+  }
+  // the raw dQ_hat chunk (rows = e, lane = query), times softmax_scale
+  float* wqb = wq + ((int64_t)bh * p.NqP + qi) * EP;
+#pragma unroll
+  for (int eb = 0; eb < EBC; ++eb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) wqb[32 * (ec * EBC + eb) + res_row(r, hf)] = dqa[eb][r] * p.scale;
+}
+
+// ---- the chain rule of the polar transform -----------------------------------------------
+// Blocks [0, nk): 32 key rows of one (batch, kv head); blocks [nk, nk + nq): 32 query rows of
+// one (batch, head).  With the raw expanded-row gradients U (cos column e = d, sin column
+// e = R + d, pass-through column e = R + d) and the row's phase (keys F[j]; queries
+// F[q_off + i] - bias, the bias on the query side as in the preparation):
+//   dx = sigmoid(x) (cos U_c + sin U_s),  dphase = softplus(x) (cos U_s - sin U_c)
+// and pass-through dims dx = U.  Key phase derivatives also sum into dbias (per block in LDS,
+// then one atomic per dim).
+template <typename T>
+__global__ __launch_bounds__(256) void wide_chain_kernel(FlashBwdParams p, const float* wk, const float* wq, int nk) {
+  __shared__ float dsum[256];
+  const int tid = threadIdx.x;
+  const int D = p.D, R = p.R, EP = p.EP;
+  if ((int)blockIdx.x < nk) {
+    const int nkb = p.NkP / 32;
+    const int k0 = 32 * (blockIdx.x % nkb), bhk = blockIdx.x / nkb;
+    const int b = bhk / p.Hk, hk = bhk % p.Hk;
+    if (k0 >= p.Nk) return;
+    for (int d = tid; d < R; d += 256) dsum[d] = 0.f;
+    __syncthreads();
+    const uint16_t* kb = p.k + (int64_t)b * p.k_s[0] + (int64_t)hk * p.k_s[1];
+    uint16_t* dkb = p.dk + (int64_t)b * p.dk_s[0] + (int64_t)hk * p.dk_s[1];
+    const float2* tb = R ? p.table + (int64_t)b * p.t_sb + (int64_t)hk * p.t_sh : nullptr;
+    float* dfb = p.dfreqs ? p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)hk * p.df_s[1] : nullptr;
+    float* kpb = p.kpart ? p.kpart + (int64_t)bhk * p.Nk * R : nullptr;
+    const float* wrow = wk + (int64_t)bhk * p.NkP * EP;
+    for (int it = tid; it < 32 * D; it += 256) {
+      const int key = k0 + it / D, d = it % D;
+      if (key >= p.Nk) continue;
+      const float* u = wrow + (int64_t)key * EP;
+      float g;
+      if (d < R) {
+        const float x = T::to_float(kb[(int64_t)key * p.k_s[2] + d]);
+        const float2 cs = tb[(int64_t)key * R + d];
+        const float uc = u[d], us = u[R + d];
+        g = sigmoid_f(x) * (cs.x * uc + cs.y * us);
+        const float dpsi = softplus_f(x) * (cs.x * us - cs.y * uc);
+        if (kpb) {
+          kpb[(int64_t)key * R + d] = dpsi;
+        } else {
+          if (dfb) atomicAdd(dfb + (int64_t)key * p.df_s[2] + d, dpsi);
+          if (p.dbias) atomicAdd(&dsum[d], dpsi);
+        }
+      } else {
+        g = u[R + d];
+      }
+      dkb[(int64_t)key * p.dk_s[2] + d] = T::bits(g);
+    }
+    if (p.dbias && !kpb) {
+      __syncthreads();
+      for (int d = tid; d < R; d += 256) atomicAdd(p.dbias + (int64_t)hk * p.bias_sh + d, dsum[d]);
+    }
+    return;
+  }
+  const int nqb = p.NqP / 32, blk = blockIdx.x - nk;
+  const int q0 = 32 * (blk % nqb), bh = blk / nqb;
+  const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
+  if (q0 >= p.Nq) return;
+  const int q_off = p.Nk - p.Nq;
+  const uint16_t* qb = p.q + (int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1];
+  uint16_t* dqb = p.dq + (int64_t)b * p.dq_s[0] + (int64_t)h * p.dq_s[1];
+  const float2* tq = R ? p.table + (int64_t)b * p.t_sb + (int64_t)h * p.t_sh : nullptr;
+  const float2* bq = R ? p.btab + (p.Hb > 1 ? hk : 0) * R : nullptr;
+  float* dfb = p.dfreqs ? p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)h * p.df_s[1] : nullptr;
+  float* qpb = p.qpart && p.dfreqs ? p.qpart + (int64_t)bh * p.Nq * R : nullptr;
+  const float* wrow = wq + (int64_t)bh * p.NqP * EP;
+  for (int it = tid; it < 32 * D; it += 256) {
+    const int i = q0 + it / D, d = it % D;
+    if (i >= p.Nq) continue;
+    const float* u = wrow + (int64_t)i * EP;
+    float g;
+    if (d < R) {
+      const float x = T::to_float(qb[(int64_t)i * p.q_s[2] + d]);
+      // cos / sin(F[q_off + i] - bias) from the tables of F and of the bias
+      const float2 tf = tq[(int64_t)(q_off + i) * R + d], tbv = bq[d];
+      const float cs = fmaf(tf.x, tbv.x, tf.y * tbv.y), sn = fmaf(tf.y, tbv.x, -tf.x * tbv.y);
+      const float uc = u[d], us = u[R + d];
+      g = sigmoid_f(x) * (cs * uc + sn * us);
+      const float dph = softplus_f(x) * (cs * us - sn * uc);
+      if (qpb) qpb[(int64_t)i * R + d] = dph;
+      else if (dfb) atomicAdd(dfb + (int64_t)(q_off + i) * p.df_s[2] + d, dph);
+    } else {
+      g = u[R + d];
+    }
+    dqb[(int64_t)i * p.dq_s[2] + d] = T::bits(g);
+  }
+}
+
+template <typename T, int EP, int DV>
+hipError_t fwd_t(const FlashFwdParams& p, hipStream_t s) {
+  return launch_named("flash_wide_fwd", wide_fwd_kernel<T, EP, DV>, dim3((p.NqP / 32) * p.B * p.Hq), dim3(64), s, p);
+}
+
+template <typename T, int EP, int DV>
+hipError_t bwd_t(const FlashBwdParams& p, float* wk, float* wq, hipStream_t s) {
+  hipError_t e = launch_named("flash_wide_kv", wide_kv_kernel<T, EP, DV>, dim3((p.NkP / 32) * p.B * p.Hk * kChunks),
+                              dim3(64), s, p, wk);
+  if (e != hipSuccess) return e;
+  e = launch_named("flash_wide_q", wide_q_kernel<T, EP, DV>, dim3((p.NqP / 32) * p.B * p.Hq * kChunks), dim3(64), s,
+                   p, wq);
+  if (e != hipSuccess) return e;
+  const int nk = (p.NkP / 32) * p.B * p.Hk, nq = (p.NqP / 32) * p.B * p.Hq;
+  return launch_named("flash_wide_chain", wide_chain_kernel<T>, dim3(nk + nq), dim3(256), s, p,
+                      (const float*)wk, (const float*)wq, nk);
+}
+
+}  // namespace
+
+bool flash_wide_shape(int EP, int DV) { return DV == 256 && (EP == 256 || EP == 384 || EP == 512); }
+
+hipError_t launch_flash_wide_fwd(const FlashFwdParams& p, int dtype, hipStream_t s) {
+  if (!flash_wide_shape(p.EP, p.DV)) return hipErrorInvalidValue;
+  if (dtype == 2) {
+    if (p.EP == 256) return fwd_t<BF16, 256, 256>(p, s);
+    if (p.EP == 384) return fwd_t<BF16, 384, 256>(p, s);
+    return fwd_t<BF16, 512, 256>(p, s);
+  }
+  if (p.EP == 256) return fwd_t<F16, 256, 256>(p, s);
+  if (p.EP == 384) return fwd_t<F16, 384, 256>(p, s);
+  return fwd_t<F16, 512, 256>(p, s);
+}
+
+hipError_t launch_flash_wide_bwd(const FlashBwdParams& p, float* wk, float* wq, int dtype, hipStream_t s) {
+  if (!flash_wide_shape(p.EP, p.DV)) return hipErrorInvalidValue;
+  if (dtype == 2) {
+    if (p.EP == 256) return bwd_t<BF16, 256, 256>(p, wk, wq, s);
+    if (p.EP == 384) return bwd_t<BF16, 384, 256>(p, wk, wq, s);
+    return bwd_t<BF16, 512, 256>(p, wk, wq, s);
+  }
+  if (p.EP == 256) return bwd_t<F16, 256, 256>(p, wk, wq, s);
+  if (p.EP == 384) return bwd_t<F16, 384, 256>(p, wk, wq, s);
+  return bwd_t<F16, 512, 256>(p, wk, wq, s);
+}
+
+}  // namespace pope

@@ -160,18 +160,26 @@ hipError_t det_reduce(const pope_desc& d, const DetParts& dp, float* dfreqs, flo
 //   | key visibility words (B, NW) u64 | last visible key + 1 (B) int32
 //   | -lse * log2 e, -delta (B, Hq, NqP) fp32 each           backward only
 // with EP = round_up(D + R, 32), DV = round_up(D, 32), NqP / NkP = round_up(N, 256) (the backward's
-// jobs cover 256 rows), NW = NkP / 64.
+// jobs cover 256 rows), NW = NkP / 64.  Wide heads (D > 128, flash_wide.hip): EP =
+// round_up(D + R, 128), DV = 256, and the backward's workspace adds the raw expanded-row
+// gradients, fp32 (B, Hk, NkP, EP) and (B, Hq, NqP, EP), before the deterministic-mode region.
 void copy3(int64_t* dst, const int64_t* src);
 
 struct FlashLayout {
   int EP, DV, NqP, NkP, NW, Bt, Ht, Hb;
+  bool wide;
   size_t table, btab, kh, qh, mwords, kend, ld, total;
+  size_t wk, wq, wide_bytes;   // backward only, offsets past `total`
 };
+
+constexpr int kFlashMaxD = 128;       // head dims of the register-tiled kernels
+constexpr int kFlashWideMaxD = 256;   // head dims of the wide kernels
 
 FlashLayout flash_layout(const pope_desc& d) {
   FlashLayout L;
-  L.EP = round_up(d.D + d.R, 32);
-  L.DV = round_up(d.D, 32);
+  L.wide = d.D > kFlashMaxD;
+  L.EP = L.wide ? round_up(d.D + d.R, 128) : round_up(d.D + d.R, 32);
+  L.DV = L.wide ? 256 : round_up(d.D, 32);
   L.NqP = round_up(d.Nq, 256);
   L.NkP = round_up(d.Nk, 256);
   L.NW = L.NkP / 64;
@@ -187,12 +195,17 @@ FlashLayout flash_layout(const pope_desc& d) {
   L.kend = off;   off += align_up((size_t)d.B * sizeof(int32_t));
   L.ld = off;     off += align_up((size_t)d.B * d.Hq * L.NqP * sizeof(float2));
   L.total = off;
+  L.wk = off;
+  L.wq = L.wk + (L.wide ? align_up((size_t)d.B * d.Hk * L.NkP * L.EP * sizeof(float)) : 0);
+  L.wide_bytes = L.wide ? L.wq - L.wk + align_up((size_t)d.B * d.Hq * L.NqP * L.EP * sizeof(float)) : 0;
   return L;
 }
 
-// The backward's workspace extends the forward's by the deterministic-mode region.
+// The backward's workspace extends the forward's by the wide path's raw gradients and the
+// deterministic-mode region.
 size_t flash_ws(const pope_desc& d, int op) {
-  return flash_layout(d).total + (op == POPE_OP_FLASH_BWD ? det_bytes(d) : 0);
+  const FlashLayout L = flash_layout(d);
+  return L.total + (op == POPE_OP_FLASH_BWD ? L.wide_bytes + det_bytes(d) : 0);
 }
 
 // The flash kernels address the rows of v and do inside one (batch, head) with 32-bit element
@@ -336,7 +349,8 @@ int check_flash_common(const pope_desc* d, const void* q, const void* k, const v
   if (rc) return rc;
   if (d->dtype != POPE_BF16 && d->dtype != POPE_F16)
     return fail(POPE_ERR_UNSUPPORTED, "flash kernels take bf16 or fp16 (dtype %d)", d->dtype);
-  if (d->D > 128) return fail(POPE_ERR_UNSUPPORTED, "flash kernels cover head dim <= 128 (got %d)", d->D);
+  if (d->D > kFlashWideMaxD)
+    return fail(POPE_ERR_UNSUPPORTED, "flash kernels cover head dim <= %d (got %d)", kFlashWideMaxD, d->D);
   if (!q || !k || !v || !o || !lse) return fail(POPE_ERR_INVALID, "q, k, v, o and lse must be non-NULL");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return fail(POPE_ERR_INVALID, "q, k, v, o must be 16-byte aligned");
@@ -476,7 +490,7 @@ int pope_flash_fwd(const pope_desc* d, const void* q, const void* k, const void*
   p.nqb = (d->Nq + 127) / 128;
   copy3(p.v_s, d->v_s);
   copy3(p.o_s, d->o_s);
-  e = pope::launch_flash_fwd(p, d->dtype, s);
+  e = L.wide ? pope::launch_flash_wide_fwd(p, d->dtype, s) : pope::launch_flash_fwd(p, d->dtype, s);
   if (e == hipErrorInvalidValue)
     return fail(POPE_ERR_UNSUPPORTED, "no flash forward kernel for head dim %d, rotate dim %d", d->D, d->R);
   if (e != hipSuccess) return hip_fail(e, "flash forward launch");
@@ -499,7 +513,7 @@ int pope_flash_bwd(const pope_desc* d, const void* dout, const void* q, const vo
   if (d->flags & ~(POPE_FLAG_PREPARED | POPE_FLAG_ZERO_GRADS | POPE_FLAG_DETERMINISTIC))
     return fail(POPE_ERR_INVALID, "unknown flags 0x%x", (unsigned)d->flags);
   const FlashLayout L = flash_layout(*d);
-  if ((rc = check_ws(L.total + det_bytes(*d), workspace, workspace_bytes))) return rc;
+  if ((rc = check_ws(L.total + L.wide_bytes + det_bytes(*d), workspace, workspace_bytes))) return rc;
   if ((rc = check_row_span("v", L.NkP, d->v_s[2])) || (rc = check_row_span("do", L.NqP, d->do_s[2]))) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
@@ -549,10 +563,18 @@ int pope_flash_bwd(const pope_desc* d, const void* dout, const void* q, const vo
   p.mask_sb = d->mask_sb;
   p.t_sb = L.Bt > 1 ? (int64_t)L.Ht * d->Nk * d->R : 0;
   p.t_sh = L.Ht > 1 ? (int64_t)d->Nk * d->R : 0;
-  const DetParts dp = det_parts(*d, ws + L.total, dfreqs, dbias);
+  const DetParts dp = det_parts(*d, ws + L.total + L.wide_bytes, dfreqs, dbias);
   p.kpart = dp.kpart;
   p.qpart = dp.qpart;
-  hipError_t e = pope::launch_flash_bwd(p, d->dtype, s);
+  hipError_t e;
+  if (L.wide) {
+    e = pope::launch_flash_bwd_delta(p, d->dtype, s);
+    if (e == hipSuccess)
+      e = pope::launch_flash_wide_bwd(p, reinterpret_cast<float*>(ws + L.wk), reinterpret_cast<float*>(ws + L.wq),
+                                      d->dtype, s);
+  } else {
+    e = pope::launch_flash_bwd(p, d->dtype, s);
+  }
   if (e == hipErrorInvalidValue)
     return fail(POPE_ERR_UNSUPPORTED, "no flash backward kernel for head dim %d, rotate dim %d", d->D, d->R);
   if (e != hipSuccess) return hip_fail(e, "flash backward launch");

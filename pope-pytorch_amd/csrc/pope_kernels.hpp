@@ -103,6 +103,15 @@ struct FlashBwdParams {
   int64_t bias_sh, mask_sb, t_sb, t_sh;
 };
 hipError_t launch_flash_bwd(const FlashBwdParams& p, int dtype, hipStream_t s);
+// The backward's row terms alone (-lse log2 e and -delta per query row; dfreqs / dbias cleared
+// with zero_grads): the wide path's first launch.
+hipError_t launch_flash_bwd_delta(const FlashBwdParams& p, int dtype, hipStream_t s);
+
+// Wide heads (flash_wide.hip): DV = 256 and EP in {256, 384, 512}.  The backward takes two fp32
+// workspaces for the raw expanded-row gradients, wk (B, Hk, NkP, EP) and wq (B, Hq, NqP, EP).
+bool flash_wide_shape(int EP, int DV);
+hipError_t launch_flash_wide_fwd(const FlashFwdParams& p, int dtype, hipStream_t s);
+hipError_t launch_flash_wide_bwd(const FlashBwdParams& p, float* wk, float* wq, int dtype, hipStream_t s);
 
 struct SimParams {
   const float* q; const float* k; const float* dsim; float* sim;

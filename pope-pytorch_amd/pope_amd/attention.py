@@ -7,9 +7,10 @@ defaults, layouts (``head_dimension_at_first``), asserts and return values.
 
 Dispatch (reference :21-26, :63-71, :86): GPU tensors go to the HIP kernels of
 libpope_hip.so; if that library is missing the call raises -- there is no silent
-fallback.  Flash attention with heads wider than the flash kernels cover (128) runs
-with the polar transform materialised on the device (the polar transform kernel) and
-the attention products in fp32 (``_attend_materialised``).  The torch path (``fused=False`` or CPU tensors) is the reference's own
+fallback.  Flash attention covers head dims up to 256 (after padding to a multiple of 8)
+with its own kernels; wider heads run with the polar transform materialised on the
+device (the polar transform kernel) and the attention products in fp32
+(``_attend_materialised``).  The torch path (``fused=False`` or CPU tensors) is the reference's own
 non-fused computation, with the key-padding and causal masks combined into one
 explicit boolean mask so the result does not depend on the torch version's
 handling of ``attn_mask`` together with ``is_causal`` (reference :133-138).
@@ -42,9 +43,9 @@ def _to_head_first(*ts):
     return tuple(t.transpose(1, 2) for t in ts)
 
 
-# widest (padded) head dim of the fused flash kernels; flash_attn_with_pope takes wider heads
-# through its materialising path
-FLASH_MAX_HEAD_DIM = 128
+# widest (padded) head dim of the fused flash kernels (the register-tiled kernels up to 128, the
+# wide ones up to 256); flash_attn_with_pope takes wider heads through its materialising path
+FLASH_MAX_HEAD_DIM = 256
 
 
 def _flash_width(D, pos_emb):
@@ -72,7 +73,7 @@ def _keep_mask(mask, causal, Nq, Nk, device):
 
 
 def _attend_materialised(q, k, v, pos_emb, mask, causal, softmax_scale):
-    """Head-first PoPE attention for heads wider than the flash kernels cover: q_hat, k_hat from
+    """Head-first PoPE attention for heads wider than the flash kernels cover (above 256): q_hat, k_hat from
     apply_pope_to_qk (the polar transform kernel for GPU tensors), then the masked softmax
     attention of attention.py:106-145 with the scores and the value product in fp32 (explicit
     products with contiguous right operands).  A row with every key masked gives 0."""

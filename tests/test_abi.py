@@ -55,6 +55,13 @@ def test_workspace_sizes():
             + al(2 * 8 * 256 * 8))
     assert _ws(_lib.OP_FLASH_FWD, d) == (0, want)
     assert _ws(_lib.OP_FLASH_BWD, d) == (0, want)   # one layout: the backward reuses the forward's
+    # wide heads (D > 128): E rounded up to 128 (here 192 + 96 -> 384 columns); the backward adds the
+    # raw expanded-row gradients, fp32 (B, Hk, NkP, EP) and (B, Hq, NqP, EP)
+    dw = _desc(D=192, R=96)
+    want_w = (al(256 * 96 * 8) + al(8 * 96 * 8) + 2 * al(2 * 8 * 256 * 384 * 2) + al(2 * 4 * 8) + al(2 * 4)
+              + al(2 * 8 * 256 * 8))
+    assert _ws(_lib.OP_FLASH_FWD, dw) == (0, want_w)
+    assert _ws(_lib.OP_FLASH_BWD, dw) == (0, want_w + 2 * al(2 * 8 * 256 * 384 * 4))
     d3 = _desc(R=0, Nk=200)                          # no tables; K_hat rows padded to 256, E = 64
     want3 = 2 * al(2 * 8 * 256 * 64 * 2) + al(2 * 4 * 8) + al(2 * 4) + al(2 * 8 * 256 * 8)
     assert _ws(_lib.OP_FLASH_FWD, d3) == (0, want3)
@@ -111,8 +118,8 @@ def test_flash_rejects_bad_shapes(field, value, needle):
 def test_flash_rejects_bad_dtype_strides_pointers_workspace():
     d = _desc(dtype=_lib.POPE_F32)
     assert _flash_fwd(d) == 2 and "bf16 or fp16" in _lib.last_error()
-    d = _desc(D=256, R=0)
-    assert _flash_fwd(d) == 2 and "head dim <= 128" in _lib.last_error()
+    d = _desc(D=264, R=0)
+    assert _flash_fwd(d) == 2 and "head dim <= 256" in _lib.last_error()
     d = _desc()
     d.q_s[2] = 65
     assert _flash_fwd(d) == 1 and "stride" in _lib.last_error()

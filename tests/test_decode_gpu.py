@@ -162,3 +162,35 @@ def test_fp32_flash_rejects_values_beyond_fp16(cuda):
     q[0, 0, 0, 0] = 7.0e4
     with pytest.raises(ValueError, match="fp16"):
         pope_amd.flash_attn_with_pope(q, inp["k"], inp["v"], pos_emb=(inp["freqs"], inp["bias"]))
+
+
+def test_decode_shape_beyond_the_split_kernel(cuda):
+    """Nq = 1 with query heads x head dim = 8192, above what the split kernel stages in LDS (4096):
+    the call takes the general forward and must still match the oracle."""
+    inp = _decode_inputs(71, 2, 64, 16, 2048, 128, 64, torch.bfloat16)
+    res = _run(inp)
+    ref = oracle_attention(inp, False, grads=False)
+    err = max_abs(res["o"], ref["o"])
+    print(f"o={err:.2e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("lengths", [[0, 3000, 1], [1, 1, 1], [2048, 0, 2048], [5, 2048, 1000]],
+                         ids=["dead-long-one", "ones", "dead-middle", "mixed"])
+def test_decode_deal_edge_lengths(cuda, lengths):
+    """The split workgroups' deal of the visible keys: batches with no visible key (o = 0 and
+    lse = -inf from the plan launch), one key, and very unequal lengths side by side."""
+    from pope_amd.hip_pope_flash_attn import flash_attn_forward
+    B, H, Nk = len(lengths), 4, 3000
+    inp = _decode_inputs(73, B, H, H, Nk, 64, 64, torch.bfloat16, lengths=lengths)
+    tr = lambda t: t.transpose(1, 2)
+    o, lse = flash_attn_forward(tr(inp["q"]), tr(inp["k"]), tr(inp["v"]), inp["freqs"], inp["bias"], inp["mask"])
+    ref = oracle_attention(inp, False, grads=False)
+    assert max_abs(tr(o), ref["o"]) <= TOL
+    finite = torch.isfinite(ref["lse"])
+    assert torch.equal(torch.isfinite(lse.cpu()), finite)
+    if finite.any():
+        assert (lse.cpu()[finite] - ref["lse"][finite]).abs().max().item() <= TOL
+    for b, L in enumerate(lengths):
+        if L == 0:
+            assert tr(o)[b].abs().max().item() == 0.0

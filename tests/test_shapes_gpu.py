@@ -4,8 +4,9 @@ through the public API on the GPU vs the oracle.
 The reference's kernels take any D and R (Triton blocks of next_pow2(D) with a rotate mask,
 triton_pope.py:58-60, triton_pope_flash_attn.py:44,252).  Here the Python entry points pad such
 shapes on the device before the kernels run (pope_amd._pad; the padding itself is pinned on the
-CPU by test_pad_cpu.py), and flash_attn_with_pope takes heads wider than 128 through the
-materialising path (polar transform kernel, fp32 attention products).  Each case runs forward and
+CPU by test_pad_cpu.py).  Heads of 136 to 256 run the wide flash kernels (flash_wide.hip), through
+flash_attn_with_pope and the reference-named operators alike; heads wider than 256 take
+flash_attn_with_pope's materialising path (polar transform kernel, fp32 attention products).  Each case runs forward and
 backward (dfreqs / dbias included) against the float64 oracle on the same rounded inputs.
 Tolerances: 2e-2 absolute beyond the bf16 rounding of the exact value for bf16 outputs and
 per-element gradients, 2e-2 * max(1, ||ref||_inf) for the summed dbias / dfreqs; 1e-4 relative
@@ -93,12 +94,73 @@ def test_reference_operator_api_dims_not_multiple_of_8(cuda):
     _check(dict(o=back(o), dq=back(dq), dk=back(dk), dv=back(dv), dfreqs=dfreqs, dbias=dbias), ref, ALL)
 
 
+WIDE_CASES = [   # (B, Hq, Hk, Nq, Nk, D, R, causal, mask, dtype)
+    (1, 2, 1, 96, 96, 160, 32, True, "prefix", torch.bfloat16),
+    (1, 2, 2, 64, 64, 256, 64, False, "none", torch.bfloat16),
+    (2, 8, 1, 59, 60, 129, 88, True, "none", torch.bfloat16),   # 8 query heads per kv head
+    (2, 4, 2, 150, 300, 192, 192, False, "random", torch.bfloat16),   # E = 384, Nq < Nk
+    (1, 2, 2, 200, 200, 256, 256, True, "prefix", torch.float16),     # E = 512, full rotation
+    (2, 3, 3, 70, 70, 160, 0, False, "dead_row", torch.bfloat16),     # no rotation, a dead batch row
+]
+
+
+def _ran(names):
+    from pope_amd import _lib
+    ran = _lib.profile_read()
+    return {n for n in names if n in ran}
+
+
+@pytest.mark.parametrize("cfg", WIDE_CASES, ids=lambda c: "x".join(map(str, c[:9])) + "-" + str(c[9])[6:])
+def test_flash_wide_heads(cuda, cfg):
+    """Heads of 136 to 256: the wide flash kernels run (no materialised scores) and match the
+    oracle, forward and backward."""
+    from pope_amd import _lib
+    *shape, causal, mask, dtype = cfg
+    inp = make_pope_inputs(74, *shape, dtype, mask)
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    got = _api(inp, causal)
+    torch.cuda.synchronize()
+    _lib.profile_enable(False)
+    assert _ran(("flash_wide_fwd", "flash_wide_kv", "flash_wide_q", "flash_wide_chain")) == {
+        "flash_wide_fwd", "flash_wide_kv", "flash_wide_q", "flash_wide_chain"}
+    _check(got, oracle_attention(inp, causal), ALL)
+
+
+@pytest.mark.parametrize("D,R", [(160, 160), (192, 64), (256, 128)])
+def test_reference_operator_api_wide_heads(cuda, D, R):
+    """flash_attn / flash_attn_forward / flash_attn_backward / FlashAttnFunction in the (B, N, H, D)
+    layout at head dims 160, 192 and 256 (the reference's Triton flash takes any D,
+    triton_pope_flash_attn.py:252-254)."""
+    from pope_amd.hip_pope_flash_attn import FlashAttnFunction, flash_attn, flash_attn_backward, flash_attn_forward
+    inp = make_pope_inputs(75, 2, 4, 2, 120, 120, D, R, torch.bfloat16, "prefix")
+    ref = oracle_attention(inp, True)
+    tr = lambda x: x.detach().transpose(1, 2).contiguous()
+    back = lambda x: x.transpose(1, 2)
+    q, k, v, do = tr(inp["q"]), tr(inp["k"]), tr(inp["v"]), tr(inp["do"])
+    freqs, bias = inp["freqs"], inp["bias"]
+    o, lse = flash_attn_forward(q, k, v, freqs, bias, inp["mask"], causal=True)
+    assert max_abs(lse, ref["lse"]) <= 1e-2
+    dq, dk, dv = torch.zeros_like(q), torch.empty_like(k), torch.empty_like(v)
+    dfreqs, dbias = torch.zeros_like(freqs), torch.zeros_like(bias)
+    flash_attn_backward(do, q, k, v, o, lse, dq, dk, dv, dfreqs, dbias, freqs, bias, inp["mask"], causal=True)
+    _check(dict(o=back(o), dq=back(dq), dk=back(dk), dv=back(dv), dfreqs=dfreqs, dbias=dbias), ref, ALL)
+    # the autograd entry points
+    for fn in (flash_attn, FlashAttnFunction.apply):
+        t = [x.clone().requires_grad_(True) for x in (q, k, v)]
+        fb = [freqs.clone().requires_grad_(True), bias.clone().requires_grad_(True)]
+        o2 = fn(t[0], t[1], t[2], fb[0], fb[1], inp["mask"], True)
+        o2.backward(do)
+        _check(dict(o=back(o2), dq=back(t[0].grad), dk=back(t[1].grad), dv=back(t[2].grad), dfreqs=fb[0].grad,
+                    dbias=fb[1].grad), ref, ALL)
+
+
 @pytest.mark.parametrize("cfg", [
-    (1, 2, 1, 96, 96, 160, 32, True, "prefix"),
-    (1, 2, 2, 64, 64, 256, 64, False, "none"),
-    (2, 8, 1, 59, 60, 129, 88, True, "none"),   # 8 query heads per kv head: dv summed over the group in fp32
+    (1, 2, 1, 64, 64, 264, 32, True, "prefix"),
+    (1, 2, 2, 40, 40, 300, 300, False, "none"),
 ], ids=lambda c: "x".join(map(str, c)))
 def test_flash_heads_wider_than_kernels(cuda, cfg):
+    """Heads wider than 256: flash_attn_with_pope's materialising path."""
     *shape, causal, mask = cfg
     inp = make_pope_inputs(74, *shape, torch.bfloat16, mask)
     _check(_api(inp, causal), oracle_attention(inp, causal), ALL)
