@@ -58,17 +58,29 @@ __device__ __forceinline__ f32x16 splat16(float x) {
 // Row offset within a 32-row block of register r of a 32x32 MFMA result in lane half hf.
 __device__ __forceinline__ int res_row(int r, int hf) { return 8 * (r >> 2) + 4 * hf + (r & 3); }
 
-// Stages rows [r0, r0 + 32) of a 16-bit row-major source (row stride rs elements) into a
-// row-major LDS tile of `cols` columns: rows past row_last repeat it, 8-column chunks at or past
-// `dlim` are zero (head columns past D).  One wave.
+// Stages rows [r0, r0 + 32) of a 16-bit row-major source (row stride rs elements) into an LDS
+// tile of `cols` columns, unpadded with the 16-byte units XOR-swizzled by the row (tile_swz: row
+// reads and transposed reads of MFMA operands are then free of bank conflicts): rows past
+// row_last repeat it, 8-column chunks at or past `dlim` are zero (head columns past D).  One
+// wave; four loads in flight before their stores.
 template <int COLS>
 __device__ __forceinline__ void stage32(uint16_t* lds, const uint16_t* src, int64_t rs, int r0, int row_last,
                                         int dlim) {
-  constexpr int U = COLS / 8;
-  for (int c = threadIdx.x; c < 32 * U; c += 64) {
-    const int r = c / U, d0 = 8 * (c % U);
-    const u32x4 v = d0 < dlim ? ld16(src + (int64_t)min(r0 + r, row_last) * rs + d0) : zero4();
-    *reinterpret_cast<u32x4*>(lds + r * COLS + d0) = v;
+  constexpr int U = COLS / 8, N = 32 * U / 64, G = 4;
+  static_assert(N % G == 0, "whole load groups");
+#pragma unroll
+  for (int i0 = 0; i0 < N; i0 += G) {
+    u32x4 v[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int c = threadIdx.x + 64 * (i0 + i), r = c / U, d0 = 8 * (c % U);
+      v[i] = d0 < dlim ? ld16(src + (int64_t)min(r0 + r, row_last) * rs + d0) : zero4();
+    }
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int c = threadIdx.x + 64 * (i0 + i), r = c / U, u = c % U;
+      *reinterpret_cast<u32x4*>(lds + r * COLS + 8 * (u ^ tile_swz(U, r))) = v[i];
+    }
   }
 }
 
@@ -98,7 +110,7 @@ __global__ __launch_bounds__(64) void wide_fwd_kernel(FlashFwdParams p) {
   const uint16_t* khb = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;
   const uint16_t* vb = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
   cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
-  const TrLane tl = tr_lane<false>(DV, lane);
+  const TileOffsets<DV / 8> vo(lane);
 
   f32x16 oacc[NDB];
 #pragma unroll
@@ -145,8 +157,8 @@ __global__ __launch_bounds__(64) void wide_fwd_kernel(FlashFwdParams p) {
       for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
 #pragma unroll
       for (int g = 0; g < 2; ++g)
-        oacc[db] = T::mfma32(as_vec8<vec8>(lds_operand_tr(vt, tl, DV, 16 * g, 32 * db)), as_vec8<vec8>(pw[g]),
-                             oacc[db]);
+        oacc[db] = T::mfma32(as_vec8<vec8>(lds_tr8(vt, vo.lo_at(db) + 16 * g * DV, vo.hi_at(db) + 16 * g * DV)),
+                             as_vec8<vec8>(pw[g]), oacc[db]);
     }
     __syncthreads();   // every V read of this tile is done before the next tile is staged
   }
@@ -205,7 +217,8 @@ __global__ __launch_bounds__(64) void wide_kv_kernel(FlashBwdParams p, float* wk
   for (int x = 0; x < EBC; ++x) dka[x] = splat16(0.f);
 #pragma unroll
   for (int x = 0; x < DBC; ++x) dva[x] = splat16(0.f);
-  const TrLane tq = tr_lane<false>(EP, lane), td = tr_lane<false>(DV, lane);
+  const TileOffsets<EP / 8> qo(lane);
+  const TileOffsets<DV / 8> dO(lane);
 
   if (__any(kvis)) {
     const int groups = p.Hq / p.Hk;
@@ -234,11 +247,19 @@ __global__ __launch_bounds__(64) void wide_kv_kernel(FlashBwdParams p, float* wk
         // S = Q_hat K_hat^T - lse and dP = dO V^T - delta (rows = queries, lane = key)
         f32x16 s = nl16, dp = nd16;
 #pragma unroll
-        for (int kk = 0; kk < KS; ++kk)
-          s = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(qt + lr * EP + 16 * kk + 8 * hf)), kreg[kk], s);
+        for (int kg = 0; kg < KS; kg += 8) {
 #pragma unroll
-        for (int kk = 0; kk < DS; ++kk)
-          dp = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(dt + lr * DV + 16 * kk + 8 * hf)), vreg[kk], dp);
+          for (int kk = kg; kk < kg + 8; ++kk)
+            s = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(qt + qo.row_at(kk))), kreg[kk], s);
+          __builtin_amdgcn_sched_barrier(0);   // eight operand reads in flight, not all of them
+        }
+#pragma unroll
+        for (int kg = 0; kg < DS; kg += 8) {
+#pragma unroll
+          for (int kk = kg; kk < kg + 8; ++kk)
+            dp = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(dt + dO.row_at(kk))), vreg[kk], dp);
+          __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const bool ok = kvis && (!p.causal || kj <= q0 + res_row(r, hf));
@@ -250,11 +271,17 @@ __global__ __launch_bounds__(64) void wide_kv_kernel(FlashBwdParams p, float* wk
         for (int g2 = 0; g2 < 2; ++g2) {
           const vec8 ap = as_vec8<vec8>(pack8w<T>(s, g2)), ads = as_vec8<vec8>(pack8w<T>(dp, g2));
 #pragma unroll
-          for (int db = 0; db < DBC; ++db)
-            dva[db] = T::mfma32(ap, as_vec8<vec8>(lds_operand_tr(dt, td, DV, 16 * g2, 32 * (ec * DBC + db))), dva[db]);
+          for (int db = 0; db < DBC; ++db) {
+            const int nb = ec * DBC + db;
+            dva[db] = T::mfma32(ap, as_vec8<vec8>(lds_tr8(dt, dO.lo_at(nb) + 16 * g2 * DV, dO.hi_at(nb) + 16 * g2 * DV)),
+                                dva[db]);
+          }
 #pragma unroll
-          for (int eb = 0; eb < EBC; ++eb)
-            dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_operand_tr(qt, tq, EP, 16 * g2, 32 * (ec * EBC + eb))), dka[eb]);
+          for (int eb = 0; eb < EBC; ++eb) {
+            const int nb = ec * EBC + eb;
+            dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_tr8(qt, qo.lo_at(nb) + 16 * g2 * EP, qo.hi_at(nb) + 16 * g2 * EP)),
+                                dka[eb]);
+          }
         }
         __syncthreads();   // every tile read is done before the next tiles are staged
       }
@@ -317,21 +344,25 @@ __global__ __launch_bounds__(64) void wide_q_kernel(FlashBwdParams p, float* wq)
   const uint16_t* khb = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;
   const uint16_t* vb = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
   cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
-  const TrLane tk = tr_lane<false>(EP, lane);
+  const TileOffsets<EP / 8> ko(lane);
   for (int j0 = 0; j0 < nkeys; j0 += 32) {
     stage32<EP>(kt, khb, EP, j0, p.NkP - 1, EP);
     __syncthreads();   // the tile's stores are complete
     // S^T = K_hat Q_hat^T - lse and dP^T = V dO^T - delta (rows = keys, lane = query)
+    const uint16_t* vr = vb + (int64_t)min(j0 + lr, Nk - 1) * p.v_s[2] + 8 * hf;
+    u32x4 va[DS];
+#pragma unroll
+    for (int kk = 0; kk < DS; ++kk) va[kk] = 16 * kk + 8 * hf < D ? ld16(vr + 16 * kk) : zero4();
     f32x16 s = splat16(nls), dp = splat16(nds);
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk)
-      s = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt + lr * EP + 16 * kk + 8 * hf)), qreg[kk], s);
-    const uint16_t* vr = vb + (int64_t)min(j0 + lr, Nk - 1) * p.v_s[2] + 8 * hf;
+    for (int kg = 0; kg < KS; kg += 8) {
 #pragma unroll
-    for (int kk = 0; kk < DS; ++kk) {
-      const u32x4 va = 16 * kk + 8 * hf < D ? ld16(vr + 16 * kk) : zero4();
-      dp = T::mfma32(as_vec8<vec8>(va), doreg[kk], dp);
+      for (int kk = kg; kk < kg + 8; ++kk)
+        s = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt + ko.row_at(kk))), qreg[kk], s);
+      __builtin_amdgcn_sched_barrier(0);   // eight operand reads in flight, not all of them
     }
+#pragma unroll
+    for (int kk = 0; kk < DS; ++kk) dp = T::mfma32(as_vec8<vec8>(va[kk]), doreg[kk], dp);
     const uint32_t wv = (uint32_t)(mw[j0 >> 6] >> (j0 & 32));
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -344,7 +375,9 @@ __global__ __launch_bounds__(64) void wide_q_kernel(FlashBwdParams p, float* wq)
       const vec8 bds = as_vec8<vec8>(pack8w<T>(dp, g2));
 #pragma unroll
       for (int eb = 0; eb < EBC; ++eb)
-        dqa[eb] = T::mfma32(as_vec8<vec8>(lds_operand_tr(kt, tk, EP, 16 * g2, 32 * (ec * EBC + eb))), bds, dqa[eb]);
+        dqa[eb] = T::mfma32(
+            as_vec8<vec8>(lds_tr8(kt, ko.lo_at(ec * EBC + eb) + 16 * g2 * EP, ko.hi_at(ec * EBC + eb) + 16 * g2 * EP)),
+            bds, dqa[eb]);
     }
     __syncthreads();   // every tile read is done before the next tile is staged
   }

@@ -2,7 +2,7 @@
 
 Each case draws its shape from its own seeded generator, so the case list and every input are fixed; the case id
 names the shape.  Flash forward + backward: batch 1-2, up to 8 query heads over 1, 2 or 4 kv heads, Nq <= Nk up
-to 700, head dims 8-136 and 160 / 192 (the materialised route), rotate dims 0..D whether or not multiples of 8,
+to 700, head dims 8-136 and 160 / 192, plus 32 cases with head dims 137-256 (the wide kernels; up to 400 keys), rotate dims 0..D whether or not multiples of 8,
 bf16 and fp16, causal or not, no / prefix / random / half masks, both layouts, 2-D or per-batch 3-D freqs.  Decode:
 up to 32 query heads, 1,024-6,000 keys, views into a longer KV cache, per-batch positions.  Similarity (both
 product paths) and the polar transform: ragged sizes, grouped heads, odd dims.
@@ -54,6 +54,20 @@ def _flash_case(i):
                 per_batch=rng.random() < 0.3)
 
 
+def _wide_case(i):
+    """Heads of 137 to 256 (the wide flash kernels), with the same draws otherwise."""
+    rng = random.Random(7900 + i)
+    Hk = rng.choice([1, 2])
+    Hq = Hk * rng.choice([1, 2, 4])
+    Nk = rng.randint(1, 400)
+    Nq = Nk if rng.random() < 0.5 else rng.randint(1, Nk)
+    D = rng.randint(137, 256)
+    return dict(seed=7900 + i, B=rng.choice([1, 2]), Hq=Hq, Hk=Hk, Nq=Nq, Nk=Nk, D=D, R=_rot(rng, D),
+                dtype=rng.choice([torch.bfloat16, torch.float16]), causal=rng.random() < 0.5,
+                mask=rng.choice(["none", "prefix", "random", "half"]), head_first=rng.random() < 0.6,
+                per_batch=rng.random() < 0.3)
+
+
 def _decode_case(i):
     rng = random.Random(7300 + i)
     Hk = rng.choice([1, 2, 4, 8])
@@ -87,7 +101,7 @@ def _cid(c):
     return "-".join(f"{k}{str(v).replace('torch.', '')}" for k, v in c.items() if k != "seed")
 
 
-FLASH = [_flash_case(i) for i in range(200)]
+FLASH = [_flash_case(i) for i in range(200)] + [_wide_case(i) for i in range(32)]
 DECODE = [_decode_case(i) for i in range(64)]
 SIM = [_sim_case(i) for i in range(64)]
 POLAR = [_polar_case(i) for i in range(64)]
