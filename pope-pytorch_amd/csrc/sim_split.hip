@@ -14,8 +14,10 @@
 //                    reference's rounding of the key phase fl(F_j + bias), pope.py:56) split
 //                    into hi / lo bf16 planes, row-major (forward) or transposed (backward);
 //   sim_split_fwd  : S = Q_hat K_hat^T, one 128 x 128 tile per workgroup;
-//   sim_split_u    : U = G K_hat (G = dS read from HBM and split on the fly);
-//   sim_split_w    : W = G^T Q_hat (G tiles split once per workgroup into LDS, transposed).
+//   sim_split_uw   : U = G K_hat (u_job: G = dS rows read from HBM and split on the fly) and
+//                    W = G^T Q_hat (w_job: G tiles split once per workgroup into LDS, transposed),
+//                    in one launch whose job order lets the second read of G hit the last-level
+//                    cache.
 // The chain rule of the polar transform then runs in sim.hip's finalize kernel on U and W.
 #include "pope_common.hpp"
 #include "pope_kernels.hpp"
@@ -290,13 +292,11 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p,
 // K_hat^T tile's loads before the step's G loads: the wait for the tile at the end of a step
 // (vmcnt counts in issue order) then leaves kGPre steps of G in flight.  Steps left over after
 // whole rounds of kGPre take a guarded tail loop.
+// One job: (half, column block ec, query block ib, batch * head bh); ts: two LDS tiles.
 template <bool VEC>
-__global__ __launch_bounds__(kThreads, 2) void sim_split_u_kernel(SimParams p, SimSplit sp, float* U, int nib, int nec) {
-  __shared__ __attribute__((aligned(16))) uint16_t ts[2][kTile];
+__device__ __forceinline__ void u_job(const SimParams& p, const SimSplit& sp, float* U, int half, int ec, int ib, int bh,
+                                      uint16_t (*ts)[kTile]) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int half = id & 1, rest = id >> 1;
-  const int ec = rest % nec, ib = (rest / nec) % nib, bh = rest / (nec * nib);
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const int Nq = p.Nq, Nk = p.Nk, EP = p.EP;
   const int i = ib * 128 + 32 * wave + lr;
@@ -408,13 +408,11 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_u_kernel(SimParams p, S
 // is one 16-byte LDS read per plane; the transposed Q_hat planes (128 columns e x 32 queries)
 // go through LDS the same way.  Both double-buffered.  Wave w owns keys 32 w .. 32 w + 31 and
 // all four column blocks.
-__global__ __launch_bounds__(kThreads, 2) void sim_split_w_kernel(SimParams p, SimSplit sp, float* W, int njb, int nec) {
-  __shared__ __attribute__((aligned(16))) uint16_t gs[2][kTile];   // G^T tiles (key-major)
-  __shared__ __attribute__((aligned(16))) uint16_t qs[2][kTile];   // Q_hat^T tiles (column-major)
+// One job: (half, column block ec, key block jb, batch * kv head bhk); gs: two G^T tiles
+// (key-major), qs: two Q_hat^T tiles (column-major).
+__device__ __forceinline__ void w_job(const SimParams& p, const SimSplit& sp, float* W, int half, int ec, int jb,
+                                      int bhk, uint16_t (*gs)[kTile], uint16_t (*qs)[kTile]) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int half = id & 1, rest = id >> 1;
-  const int ec = rest % nec, jb = (rest / nec) % njb, bhk = rest / (nec * njb);
   const int b = bhk / p.Hk, hk = bhk % p.Hk;
   const int Nq = p.Nq, Nk = p.Nk, EP = p.EP;
   const int groups = p.Hq / p.Hk;
@@ -523,6 +521,33 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_w_kernel(SimParams p, S
   }
 }
 
+// Both passes in one launch.  Logical ids run over units of (batch, kv head): a unit holds the U
+// jobs of the kv head's query heads and the W jobs of the kv head, interleaved, so the two jobs
+// that read a block of G run at about the same time (xcd_remap keeps a unit's jobs on one XCD).
+// The G of the units in flight (16.8 MB per head at 2048 x 2048) stays in the 256 MB last-level
+// cache (Infinity Cache) between its two reads, so G crosses HBM about once.  The LDS of a
+// workgroup is the larger of the two jobs' needs (four tiles, 80 KB; two workgroups per CU).
+template <bool VEC>
+__global__ __launch_bounds__(kThreads, 2) void sim_split_uw_kernel(SimParams p, SimSplit sp, float* U, float* W,
+                                                                   int nib, int njb, int nec) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[4][kTile];
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int groups = p.Hq / p.Hk;
+  const int nu = 2 * nec * nib * groups, nw = 2 * nec * njb;   // jobs per unit
+  const int unit = id / (nu + nw), r = id % (nu + nw);
+  const int b = unit / p.Hk, hk = unit % p.Hk;
+  const int m = min(nu, nw);
+  const bool is_u = r < 2 * m ? !(r & 1) : nu > nw;
+  const int k = r < 2 * m ? r >> 1 : r - m;
+  const int half = k & 1, rest = k >> 1;
+  if (is_u) {
+    const int ec = rest % nec, ib = (rest / nec) % nib, g = rest / (nec * nib);
+    u_job<VEC>(p, sp, U, half, ec, ib, b * p.Hq + g * p.Hk + hk, lds);
+  } else {
+    w_job(p, sp, W, half, rest % nec, rest / nec, b * p.Hk + hk, lds, lds + 2);
+  }
+}
+
 }  // namespace
 
 hipError_t launch_sim_split_prep(const SimParams& p, const SimSplit& sp, int transposed, hipStream_t s) {
@@ -549,15 +574,12 @@ hipError_t launch_sim_split_bwd(const SimParams& p, const SimSplit& sp, float* U
   if (e != hipSuccess) return e;
   const int nec = (p.EP + 127) / 128;
   const int nib = (p.Nq + 127) / 128, njb = (p.Nk + 127) / 128;
-  const dim3 ugrid(2 * nib * nec * p.B * p.Hq);
+  const dim3 grid((2 * nec * nib * (p.Hq / p.Hk) + 2 * nec * njb) * p.B * p.Hk);
   // VEC needs Nk % 8 == 0: every 8-key chunk then lies wholly inside or wholly past the row, so a
   // clamped chunk is only ever one whose entries are all zeroed
   e = p.g_vec && p.Nk % 8 == 0
-          ? launch_named("sim_split_u", sim_split_u_kernel<true>, ugrid, dim3(kThreads), s, p, sp, U, nib, nec)
-          : launch_named("sim_split_u", sim_split_u_kernel<false>, ugrid, dim3(kThreads), s, p, sp, U, nib, nec);
-  if (e != hipSuccess) return e;
-  e = launch_named("sim_split_w", sim_split_w_kernel, dim3(2 * njb * nec * p.B * p.Hk), dim3(kThreads), s, p, sp, W,
-                   njb, nec);
+          ? launch_named("sim_split_uw", sim_split_uw_kernel<true>, grid, dim3(kThreads), s, p, sp, U, W, nib, njb, nec)
+          : launch_named("sim_split_uw", sim_split_uw_kernel<false>, grid, dim3(kThreads), s, p, sp, U, W, nib, njb, nec);
   if (e != hipSuccess) return e;
   return launch_sim_finalize(p, U, sp.U2, W, sp.W2, s);
 }
