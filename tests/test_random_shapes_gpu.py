@@ -2,8 +2,8 @@
 
 Each case draws its shape from its own seeded generator, so the case list and every input are fixed; the case id
 names the shape.  Flash forward + backward: batch 1-2, up to 8 query heads over 1, 2 or 4 kv heads, Nq <= Nk up
-to 700, head dims 8-136 and 160 / 192, plus 32 cases with head dims 137-256 (the wide kernels; up to 400 keys), rotate dims 0..D whether or not multiples of 8,
-bf16 and fp16, causal or not, no / prefix / random / half masks, both layouts, 2-D or per-batch 3-D freqs.  Decode:
+to 700, head dims 8-136 and 160 / 192, plus 32 cases with head dims 137-256 and up to 400 keys (head dims above
+128 run the wide-head kernels), rotate dims 0..D whether or not multiples of 8, bf16 and fp16, causal or not, no / prefix / random / half masks, both layouts, 2-D or per-batch 3-D freqs.  Decode:
 up to 32 query heads, 1,024-6,000 keys, views into a longer KV cache, per-batch positions.  Similarity (both
 product paths) and the polar transform: ragged sizes, grouped heads, odd dims.
 
