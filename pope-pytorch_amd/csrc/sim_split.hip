@@ -19,6 +19,8 @@
 //                    in one launch whose job order lets the second read of G hit the last-level
 //                    cache.
 // The chain rule of the polar transform then runs in sim.hip's finalize kernel on U and W.
+#include <type_traits>
+
 #include "pope_common.hpp"
 #include "pope_kernels.hpp"
 #include "sim_phase.hpp"
@@ -185,14 +187,17 @@ constexpr int kLd = 40;
 constexpr int kTile = 2 * 128 * kLd;   // bf16 per tile (both planes)
 
 // Loads rows [0, 128) x k values [k0, k0 + 32) of two planes (row stride rs elements); rows at
-// or past nrows read as zero.
+// or past nrows (nrows >= 1) read as zero.
 __device__ __forceinline__ void tile_load(const uint16_t* ph, const uint16_t* pl, int64_t rs, int k0, int nrows,
                                           u32x4* v, int tid) {
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const int c = tid + kThreads * m, plane = c >> 9, row = (c >> 2) & 127, kc = c & 3;
     const uint16_t* base = plane ? pl : ph;
-    v[m] = row < nrows ? ld16(base + row * rs + k0 + 8 * kc) : u32x4{0u, 0u, 0u, 0u};
+    // branch-free: rows past nrows read the last row and are zeroed, so the compiler counts the
+    // loads and waits only for the ones a use needs
+    const u32x4 x = ld16(base + min(row, nrows - 1) * rs + k0 + 8 * kc);
+    v[m] = row < nrows ? x : u32x4{0u, 0u, 0u, 0u};
   }
 }
 __device__ __forceinline__ void tile_store(uint16_t* t, const u32x4* v, int tid) {
@@ -410,6 +415,7 @@ __device__ __forceinline__ void u_job(const SimParams& p, const SimSplit& sp, fl
 // all four column blocks.
 // One job: (half, column block ec, key block jb, batch * kv head bhk); gs: two G^T tiles
 // (key-major), qs: two Q_hat^T tiles (column-major).
+template <bool VEC>
 __device__ __forceinline__ void w_job(const SimParams& p, const SimSplit& sp, float* W, int half, int ec, int jb,
                                       int bhk, uint16_t (*gs)[kTile], uint16_t (*qs)[kTile]) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
@@ -426,7 +432,6 @@ __device__ __forceinline__ void w_job(const SimParams& p, const SimSplit& sp, fl
   // global load reads eight 128-byte row segments.
   const int c = tid >> 3, rg = tid & 7;
   const int jq = jb * 128 + 4 * c;
-  const bool vec = p.g_vec && jq + 3 < Nk;
 
   f32x16 acc[4];
 #pragma unroll
@@ -442,15 +447,17 @@ __device__ __forceinline__ void w_job(const SimParams& p, const SimSplit& sp, fl
       const int ii = i0 + 4 * rg + t;
       const float* row = gb + (int64_t)min(ii, Nq - 1) * p.sim_s[2];
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (ii < Nq) {
-        if (vec) {
-          v = *reinterpret_cast<const float4*>(row + jq);
-        } else {
-          v.x = jq < Nk ? row[jq] : 0.f;
-          v.y = jq + 1 < Nk ? row[jq + 1] : 0.f;
-          v.z = jq + 2 < Nk ? row[jq + 2] : 0.f;
-          v.w = jq + 3 < Nk ? row[jq + 3] : 0.f;
-        }
+      if constexpr (VEC) {
+        // 4-wide and branch-free (16-byte aligned rows, Nk a multiple of 8: a key quad lies wholly
+        // inside or wholly past the row; one past it reads the last quad and is zeroed), so the wait
+        // before a step's stores covers only that step's loads
+        v = *reinterpret_cast<const float4*>(row + min(jq, Nk - 4));
+        if (ii >= Nq || jq >= Nk) v = make_float4(0.f, 0.f, 0.f, 0.f);
+      } else if (ii < Nq) {
+        v.x = jq < Nk ? row[jq] : 0.f;
+        v.y = jq + 1 < Nk ? row[jq + 1] : 0.f;
+        v.z = jq + 2 < Nk ? row[jq + 2] : 0.f;
+        v.w = jq + 3 < Nk ? row[jq + 3] : 0.f;
       }
       g[t] = v;
     }
@@ -475,37 +482,45 @@ __device__ __forceinline__ void w_job(const SimParams& p, const SimSplit& sp, fl
     const int64_t qo = ((int64_t)(b * p.Hq + h) * EP + ec * 128) * sp.NqP;
     tile_load(sp.qh + qo, sp.ql + qo, sp.NqP, i0, erows, v, tid);
   };
-  float4 gr[4];
-  u32x4 vq[4];
-  if (s0 < s1) {
-    load_g(s0, gr);
-    load_q(s0, vq);
-    store_g(gs[0], gr);
-    tile_store(qs[0], vq, tid);
-  }
-  __syncthreads();
-  for (int st = s0; st < s1; ++st) {
-    const int buf = (st - s0) & 1;
-    if (st + 1 < s1) {
-      load_g(st + 1, gr);
-      load_q(st + 1, vq);
-    }
+  // Two steps in flight: at step st the LDS buffer (st - s0) & 1 holds step st, register set
+  // (st - s0 + 1) & 1 step st + 1 (stored to the other buffer at the end of the step) and the other
+  // set receives step st + 2 (clamped to the last step: the same loads every step).
+  float4 gr[2][4];
+  u32x4 vq[2][4];
+  auto fetch = [&](int st, int k) {
+    load_g(min(st, s1 - 1), gr[k]);
+    load_q(min(st, s1 - 1), vq[k]);
+  };
+  auto step = [&](int st, auto kc) {
+    constexpr int K = decltype(kc)::value;
+    fetch(st + 2, K);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       u32x4 ah, al;
-      tile_frag(gs[buf], 32 * wave, u, lr, hf, ah, al);
+      tile_frag(gs[K], 32 * wave, u, lr, hf, ah, al);
 #pragma unroll
       for (int y = 0; y < 4; ++y) {
         u32x4 bh16, bl16;
-        tile_frag(qs[buf], 32 * y, u, lr, hf, bh16, bl16);
+        tile_frag(qs[K], 32 * y, u, lr, hf, bh16, bl16);
         acc[y] = mfma3(ah, al, bh16, bl16, acc[y]);
       }
     }
-    if (st + 1 < s1) {
-      store_g(gs[buf ^ 1], gr);
-      tile_store(qs[buf ^ 1], vq, tid);
-    }
+    store_g(gs[K ^ 1], gr[K ^ 1]);   // the last step's copy is never read
+    tile_store(qs[K ^ 1], vq[K ^ 1], tid);
     __syncthreads();
+  };
+  if (s0 < s1) {
+    fetch(s0, 0);
+    fetch(s0 + 1, 1);
+    store_g(gs[0], gr[0]);
+    tile_store(qs[0], vq[0], tid);
+    __syncthreads();
+    int st = s0;
+    for (; st + 1 < s1; st += 2) {
+      step(st, std::integral_constant<int, 0>{});
+      step(st + 1, std::integral_constant<int, 1>{});
+    }
+    if (st < s1) step(st, std::integral_constant<int, 0>{});
   }
 
   float* wb = (half ? sp.W2 : W) + (int64_t)bhk * Nk * EP;
@@ -544,7 +559,7 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_uw_kernel(SimParams p, 
     const int ec = rest % nec, ib = (rest / nec) % nib, g = rest / (nec * nib);
     u_job<VEC>(p, sp, U, half, ec, ib, b * p.Hq + g * p.Hk + hk, lds);
   } else {
-    w_job(p, sp, W, half, rest % nec, rest / nec, b * p.Hk + hk, lds, lds + 2);
+    w_job<VEC>(p, sp, W, half, rest % nec, rest / nec, b * p.Hk + hk, lds, lds + 2);
   }
 }
 
