@@ -187,17 +187,16 @@ constexpr int kLd = 40;
 constexpr int kTile = 2 * 128 * kLd;   // bf16 per tile (both planes)
 
 // Loads rows [0, 128) x k values [k0, k0 + 32) of two planes (row stride rs elements); rows at
-// or past nrows (nrows >= 1) read as zero.
+// or past nrows (nrows >= 1) repeat the last row.  Such rows only reach output columns that the
+// callers never store (expanded columns past EP), and loads without a select on their values
+// leave each wait to the instruction that first uses them.
 __device__ __forceinline__ void tile_load(const uint16_t* ph, const uint16_t* pl, int64_t rs, int k0, int nrows,
                                           u32x4* v, int tid) {
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const int c = tid + kThreads * m, plane = c >> 9, row = (c >> 2) & 127, kc = c & 3;
     const uint16_t* base = plane ? pl : ph;
-    // branch-free: rows past nrows read the last row and are zeroed, so the compiler counts the
-    // loads and waits only for the ones a use needs
-    const u32x4 x = ld16(base + min(row, nrows - 1) * rs + k0 + 8 * kc);
-    v[m] = row < nrows ? x : u32x4{0u, 0u, 0u, 0u};
+    v[m] = ld16(base + min(row, nrows - 1) * rs + k0 + 8 * kc);
   }
 }
 __device__ __forceinline__ void tile_store(uint16_t* t, const u32x4* v, int tid) {
