@@ -127,6 +127,7 @@ __global__ __launch_bounds__(kThreads, 2) void sim_fwd_kernel(SimParams p, int n
   }
   // S^T layout: acc lane = key column (lr), registers = query rows.
   // Here A = Q (rows i) and B = K (cols j): result lane <-> j, regs <-> i.
+  // non-temporal stores: S is not read again by this path and stays out of the caches
   float* sbase = p.sim + (int64_t)b * p.sim_s[0] + (int64_t)h * p.sim_s[1];
 #pragma unroll
   for (int x = 0; x < 2; ++x)
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(kThreads, 2) void sim_fwd_kernel(SimParams p, int n
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int i = i0 + wr + 32 * x + 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (i < Nq && j < Nk) sbase[(int64_t)i * p.sim_s[2] + j] = acc[x][y][r];
+        if (i < Nq && j < Nk) __builtin_nontemporal_store(acc[x][y][r], sbase + (int64_t)i * p.sim_s[2] + j);
       }
     }
 }

@@ -269,6 +269,9 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p,
     __syncthreads();
   }
 
+  // S is written with non-temporal stores: its 4 bytes per (i, j) are not read again by this
+  // path, and kept out of the caches they leave the operand planes and dS of the neighbouring
+  // launches cached (C2: the step's other kernels ran 10-15 us faster)
   float* sbase = p.sim + (int64_t)b * p.sim_s[0] + (int64_t)h * p.sim_s[1];
   const int i0 = ib * 128 + wr, j0 = jb * 128 + wc;
 #pragma unroll
@@ -279,7 +282,7 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p,
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int i = i0 + 32 * x + 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (i < p.Nq && j < p.Nk) sbase[(int64_t)i * p.sim_s[2] + j] = acc[x][y][r];
+        if (i < p.Nq && j < p.Nk) __builtin_nontemporal_store(acc[x][y][r], sbase + (int64_t)i * p.sim_s[2] + j);
       }
     }
 }
