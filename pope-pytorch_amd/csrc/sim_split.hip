@@ -30,7 +30,6 @@ namespace pope {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kGPre = 3;   // steps of G in flight in the U pass
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
@@ -290,28 +289,30 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p,
 // U[b,h,i,e] = sum_j G[b,h,i,j] K_hat[b,hk,j,e] over half of the keys (two halves, the second
 // into sp.U2: twice the waves of one full pass; the finalize adds them).  One workgroup = 128
 // query rows x 128 expanded columns; wave w owns rows 32 w .. 32 w + 31 and all four column
-// blocks, so each G value is loaded and split once.  A = G rows (lane = row, 8 consecutive
-// keys, 32 bytes, split on the fly); B = the transposed K_hat planes (128 columns e x 32 keys)
-// through LDS, loaded once per workgroup and double-buffered.
-// G is the stream (dS, read once from HBM): its rows are loaded kGPre steps ahead into a ring of
-// registers.  With VEC (16-byte aligned rows, Nk a multiple of 8) the steps of the unrolled main loop issue
-// the same loads every time (addresses clamped, elements past Nk zeroed after the load), the
-// K_hat^T tile's loads before the step's G loads: the wait for the tile at the end of a step
-// (vmcnt counts in issue order) then leaves kGPre steps of G in flight.  Steps left over after
-// whole rounds of kGPre take a guarded tail loop.
-// One job: (half, column block ec, query block ib, batch * head bh); ts: two LDS tiles.
+// blocks.  Per step of 32 keys the 128 x 32 G tile is loaded coalesced (thread: one 4-key quad of
+// four rows), split once into bf16 hi / lo and stored row-major in LDS, where the A operand (lane =
+// row, 8 consecutive keys) is one 16-byte read per plane; the B operand comes from the transposed
+// K_hat planes (128 columns e x 32 keys), also through LDS.  Two steps of both are in flight: at
+// step st the LDS buffers (st - s0) & 1 hold step st, register set (st - s0 + 1) & 1 holds step
+// st + 1 (stored to the other buffers at the end of the step) and the other set receives step
+// st + 2 (clamped to the last step: the same loads every step, so each wait covers only the
+// loads a store needs).
+// One job: (half, column block ec, query block ib, batch * head bh); gs: two G tiles, ts: two
+// K_hat^T tiles.
 template <bool VEC>
 __device__ __forceinline__ void u_job(const SimParams& p, const SimSplit& sp, float* U, int half, int ec, int ib, int bh,
-                                      uint16_t (*ts)[kTile]) {
+                                      uint16_t (*gs)[kTile], uint16_t (*ts)[kTile]) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const int Nq = p.Nq, Nk = p.Nk, EP = p.EP;
-  const int i = ib * 128 + 32 * wave + lr;
-  const float* grow = p.dsim + (int64_t)b * p.sim_s[0] + (int64_t)h * p.sim_s[1] + (int64_t)min(i, Nq - 1) * p.sim_s[2];
+  const float* gb = p.dsim + (int64_t)b * p.sim_s[0] + (int64_t)h * p.sim_s[1];
   const int nst = (Nk + 31) / 32, hst = (nst + 1) / 2;
   const int s0 = half * hst, s1 = min(nst, s0 + hst);
   const int64_t bo = ((int64_t)(b * p.Hk + hk) * EP + ec * 128) * sp.NkP;
   const int erows = min(128, EP - ec * 128);
+  // G loader: thread -> key quad kq (keys 4 kq .. 4 kq + 3 of the step) of rows rr + 32 m, m < 4:
+  // a wave's load reads eight 128-byte row pieces
+  const int kq = tid & 7, rr = tid >> 3;
 
   f32x16 acc[4];
 #pragma unroll
@@ -319,80 +320,76 @@ __device__ __forceinline__ void u_job(const SimParams& p, const SimSplit& sp, fl
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[y][r] = 0.f;
 
-  // G of the 32 keys of step st (clamped into [s0, s1)): sub-step u covers keys
-  // j0 + 16 u + 8 hf .. + 8
-  auto load_g = [&](int st, float* g) {
-    const int j0 = 32 * min(max(st, s0), s1 - 1);
-    if constexpr (VEC) {
-      // a valid, 16-byte aligned chunk; a step reaching past Nk zeroes its extra entries when it
-      // is consumed (`step`), so nothing here waits for the load
+  auto load_g = [&](int st, float4* g) {
+    const int j = 32 * st + 4 * kq;
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int jl = min(j0 + 16 * u + 8 * hf, Nk - 8);
-        const float4 a = *reinterpret_cast<const float4*>(grow + jl);
-        const float4 c = *reinterpret_cast<const float4*>(grow + jl + 4);
-        g[8 * u + 0] = a.x; g[8 * u + 1] = a.y; g[8 * u + 2] = a.z; g[8 * u + 3] = a.w;
-        g[8 * u + 4] = c.x; g[8 * u + 5] = c.y; g[8 * u + 6] = c.z; g[8 * u + 7] = c.w;
+    for (int m = 0; m < 4; ++m) {
+      const int ii = ib * 128 + rr + 32 * m;
+      const float* row = gb + (int64_t)min(ii, Nq - 1) * p.sim_s[2];
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (VEC) {
+        // 16-byte aligned rows, Nk a multiple of 8: a quad lies wholly inside or wholly past the
+        // row (one past it reads the last quad and is zeroed)
+        v = *reinterpret_cast<const float4*>(row + min(j, Nk - 4));
+        if (ii >= Nq || j >= Nk) v = make_float4(0.f, 0.f, 0.f, 0.f);
+      } else if (ii < Nq) {
+        v.x = j < Nk ? row[j] : 0.f;
+        v.y = j + 1 < Nk ? row[j + 1] : 0.f;
+        v.z = j + 2 < Nk ? row[j + 2] : 0.f;
+        v.w = j + 3 < Nk ? row[j + 3] : 0.f;
       }
-    } else {
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const int j = j0 + 16 * u + 8 * hf + t;
-          g[8 * u + t] = j < Nk ? grow[j] : 0.f;
-        }
+      g[m] = v;
     }
   };
-  // one step: split the step's G, issue the next tile's loads and step st + kGPre's G loads, the
-  // products on the current tile, the next tile into the other LDS buffer
-  auto step = [&](int st, float* g) {
-    const int buf = (st - s0) & 1;
-    if (VEC && 32 * st + 32 > Nk) {   // the last, partial step: keys past Nk read as zero
-      POPE_COLD_PATH();
+  // split the thread's four quads; one 8-byte store per plane and row
+  auto store_g = [&](uint16_t* t, const float4* g) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const int j = 32 * st + 16 * u + 8 * hf + t;
-          if (j >= Nk) g[8 * u + t] = 0.f;
-        }
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t h0 = BF16::pack2(g[m].x, g[m].y), h1 = BF16::pack2(g[m].z, g[m].w);
+      const uint32_t l0 = BF16::pack2(g[m].x - __uint_as_float(h0 << 16), g[m].y - __uint_as_float(h0 & 0xffff0000u));
+      const uint32_t l1 = BF16::pack2(g[m].z - __uint_as_float(h1 << 16), g[m].w - __uint_as_float(h1 & 0xffff0000u));
+      const int o = (rr + 32 * m) * kLd + 4 * kq;
+      *reinterpret_cast<u32x2*>(t + o) = u32x2{h0, h1};
+      *reinterpret_cast<u32x2*>(t + 128 * kLd + o) = u32x2{l0, l1};
     }
-    u32x4 ah[2], al[2];
-    split8(g, ah[0], al[0]);
-    split8(g + 8, ah[1], al[1]);
-    u32x4 vb[4];
-    tile_load(sp.kh + bo, sp.kl + bo, sp.NkP, 32 * min(st + 1, s1 - 1), erows, vb, tid);
-    load_g(st + kGPre, g);
+  };
+  float4 gr[2][4];
+  u32x4 vb[2][4];
+  auto fetch = [&](int st, int k) {
+    const int sc = min(st, s1 - 1);
+    load_g(sc, gr[k]);
+    tile_load(sp.kh + bo, sp.kl + bo, sp.NkP, 32 * sc, erows, vb[k], tid);
+  };
+  auto step = [&](int st, auto kc) {
+    constexpr int K = decltype(kc)::value;
+    fetch(st + 2, K);
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < 2; ++u) {
+      u32x4 ah, al;
+      tile_frag(gs[K], 32 * wave, u, lr, hf, ah, al);
 #pragma unroll
       for (int y = 0; y < 4; ++y) {
         u32x4 bh16, bl16;
-        tile_frag(ts[buf], 32 * y, u, lr, hf, bh16, bl16);
-        acc[y] = mfma3(ah[u], al[u], bh16, bl16, acc[y]);
+        tile_frag(ts[K], 32 * y, u, lr, hf, bh16, bl16);
+        acc[y] = mfma3(ah, al, bh16, bl16, acc[y]);
       }
-    tile_store(ts[buf ^ 1], vb, tid);   // the last step's copy is never read
+    }
+    store_g(gs[K ^ 1], gr[K ^ 1]);   // the last step's copy is never read
+    tile_store(ts[K ^ 1], vb[K ^ 1], tid);
     __syncthreads();
   };
-  float g[kGPre][16];
   if (s0 < s1) {
-    {
-      u32x4 vb[4];
-      tile_load(sp.kh + bo, sp.kl + bo, sp.NkP, 32 * s0, erows, vb, tid);
-#pragma unroll
-      for (int k = 0; k < kGPre; ++k) load_g(s0 + k, g[k]);
-      tile_store(ts[0], vb, tid);
-    }
+    fetch(s0, 0);
+    fetch(s0 + 1, 1);
+    store_g(gs[0], gr[0]);
+    tile_store(ts[0], vb[0], tid);
     __syncthreads();
-    const int nmain = s0 + ((s1 - s0) / kGPre) * kGPre;
-    for (int sb = s0; sb < nmain; sb += kGPre) {
-#pragma unroll
-      for (int k = 0; k < kGPre; ++k) step(sb + k, g[k]);
+    int st = s0;
+    for (; st + 1 < s1; st += 2) {
+      step(st, std::integral_constant<int, 0>{});
+      step(st + 1, std::integral_constant<int, 1>{});
     }
-#pragma unroll
-    for (int k = 0; k < kGPre - 1; ++k)
-      if (nmain + k < s1) step(nmain + k, g[k]);
+    if (st < s1) step(st, std::integral_constant<int, 0>{});
   }
 
   float* ub = (half ? sp.U2 : U) + (int64_t)bh * Nq * EP;
@@ -559,7 +556,7 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_uw_kernel(SimParams p, 
   const int half = k & 1, rest = k >> 1;
   if (is_u) {
     const int ec = rest % nec, ib = (rest / nec) % nib, g = rest / (nec * nib);
-    u_job<VEC>(p, sp, U, half, ec, ib, b * p.Hq + g * p.Hk + hk, lds);
+    u_job<VEC>(p, sp, U, half, ec, ib, b * p.Hq + g * p.Hk + hk, lds, lds + 2);
   } else {
     w_job<VEC>(p, sp, W, half, rest % nec, rest / nec, b * p.Hk + hk, lds, lds + 2);
   }
