@@ -13,7 +13,7 @@
 //   sim_split_prep : the expanded rows Q_hat / K_hat (columns [a cos | a sin | rest], the
 //                    reference's rounding of the key phase fl(F_j + bias), pope.py:56) split
 //                    into hi / lo bf16 planes, row-major (forward) or transposed (backward);
-//   sim_split_fwd  : S = Q_hat K_hat^T, one 128 x 128 tile per workgroup;
+//   sim_split_fwd  : S = Q_hat K_hat^T, two neighbouring 128 x 128 tiles per workgroup;
 //   sim_split_uw   : U = G K_hat (u_job: G = dS rows read from HBM and split on the fly) and
 //                    W = G^T Q_hat (w_job: G tiles split once per workgroup into LDS, transposed),
 //                    in one launch whose job order lets the second read of G hit the last-level
@@ -213,19 +213,28 @@ __device__ __forceinline__ void tile_frag(const uint16_t* t, int r, int u, int l
   lo = *reinterpret_cast<const u32x4*>(t + 128 * kLd + o);
 }
 
-// Forward: one workgroup = 128 x 128 tile of S; 4 waves of 64 x 64 (2 x 2 blocks of 32 x 32).
-// Per 32 expanded columns the Q_hat and K_hat tiles go through LDS (double-buffered: the next
-// step's loads are in flight during the products).
+// Forward: one workgroup = two neighbouring 128 x 128 tiles of S (key blocks 2 jp and 2 jp + 1),
+// computed one after the other; 4 waves of 64 x 64 per tile (2 x 2 blocks of 32 x 32).  Per 32
+// expanded columns the Q_hat and K_hat tiles go through LDS.  The steps of both tiles form one
+// stream with two steps in flight (LDS buffer (s & 1) holds step s, register set (s + 1) & 1 step
+// s + 1, the other set receives step s + 2, clamped to the last step), so the second tile's first
+// loads overlap the first tile's products and its S stores.
 __global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p, SimSplit sp, int nib, int njb) {
   __shared__ __attribute__((aligned(16))) uint16_t ts[2][2][kTile];   // [buffer][Q_hat, K_hat]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int jb = id % njb, ib = (id / njb) % nib, bh = id / (njb * nib);
+  const int njp = (njb + 1) / 2;
+  const int jp = id % njp, ib = (id / njp) % nib, bh = id / (njp * nib);
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const int EP = p.EP;
   const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
   const int64_t qo = ((int64_t)bh * sp.NqP + ib * 128) * EP;
-  const int64_t ko = ((int64_t)(b * p.Hk + hk) * sp.NkP + jb * 128) * EP;
+  const int64_t ko = ((int64_t)(b * p.Hk + hk) * sp.NkP + jp * 256) * EP;
+  const int nst = EP / 32, ntile = min(2, njb - 2 * jp), S = ntile * nst;
+  // S is written with non-temporal stores: its 4 bytes per (i, j) are not read again by this
+  // path, and kept out of the caches they leave the operand planes and dS of the neighbouring
+  // launches cached (C2: the step's other kernels ran 10-15 us faster)
+  float* sbase = p.sim + (int64_t)b * p.sim_s[0] + (int64_t)h * p.sim_s[1];
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -235,55 +244,59 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p,
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
 
-  u32x4 va[4], vb[4];
-  const int nst = EP / 32;
-  tile_load(sp.qh + qo, sp.ql + qo, EP, 0, 128, va, tid);
-  tile_load(sp.kh + ko, sp.kl + ko, EP, 0, 128, vb, tid);
-  tile_store(ts[0][0], va, tid);
-  tile_store(ts[0][1], vb, tid);
-  __syncthreads();
-  for (int st = 0; st < nst; ++st) {
-    const int buf = st & 1;
-    if (st + 1 < nst) {
-      tile_load(sp.qh + qo, sp.ql + qo, EP, 32 * (st + 1), 128, va, tid);
-      tile_load(sp.kh + ko, sp.kl + ko, EP, 32 * (st + 1), 128, vb, tid);
-    }
+  u32x4 va[2][4], vb[2][4];
+  auto fetch = [&](int st, int k) {
+    const int sc = min(st, S - 1), t = sc / nst, kk = sc - t * nst;
+    tile_load(sp.qh + qo, sp.ql + qo, EP, 32 * kk, 128, va[k], tid);
+    const int64_t kt = ko + (int64_t)t * 128 * EP;
+    tile_load(sp.kh + kt, sp.kl + kt, EP, 32 * kk, 128, vb[k], tid);
+  };
+  auto step = [&](int st, auto kc) {
+    constexpr int K = decltype(kc)::value;
+    fetch(st + 2, K);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       u32x4 ah[2], al[2], bh16[2], bl16[2];
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
-        tile_frag(ts[buf][0], wr + 32 * x, u, lr, hf, ah[x], al[x]);
-        tile_frag(ts[buf][1], wc + 32 * x, u, lr, hf, bh16[x], bl16[x]);
+        tile_frag(ts[K][0], wr + 32 * x, u, lr, hf, ah[x], al[x]);
+        tile_frag(ts[K][1], wc + 32 * x, u, lr, hf, bh16[x], bl16[x]);
       }
 #pragma unroll
       for (int x = 0; x < 2; ++x)
 #pragma unroll
         for (int y = 0; y < 2; ++y) acc[x][y] = mfma3(ah[x], al[x], bh16[y], bl16[y], acc[x][y]);
     }
-    if (st + 1 < nst) {
-      tile_store(ts[buf ^ 1][0], va, tid);   // the other buffer: its last readers passed the barrier
-      tile_store(ts[buf ^ 1][1], vb, tid);
+    tile_store(ts[K ^ 1][0], va[K ^ 1], tid);   // the last step's copy is never read
+    tile_store(ts[K ^ 1][1], vb[K ^ 1], tid);
+    if ((st + 1) % nst == 0) {   // the tile's last step: write it, start the next from zero
+      const int i0 = ib * 128 + wr, j0 = (2 * jp + st / nst) * 128 + wc;
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) {
+          const int j = j0 + 32 * y + lr;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int i = i0 + 32 * x + 8 * (r >> 2) + 4 * hf + (r & 3);
+            if (i < p.Nq && j < p.Nk) __builtin_nontemporal_store(acc[x][y][r], sbase + (int64_t)i * p.sim_s[2] + j);
+            acc[x][y][r] = 0.f;
+          }
+        }
     }
     __syncthreads();
+  };
+  fetch(0, 0);
+  fetch(1, 1);
+  tile_store(ts[0][0], va[0], tid);
+  tile_store(ts[0][1], vb[0], tid);
+  __syncthreads();
+  int st = 0;
+  for (; st + 1 < S; st += 2) {
+    step(st, std::integral_constant<int, 0>{});
+    step(st + 1, std::integral_constant<int, 1>{});
   }
-
-  // S is written with non-temporal stores: its 4 bytes per (i, j) are not read again by this
-  // path, and kept out of the caches they leave the operand planes and dS of the neighbouring
-  // launches cached (C2: the step's other kernels ran 10-15 us faster)
-  float* sbase = p.sim + (int64_t)b * p.sim_s[0] + (int64_t)h * p.sim_s[1];
-  const int i0 = ib * 128 + wr, j0 = jb * 128 + wc;
-#pragma unroll
-  for (int x = 0; x < 2; ++x)
-#pragma unroll
-    for (int y = 0; y < 2; ++y) {
-      const int j = j0 + 32 * y + lr;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int i = i0 + 32 * x + 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (i < p.Nq && j < p.Nk) __builtin_nontemporal_store(acc[x][y][r], sbase + (int64_t)i * p.sim_s[2] + j);
-      }
-    }
+  if (st < S) step(st, std::integral_constant<int, 0>{});
 }
 
 // U[b,h,i,e] = sum_j G[b,h,i,j] K_hat[b,hk,j,e] over half of the keys (two halves, the second
@@ -579,8 +592,8 @@ hipError_t launch_sim_split_fwd(const SimParams& p, const SimSplit& sp, hipStrea
   hipError_t e = launch_sim_split_prep(p, sp, 0, s);
   if (e != hipSuccess) return e;
   const int nib = (p.Nq + 127) / 128, njb = (p.Nk + 127) / 128;
-  return launch_named("sim_split_fwd", sim_split_fwd_kernel, dim3(nib * njb * p.B * p.Hq), dim3(kThreads), s, p, sp,
-                      nib, njb);
+  return launch_named("sim_split_fwd", sim_split_fwd_kernel, dim3(nib * ((njb + 1) / 2) * p.B * p.Hq), dim3(kThreads),
+                      s, p, sp, nib, njb);
 }
 
 hipError_t launch_sim_split_bwd(const SimParams& p, const SimSplit& sp, float* U, float* W, hipStream_t s) {
