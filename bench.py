@@ -256,11 +256,14 @@ def sim_bench(steps: int, warmup: int):
     k = torch.randn(B_, H_, N_, D_, generator=g).to(dev).requires_grad_(True)
     ds = torch.randn(B_, H_, N_, N_, generator=g).to(dev)
     pope = pope_amd.PoPE(D_, heads=H_).to(dev)
+    # pos_emb is the op's input, made once as in the C3 line (the clamped bias a leaf that
+    # receives dbias): the step times compute_attn_similarity forward + backward
+    freqs, bias = pope(N_)
+    bias = bias.detach().requires_grad_(True)
 
     def step():
-        q.grad = k.grad = None
-        pope.bias.grad = None
-        sim = pope_amd.compute_attn_similarity(q, k, pope(N_))
+        q.grad = k.grad = bias.grad = None
+        sim = pope_amd.compute_attn_similarity(q, k, (freqs, bias))
         sim.backward(ds)
 
     prewarm(step)
