@@ -30,6 +30,7 @@ namespace pope {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int64_t kSimMinJobs = 512;   // U / W workgroups below which each job's reduction is split
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
@@ -299,8 +300,8 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p,
   if (st < S) step(st, std::integral_constant<int, 0>{});
 }
 
-// U[b,h,i,e] = sum_j G[b,h,i,j] K_hat[b,hk,j,e] over half of the keys (two halves, the second
-// into sp.U2: twice the waves of one full pass; the finalize adds them).  One workgroup = 128
+// U[b,h,i,e] = sum_j G[b,h,i,j] K_hat[b,hk,j,e] over all keys, or with nsplit = 2 over half of
+// them (the second half into sp.U2: twice the workgroups of one full pass; the finalize adds them).  One workgroup = 128
 // query rows x 128 expanded columns; wave w owns rows 32 w .. 32 w + 31 and all four column
 // blocks.  Per step of 32 keys the 128 x 32 G tile is loaded coalesced (thread: one 4-key quad of
 // four rows), split once into bf16 hi / lo and stored row-major in LDS, where the A operand (lane =
@@ -310,16 +311,16 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p,
 // st + 1 (stored to the other buffers at the end of the step) and the other set receives step
 // st + 2 (clamped to the last step: the same loads every step, so each wait covers only the
 // loads a store needs).
-// One job: (half, column block ec, query block ib, batch * head bh); gs: two G tiles, ts: two
+// One job: (part `half` of nsplit, column block ec, query block ib, batch * head bh); gs: two G tiles, ts: two
 // K_hat^T tiles.
 template <bool VEC>
-__device__ __forceinline__ void u_job(const SimParams& p, const SimSplit& sp, float* U, int half, int ec, int ib, int bh,
-                                      uint16_t (*gs)[kTile], uint16_t (*ts)[kTile]) {
+__device__ __forceinline__ void u_job(const SimParams& p, const SimSplit& sp, float* U, int nsplit, int half, int ec,
+                                      int ib, int bh, uint16_t (*gs)[kTile], uint16_t (*ts)[kTile]) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const int Nq = p.Nq, Nk = p.Nk, EP = p.EP;
   const float* gb = p.dsim + (int64_t)b * p.sim_s[0] + (int64_t)h * p.sim_s[1];
-  const int nst = (Nk + 31) / 32, hst = (nst + 1) / 2;
+  const int nst = (Nk + 31) / 32, hst = (nst + nsplit - 1) / nsplit;
   const int s0 = half * hst, s1 = min(nst, s0 + hst);
   const int64_t bo = ((int64_t)(b * p.Hk + hk) * EP + ec * 128) * sp.NkP;
   const int erows = min(128, EP - ec * 128);
@@ -418,24 +419,24 @@ __device__ __forceinline__ void u_job(const SimParams& p, const SimSplit& sp, fl
   }
 }
 
-// W[b,hk,j,e] = sum_{h in group(hk)} sum_i G[b,h,i,j] Q_hat[b,h,i,e] over half of the (query
-// head, 32-query step) sequence (the second half into sp.W2).  One workgroup = 128 keys x 128
+// W[b,hk,j,e] = sum_{h in group(hk)} sum_i G[b,h,i,j] Q_hat[b,h,i,e] over the (query head,
+// 32-query step) sequence, or with nsplit = 2 over half of it (the second half into sp.W2).  One workgroup = 128 keys x 128
 // expanded columns.  Per step the 32 x 128 G tile is loaded coalesced (thread: 4 rows x 4 keys),
 // split once and stored key-major in LDS, so the A operand (lane = key, 8 consecutive queries)
 // is one 16-byte LDS read per plane; the transposed Q_hat planes (128 columns e x 32 queries)
 // go through LDS the same way.  Both double-buffered.  Wave w owns keys 32 w .. 32 w + 31 and
 // all four column blocks.
-// One job: (half, column block ec, key block jb, batch * kv head bhk); gs: two G^T tiles
+// One job: (part `half` of nsplit, column block ec, key block jb, batch * kv head bhk); gs: two G^T tiles
 // (key-major), qs: two Q_hat^T tiles (column-major).
 template <bool VEC>
-__device__ __forceinline__ void w_job(const SimParams& p, const SimSplit& sp, float* W, int half, int ec, int jb,
-                                      int bhk, uint16_t (*gs)[kTile], uint16_t (*qs)[kTile]) {
+__device__ __forceinline__ void w_job(const SimParams& p, const SimSplit& sp, float* W, int nsplit, int half, int ec,
+                                      int jb, int bhk, uint16_t (*gs)[kTile], uint16_t (*qs)[kTile]) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int b = bhk / p.Hk, hk = bhk % p.Hk;
   const int Nq = p.Nq, Nk = p.Nk, EP = p.EP;
   const int groups = p.Hq / p.Hk;
   const int nis = (Nq + 31) / 32;              // 32-query steps per head
-  const int nst = groups * nis, hst = (nst + 1) / 2;
+  const int nst = groups * nis, hst = (nst + nsplit - 1) / nsplit;
   const int s0 = half * hst, s1 = min(nst, s0 + hst);
   const int erows = min(128, EP - ec * 128);
   // G tile loader: thread -> key quad c (keys 4 c .. 4 c + 3), rows 4 rg .. 4 rg + 3 of the step.
@@ -556,22 +557,22 @@ __device__ __forceinline__ void w_job(const SimParams& p, const SimSplit& sp, fl
 // workgroup is the larger of the two jobs' needs (four tiles, 80 KB; two workgroups per CU).
 template <bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void sim_split_uw_kernel(SimParams p, SimSplit sp, float* U, float* W,
-                                                                   int nib, int njb, int nec) {
+                                                                   int nib, int njb, int nec, int nsplit) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[4][kTile];
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int groups = p.Hq / p.Hk;
-  const int nu = 2 * nec * nib * groups, nw = 2 * nec * njb;   // jobs per unit
+  const int nu = nsplit * nec * nib * groups, nw = nsplit * nec * njb;   // jobs per unit
   const int unit = id / (nu + nw), r = id % (nu + nw);
   const int b = unit / p.Hk, hk = unit % p.Hk;
   const int m = min(nu, nw);
   const bool is_u = r < 2 * m ? !(r & 1) : nu > nw;
   const int k = r < 2 * m ? r >> 1 : r - m;
-  const int half = k & 1, rest = k >> 1;
+  const int half = k % nsplit, rest = k / nsplit;
   if (is_u) {
     const int ec = rest % nec, ib = (rest / nec) % nib, g = rest / (nec * nib);
-    u_job<VEC>(p, sp, U, half, ec, ib, b * p.Hq + g * p.Hk + hk, lds, lds + 2);
+    u_job<VEC>(p, sp, U, nsplit, half, ec, ib, b * p.Hq + g * p.Hk + hk, lds, lds + 2);
   } else {
-    w_job<VEC>(p, sp, W, half, rest % nec, rest / nec, b * p.Hk + hk, lds, lds + 2);
+    w_job<VEC>(p, sp, W, nsplit, half, rest % nec, rest / nec, b * p.Hk + hk, lds, lds + 2);
   }
 }
 
@@ -601,14 +602,20 @@ hipError_t launch_sim_split_bwd(const SimParams& p, const SimSplit& sp, float* U
   if (e != hipSuccess) return e;
   const int nec = (p.EP + 127) / 128;
   const int nib = (p.Nq + 127) / 128, njb = (p.Nk + 127) / 128;
-  const dim3 grid((2 * nec * nib * (p.Hq / p.Hk) + 2 * nec * njb) * p.B * p.Hk);
+  // each job's reduction split in kSimSplits parts (partial sums U, U2 and W, W2 that the
+  // finalize adds) when one part per job would leave fewer than kSimMinJobs workgroups
+  const int64_t jobs1 = (int64_t)(nec * nib * (p.Hq / p.Hk) + nec * njb) * p.B * p.Hk;
+  const int nsplit = jobs1 < kSimMinJobs ? 2 : 1;
+  const dim3 grid((unsigned)(nsplit * jobs1));
   // VEC needs Nk % 8 == 0: every 8-key chunk then lies wholly inside or wholly past the row, so a
   // clamped chunk is only ever one whose entries are all zeroed
   e = p.g_vec && p.Nk % 8 == 0
-          ? launch_named("sim_split_uw", sim_split_uw_kernel<true>, grid, dim3(kThreads), s, p, sp, U, W, nib, njb, nec)
-          : launch_named("sim_split_uw", sim_split_uw_kernel<false>, grid, dim3(kThreads), s, p, sp, U, W, nib, njb, nec);
+          ? launch_named("sim_split_uw", sim_split_uw_kernel<true>, grid, dim3(kThreads), s, p, sp, U, W, nib, njb, nec,
+                         nsplit)
+          : launch_named("sim_split_uw", sim_split_uw_kernel<false>, grid, dim3(kThreads), s, p, sp, U, W, nib, njb, nec,
+                         nsplit);
   if (e != hipSuccess) return e;
-  return launch_sim_finalize(p, U, sp.U2, W, sp.W2, s);
+  return launch_sim_finalize(p, U, nsplit == 2 ? sp.U2 : nullptr, W, nsplit == 2 ? sp.W2 : nullptr, s);
 }
 
 }  // namespace pope
