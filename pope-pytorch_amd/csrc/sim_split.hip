@@ -13,7 +13,7 @@
 //   sim_split_prep : the expanded rows Q_hat / K_hat (columns [a cos | a sin | rest], the
 //                    reference's rounding of the key phase fl(F_j + bias), pope.py:56) split
 //                    into hi / lo bf16 planes, row-major (forward) or transposed (backward);
-//   sim_split_fwd  : S = Q_hat K_hat^T, two neighbouring 128 x 128 tiles per workgroup;
+//   sim_split_fwd  : S = Q_hat K_hat^T, two or four neighbouring 128 x 128 tiles per workgroup;
 //   sim_split_uw   : U = G K_hat (u_job: G = dS rows read from HBM and split on the fly) and
 //                    W = G^T Q_hat (w_job: G tiles split once per workgroup into LDS, transposed),
 //                    in one launch whose job order lets the second read of G hit the last-level
@@ -214,24 +214,25 @@ __device__ __forceinline__ void tile_frag(const uint16_t* t, int r, int u, int l
   lo = *reinterpret_cast<const u32x4*>(t + 128 * kLd + o);
 }
 
-// Forward: one workgroup = two neighbouring 128 x 128 tiles of S (key blocks 2 jp and 2 jp + 1),
-// computed one after the other; 4 waves of 64 x 64 per tile (2 x 2 blocks of 32 x 32).  Per 32
-// expanded columns the Q_hat and K_hat tiles go through LDS.  The steps of both tiles form one
+// Forward: one workgroup = tpw neighbouring 128 x 128 tiles of S (key blocks tpw jp ..
+// tpw jp + tpw - 1), computed one after the other; 4 waves of 64 x 64 per tile (2 x 2 blocks of 32 x 32).  Per 32
+// expanded columns the Q_hat and K_hat tiles go through LDS.  The steps of all tiles form one
 // stream with two steps in flight (LDS buffer (s & 1) holds step s, register set (s + 1) & 1 step
-// s + 1, the other set receives step s + 2, clamped to the last step), so the second tile's first
-// loads overlap the first tile's products and its S stores.
-__global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p, SimSplit sp, int nib, int njb) {
+// s + 1, the other set receives step s + 2, clamped to the last step), so a tile's first loads
+// overlap the previous tile's products and its S stores.
+__global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p, SimSplit sp, int nib, int njb,
+                                                                    int tpw) {
   __shared__ __attribute__((aligned(16))) uint16_t ts[2][2][kTile];   // [buffer][Q_hat, K_hat]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int njp = (njb + 1) / 2;
+  const int njp = (njb + tpw - 1) / tpw;
   const int jp = id % njp, ib = (id / njp) % nib, bh = id / (njp * nib);
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const int EP = p.EP;
   const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
   const int64_t qo = ((int64_t)bh * sp.NqP + ib * 128) * EP;
-  const int64_t ko = ((int64_t)(b * p.Hk + hk) * sp.NkP + jp * 256) * EP;
-  const int nst = EP / 32, ntile = min(2, njb - 2 * jp), S = ntile * nst;
+  const int64_t ko = ((int64_t)(b * p.Hk + hk) * sp.NkP + jp * tpw * 128) * EP;
+  const int nst = EP / 32, ntile = min(tpw, njb - tpw * jp), S = ntile * nst;
   // S is written with non-temporal stores: its 4 bytes per (i, j) are not read again by this
   // path, and kept out of the caches they leave the operand planes and dS of the neighbouring
   // launches cached (C2: the step's other kernels ran 10-15 us faster)
@@ -271,7 +272,7 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p,
     tile_store(ts[K ^ 1][0], va[K ^ 1], tid);   // the last step's copy is never read
     tile_store(ts[K ^ 1][1], vb[K ^ 1], tid);
     if ((st + 1) % nst == 0) {   // the tile's last step: write it, start the next from zero
-      const int i0 = ib * 128 + wr, j0 = (2 * jp + st / nst) * 128 + wc;
+      const int i0 = ib * 128 + wr, j0 = (tpw * jp + st / nst) * 128 + wc;
 #pragma unroll
       for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -593,8 +594,11 @@ hipError_t launch_sim_split_fwd(const SimParams& p, const SimSplit& sp, hipStrea
   hipError_t e = launch_sim_split_prep(p, sp, 0, s);
   if (e != hipSuccess) return e;
   const int nib = (p.Nq + 127) / 128, njb = (p.Nk + 127) / 128;
-  return launch_named("sim_split_fwd", sim_split_fwd_kernel, dim3(nib * ((njb + 1) / 2) * p.B * p.Hq), dim3(kThreads),
-                      s, p, sp, nib, njb);
+  // tiles per workgroup: 4 while that still leaves 1,024 workgroups (two rounds at two per CU), else 2
+  const int64_t rows = (int64_t)nib * p.B * p.Hq;
+  const int tpw = rows * ((njb + 3) / 4) >= 1024 ? 4 : 2;
+  return launch_named("sim_split_fwd", sim_split_fwd_kernel, dim3((unsigned)(rows * ((njb + tpw - 1) / tpw))),
+                      dim3(kThreads), s, p, sp, nib, njb, tpw);
 }
 
 hipError_t launch_sim_split_bwd(const SimParams& p, const SimSplit& sp, float* U, float* W, hipStream_t s) {
