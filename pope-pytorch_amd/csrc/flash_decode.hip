@@ -44,7 +44,6 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 __device__ __forceinline__ float2 half2f(uint32_t w) {
   const f16x2 v = __builtin_bit_cast(f16x2, w);
@@ -184,9 +183,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
     qwc[1] = lds_read16_at(a + 16);
   };
   u32x4 kb[kLoads], vb[kLoads];
+  // K and V rows are read once per call: non-temporal loads keep them from evicting what is read
+  // again (the split's freqs rows, shared by every batch, and the partials the combine reads)
   auto load = [&](u32x4* buf, const uint16_t* lp, int stride) {
 #pragma unroll
-    for (int u = 0; u < kLoads; ++u) buf[u] = ld16(lp + min(u * RPI, rows_left) * stride);
+    for (int u = 0; u < kLoads; ++u)
+      buf[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(lp + min(u * RPI, rows_left) * stride));
   };
 
   // ---- the split's phase rows F[j] (rows past Nk repeat the last row), then the first head's
