@@ -16,8 +16,8 @@
 //   sim_split_fwd  : S = Q_hat K_hat^T, two or four neighbouring 128 x 128 tiles per workgroup;
 //   sim_split_uw   : U = G K_hat (u_job: G = dS rows read from HBM and split on the fly) and
 //                    W = G^T Q_hat (w_job: G tiles split once per workgroup into LDS, transposed),
-//                    in one launch whose job order lets the second read of G hit the last-level
-//                    cache.
+//                    in one launch whose job order puts the two reads of each block of G close
+//                    together in time.
 // The chain rule of the polar transform then runs in sim.hip's finalize kernel on U and W.
 #include <type_traits>
 
@@ -552,10 +552,10 @@ __device__ __forceinline__ void w_job(const SimParams& p, const SimSplit& sp, fl
 
 // Both passes in one launch.  Logical ids run over units of (batch, kv head): a unit holds the U
 // jobs of the kv head's query heads and the W jobs of the kv head, interleaved, so the two jobs
-// that read a block of G run at about the same time (xcd_remap keeps a unit's jobs on one XCD).
-// The G of the units in flight (16.8 MB per head at 2048 x 2048) stays in the 256 MB last-level
-// cache (Infinity Cache) between its two reads, so G crosses HBM about once.  The LDS of a
-// workgroup is the larger of the two jobs' needs (four tiles, 80 KB; two workgroups per CU).
+// that read a block of G run at about the same time (xcd_remap keeps a unit's jobs on one XCD)
+// and the G of the units in flight (16.8 MB per head at 2048 x 2048) fits the 256 MB last-level
+// cache between its two reads.  U jobs and W jobs also hide each other's load latency.  The LDS of
+// a workgroup is the larger of the two jobs' needs (four tiles, 80 KB; two workgroups per CU).
 template <bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void sim_split_uw_kernel(SimParams p, SimSplit sp, float* U, float* W,
                                                                    int nib, int njb, int nec, int nsplit) {
