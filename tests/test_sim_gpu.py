@@ -96,6 +96,16 @@ def test_similarity_multi_config(cuda, cfg, allow_tf32):
     _compare(S, g, S_ref, g_ref)
 
 
+def test_similarity_large_grid_paths(cuda):
+    """A shape whose grids take the split-bf16 kernels' large-problem paths: U / W jobs without the
+    split reduction (at least 512 workgroups of one part each) and four S tiles per forward
+    workgroup with a partial last group (nine key blocks), with grouped heads and ragged sizes."""
+    q, k, freqs, bias, G = _case(101, 1, 64, 16, 1000, 1150, 64, 32)
+    S_ref, g_ref = _oracle(q, k, freqs, bias, G)
+    S, g = _kernel(q, k, freqs, bias, G, allow_tf32=True)
+    _compare(S, g, S_ref, g_ref)
+
+
 def test_similarity_non_contiguous(cuda):
     import pope_amd
     g = torch.Generator().manual_seed(5)
