@@ -85,19 +85,25 @@ __device__ __forceinline__ void stage32(uint16_t* lds, const uint16_t* src, int6
 }
 
 // ---- forward ---------------------------------------------------------------------------
+// Four waves per workgroup, 128 query rows (wave w: rows q0 + 32 w ..); per 32-key tile the K_hat
+// rows and the V rows go through LDS once for the four waves (unpadded, XOR-swizzled), double
+// buffered: the next tile's loads are in flight in registers while the current tile is computed.
 template <typename T, int EP, int DV>
-__global__ __launch_bounds__(64) void wide_fwd_kernel(FlashFwdParams p) {
+__global__ __launch_bounds__(256) void wide_fwd_kernel(FlashFwdParams p) {
   constexpr int KS = EP / 16, NDB = DV / 32;
+  constexpr int KU = EP / 8, VU = DV / 8;              // 16-byte units per K_hat / V row
+  constexpr int KN = 32 * KU / 256, VN = 32 * VU / 256;  // units per thread and tile
   typedef typename T::vec8 vec8;
-  __shared__ __attribute__((aligned(16))) uint16_t vt[32 * DV];
+  __shared__ __attribute__((aligned(16))) uint16_t kt[2][32 * EP];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[2][32 * DV];
 
-  const int lane = threadIdx.x, lr = lane & 31, hf = lane >> 5;
-  const int BH = p.B * p.Hq, nqb = p.NqP / 32;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
+  const int BH = p.B * p.Hq, nqb = p.NqP / 128;
   const int bh = blockIdx.x % BH;
-  const int q0 = 32 * (nqb - 1 - (int)(blockIdx.x / BH));   // heaviest causal blocks first
+  const int q0 = 128 * (nqb - 1 - (int)(blockIdx.x / BH));   // heaviest causal blocks first
   if (q0 >= p.Nq) return;
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
-  const int Nk = p.Nk, D = p.D, qi = q0 + lr;
+  const int Nk = p.Nk, D = p.D, qi = q0 + 32 * wave + lr;
 
   vec8 qreg[KS];
   {
@@ -106,24 +112,60 @@ __global__ __launch_bounds__(64) void wide_fwd_kernel(FlashFwdParams p) {
     for (int kk = 0; kk < KS; ++kk) qreg[kk] = as_vec8<vec8>(ld16(qrow + 16 * kk));
   }
   int nkeys = min(((ci32*)p.kend)[b], Nk);
-  if (p.causal) nkeys = min(nkeys, q0 + 32);
-  const uint16_t* khb = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;
+  if (p.causal) nkeys = min(nkeys, q0 + 128);
+  const uint16_t* khb = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;   // rows padded to NkP
   const uint16_t* vb = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
   cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
-  const TileOffsets<DV / 8> vo(lane);
+  const TileOffsets<KU> ko(lane);
+  const TileOffsets<VU> vo(lane);
+
+  // tile staging: unit c = tid + 256 i of the tile's rows (row c / U, unit c % U); V rows past Nk
+  // repeat the last one, V columns at or past D are zero
+  u32x4 kst[KN], vst[VN];
+  auto load_tile = [&](int j0) {
+#pragma unroll
+    for (int i = 0; i < KN; ++i) {
+      const int c = tid + 256 * i;
+      kst[i] = ld16(khb + (int64_t)(j0 + c / KU) * EP + 8 * (c % KU));
+    }
+#pragma unroll
+    for (int i = 0; i < VN; ++i) {
+      const int c = tid + 256 * i, d0 = 8 * (c % VU);
+      vst[i] = d0 < D ? ld16(vb + (int64_t)min(j0 + c / VU, Nk - 1) * p.v_s[2] + d0) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KN; ++i) {
+      const int c = tid + 256 * i, r = c / KU, u = c % KU;
+      *reinterpret_cast<u32x4*>(kt[buf] + r * EP + 8 * (u ^ tile_swz(KU, r))) = kst[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VN; ++i) {
+      const int c = tid + 256 * i, r = c / VU, u = c % VU;
+      *reinterpret_cast<u32x4*>(vt[buf] + r * DV + 8 * (u ^ tile_swz(VU, r))) = vst[i];
+    }
+  };
 
   f32x16 oacc[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) oacc[db] = splat16(0.f);
   float m = -INFINITY, l = 0.f;
   const uint32_t ones = T::pack2(1.f, 1.f);
-  for (int j0 = 0; j0 < nkeys; j0 += 32) {
-    stage32<DV>(vt, vb, p.v_s[2], j0, Nk - 1, D);
+  const int nt = (nkeys + 31) / 32;
+  if (nt > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < nt; ++t) {
+    const int buf = t & 1, j0 = 32 * t;
+    if (t + 1 < nt) load_tile(j0 + 32);
     // S^T (rows = keys, lane = query), log2 units
     f32x16 s = splat16(0.f);
-    const uint16_t* kr = khb + (int64_t)(j0 + lr) * EP + 8 * hf;   // rows padded to NkP
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) s = T::mfma32(as_vec8<vec8>(ld16(kr + 16 * kk)), qreg[kk], s);
+    for (int kk = 0; kk < KS; ++kk)
+      s = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt[buf] + ko.row_at(kk))), qreg[kk], s);
     const uint32_t wv = (uint32_t)(mw[j0 >> 6] >> (j0 & 32));
     float mt = -INFINITY;
 #pragma unroll
@@ -150,17 +192,17 @@ __global__ __launch_bounds__(64) void wide_fwd_kernel(FlashFwdParams p) {
       }
     l = l * alpha + ls + __shfl_xor(ls, 32, 64);
     m = mn;
-    __syncthreads();   // the V tile's stores are complete
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
 #pragma unroll
       for (int g = 0; g < 2; ++g)
-        oacc[db] = T::mfma32(as_vec8<vec8>(lds_tr8(vt, vo.lo_at(db) + 16 * g * DV, vo.hi_at(db) + 16 * g * DV)),
+        oacc[db] = T::mfma32(as_vec8<vec8>(lds_tr8(vt[buf], vo.lo_at(db) + 16 * g * DV, vo.hi_at(db) + 16 * g * DV)),
                              as_vec8<vec8>(pw[g]), oacc[db]);
     }
-    __syncthreads();   // every V read of this tile is done before the next tile is staged
+    if (t + 1 < nt) store_tile(buf ^ 1);   // the other buffer's last reads were before the last barrier
+    __syncthreads();
   }
   if (qi >= p.Nq) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
@@ -479,7 +521,7 @@ __global__ __launch_bounds__(256) void wide_chain_kernel(FlashBwdParams p, const
 
 template <typename T, int EP, int DV>
 hipError_t fwd_t(const FlashFwdParams& p, hipStream_t s) {
-  return launch_named("flash_wide_fwd", wide_fwd_kernel<T, EP, DV>, dim3((p.NqP / 32) * p.B * p.Hq), dim3(64), s, p);
+  return launch_named("flash_wide_fwd", wide_fwd_kernel<T, EP, DV>, dim3((p.NqP / 128) * p.B * p.Hq), dim3(256), s, p);
 }
 
 template <typename T, int EP, int DV>
