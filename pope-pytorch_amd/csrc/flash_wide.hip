@@ -7,21 +7,23 @@
 //
 // The rows of these heads do not fit the register tiling of flash_fwd.hip / flash_bwd.hip (the
 // backward's dK_hat accumulator alone is 256 registers per lane at E = 512), so the wide path
-// trades speed for a plain structure: one wave per workgroup, 32 rows per wave, the
-// accumulators of the backward split over kChunks column chunks (each chunk recomputes the
-// scores), and the polar transform's chain rule in a separate pass.  Memory stays linear in the
+// trades speed for a plain structure: four waves per workgroup (one per SIMD, up to 512
+// registers), 32 rows per wave in the forward, the backward's accumulators split over the four
+// waves as column chunks (each chunk recomputes the scores), tiles shared by the four waves through
+// LDS, and the polar transform's chain rule in a separate pass.  Memory stays linear in the
 // sequence length: no score matrix is stored.  Same workspace preparation as the narrow path
 // (flash_prep.hip: K_hat, Q_hat pre-scaled by softmax_scale * log2 e, key visibility words,
 // phase tables), with EP = E rounded up to 128 and DV = 256.
-//   wide_fwd   one wave per (32 queries, batch * head): S^T = K_hat Q_hat^T (K_hat rows from
-//              global memory), online softmax in log2 units, O^T += V^T P^T with V staged in LDS
-//              and read transposed (ds_read_b64_tr_b16).
-//   wide_kv    one wave per (32 keys, column chunk, batch * kv head): S = Q_hat K_hat^T - lse,
-//              dP = dO V^T - delta (Q_hat and dO tiles staged in LDS), P = exp2 S, dS = P dP;
-//              dV (its chunk of D columns) += P^T dO and dK_hat (its chunk of E columns) +=
-//              dS^T Q_hat; writes dV and the raw dK_hat chunk (fp32 workspace).
-//   wide_q     one wave per (32 queries, column chunk, batch * head): S^T, dP^T with the K_hat
-//              tile in LDS, dQ_hat^T (its chunk) += K_hat^T dS^T; writes the raw dQ_hat chunk.
+//   wide_fwd   one workgroup per (128 queries, batch * head): S^T = K_hat Q_hat^T, online softmax
+//              in log2 units, O^T += V^T P^T with V read transposed (ds_read_b64_tr_b16); the
+//              K_hat and V tiles of 32 keys double-buffered in LDS.
+//   wide_kv    one workgroup per (32 keys, batch * kv head), wave = column chunk: S = Q_hat K_hat^T
+//              - lse, dP = dO V^T - delta (Q_hat and dO tiles double-buffered in LDS), P = exp2 S,
+//              dS = P dP; dV (the wave's chunk of D columns) += P^T dO and dK_hat (its chunk of E
+//              columns) += dS^T Q_hat; writes dV and the raw dK_hat chunk (fp32 workspace).
+//   wide_q     one workgroup per (32 queries, batch * head), wave = column chunk: S^T, dP^T with
+//              the K_hat and V tiles in LDS, dQ_hat^T (its chunk) += K_hat^T dS^T; writes the raw
+//              dQ_hat chunk.
 //   wide_chain the chain rule of the polar transform from the raw rows: dk, dq, dfreqs, dbias
 //              (deterministic mode: the per-row phase derivatives, summed later in a fixed order).
 #include "pope_common.hpp"
@@ -31,7 +33,7 @@ namespace pope {
 
 namespace {
 
-constexpr int kChunks = 4;   // column chunks of the backward's accumulators
+constexpr int kChunks = 4;   // column chunks of the backward's accumulators, one per wave of a workgroup
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
@@ -57,32 +59,6 @@ __device__ __forceinline__ f32x16 splat16(float x) {
 
 // Row offset within a 32-row block of register r of a 32x32 MFMA result in lane half hf.
 __device__ __forceinline__ int res_row(int r, int hf) { return 8 * (r >> 2) + 4 * hf + (r & 3); }
-
-// Stages rows [r0, r0 + 32) of a 16-bit row-major source (row stride rs elements) into an LDS
-// tile of `cols` columns, unpadded with the 16-byte units XOR-swizzled by the row (tile_swz: row
-// reads and transposed reads of MFMA operands are then free of bank conflicts): rows past
-// row_last repeat it, 8-column chunks at or past `dlim` are zero (head columns past D).  One
-// wave; four loads in flight before their stores.
-template <int COLS>
-__device__ __forceinline__ void stage32(uint16_t* lds, const uint16_t* src, int64_t rs, int r0, int row_last,
-                                        int dlim) {
-  constexpr int U = COLS / 8, N = 32 * U / 64, G = 4;
-  static_assert(N % G == 0, "whole load groups");
-#pragma unroll
-  for (int i0 = 0; i0 < N; i0 += G) {
-    u32x4 v[G];
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-      const int c = threadIdx.x + 64 * (i0 + i), r = c / U, d0 = 8 * (c % U);
-      v[i] = d0 < dlim ? ld16(src + (int64_t)min(r0 + r, row_last) * rs + d0) : zero4();
-    }
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-      const int c = threadIdx.x + 64 * (i0 + i), r = c / U, u = c % U;
-      *reinterpret_cast<u32x4*>(lds + r * COLS + 8 * (u ^ tile_swz(U, r))) = v[i];
-    }
-  }
-}
 
 // ---- forward ---------------------------------------------------------------------------
 // Four waves per workgroup, 128 query rows (wave w: rows q0 + 32 w ..); per 32-key tile the K_hat
@@ -224,17 +200,21 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(FlashFwdParams p) {
 }
 
 // ---- backward: dK_hat / dV --------------------------------------------------------------
+// One workgroup per (32 keys, batch * kv head), wave w = column chunk w of the accumulators; the
+// Q_hat and dO tiles of each 32-query step go through LDS once for the four waves, double
+// buffered (the next step's loads in flight in registers during the current step).
 template <typename T, int EP, int DV>
-__global__ __launch_bounds__(64) void wide_kv_kernel(FlashBwdParams p, float* wk) {
+__global__ __launch_bounds__(256) void wide_kv_kernel(FlashBwdParams p, float* wk) {
   constexpr int KS = EP / 16, DS = DV / 16, EBC = EP / 32 / kChunks, DBC = DV / 32 / kChunks;
+  constexpr int QU = EP / 8, OU = DV / 8, QN = 32 * QU / 256, ON = 32 * OU / 256;
   typedef typename T::vec8 vec8;
-  __shared__ __attribute__((aligned(16))) uint16_t qt[32 * EP];
-  __shared__ __attribute__((aligned(16))) uint16_t dt[32 * DV];
+  __shared__ __attribute__((aligned(16))) uint16_t qt[2][32 * EP];
+  __shared__ __attribute__((aligned(16))) uint16_t dt[2][32 * DV];
 
-  const int lane = threadIdx.x, lr = lane & 31, hf = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int nkb = p.NkP / 32;
-  const int ec = blockIdx.x % kChunks, rest = blockIdx.x / kChunks;
-  const int k0 = 32 * (rest % nkb), bhk = rest / nkb;   // key block 0 (the heaviest causal one) first
+  const int ec = tid >> 6;   // the wave's column chunk
+  const int k0 = 32 * ((int)blockIdx.x % nkb), bhk = (int)blockIdx.x / nkb;   // key block 0 (the heaviest causal one) first
   const int b = bhk / p.Hk, hk = bhk % p.Hk;
   const int Nk = p.Nk, Nq = p.Nq, D = p.D, NqP = p.NqP;
   if (k0 >= Nk) return;
@@ -259,75 +239,112 @@ __global__ __launch_bounds__(64) void wide_kv_kernel(FlashBwdParams p, float* wk
   for (int x = 0; x < EBC; ++x) dka[x] = splat16(0.f);
 #pragma unroll
   for (int x = 0; x < DBC; ++x) dva[x] = splat16(0.f);
-  const TileOffsets<EP / 8> qo(lane);
-  const TileOffsets<DV / 8> dO(lane);
+  const TileOffsets<QU> qo(lane);
+  const TileOffsets<OU> dO(lane);
 
-  if (__any(kvis)) {
-    const int groups = p.Hq / p.Hk;
-    for (int g = 0; g < groups; ++g) {
-      const int h = g * p.Hk + hk, bh = b * p.Hq + h;
-      const uint16_t* qhb = p.qh + (int64_t)bh * NqP * EP;
-      const uint16_t* dob = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1];
-      const float* nlb = p.nl + (int64_t)bh * NqP;
-      const float* ndb = p.nd + (int64_t)bh * NqP;
-      for (int q0 = p.causal ? k0 : 0; q0 < Nq; q0 += 32) {
-        stage32<EP>(qt, qhb, EP, q0, NqP - 1, EP);
-        stage32<DV>(dt, dob, p.do_s[2], q0, Nq - 1, D);
-        // -lse and -delta of the result rows (queries q0 + res_row(r, hf); padded rows give P = 0)
-        f32x16 nl16, nd16;
+  // the steps: (query head g of the kv head's group, 32-query block q0), flattened
+  const int groups = p.Hq / p.Hk;
+  const int qstart = p.causal ? k0 : 0;
+  const int nsq = Nq > qstart ? (Nq - qstart + 31) / 32 : 0;
+  const int nsteps = __any(kvis) ? groups * nsq : 0;   // uniform over the workgroup (same keys)
+  u32x4 qst[QN], ost[ON];
+  auto step_at = [&](int st, int& h, int& q0) {
+    h = (st / nsq) * p.Hk + hk;
+    q0 = qstart + 32 * (st % nsq);
+  };
+  auto load_tile = [&](int st) {
+    int h, q0;
+    step_at(st, h, q0);
+    const uint16_t* qhb = p.qh + (int64_t)(b * p.Hq + h) * NqP * EP;   // rows padded to NqP
+    const uint16_t* dob = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const f32x4 a = *reinterpret_cast<const f32x4*>(nlb + q0 + 8 * q + 4 * hf);
-          const f32x4 c = *reinterpret_cast<const f32x4*>(ndb + q0 + 8 * q + 4 * hf);
+    for (int i = 0; i < QN; ++i) {
+      const int c = tid + 256 * i;
+      qst[i] = ld16(qhb + (int64_t)(q0 + c / QU) * EP + 8 * (c % QU));
+    }
 #pragma unroll
-          for (int x = 0; x < 4; ++x) {
-            nl16[4 * q + x] = a[x];
-            nd16[4 * q + x] = c[x];
-          }
-        }
-        __syncthreads();   // the tiles' stores are complete
-        // S = Q_hat K_hat^T - lse and dP = dO V^T - delta (rows = queries, lane = key)
-        f32x16 s = nl16, dp = nd16;
+    for (int i = 0; i < ON; ++i) {
+      const int c = tid + 256 * i, d0 = 8 * (c % OU);
+      ost[i] = d0 < D ? ld16(dob + (int64_t)min(q0 + c / OU, Nq - 1) * p.do_s[2] + d0) : zero4();
+    }
+  };
+  auto store_tile = [&](int buf) {
 #pragma unroll
-        for (int kg = 0; kg < KS; kg += 8) {
+    for (int i = 0; i < QN; ++i) {
+      const int c = tid + 256 * i, r = c / QU, u = c % QU;
+      *reinterpret_cast<u32x4*>(qt[buf] + r * EP + 8 * (u ^ tile_swz(QU, r))) = qst[i];
+    }
 #pragma unroll
-          for (int kk = kg; kk < kg + 8; ++kk)
-            s = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(qt + qo.row_at(kk))), kreg[kk], s);
-          __builtin_amdgcn_sched_barrier(0);   // eight operand reads in flight, not all of them
-        }
+    for (int i = 0; i < ON; ++i) {
+      const int c = tid + 256 * i, r = c / OU, u = c % OU;
+      *reinterpret_cast<u32x4*>(dt[buf] + r * DV + 8 * (u ^ tile_swz(OU, r))) = ost[i];
+    }
+  };
+  if (nsteps > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int st = 0; st < nsteps; ++st) {
+    const int buf = st & 1;
+    int h, q0;
+    step_at(st, h, q0);
+    if (st + 1 < nsteps) load_tile(st + 1);
+    const int bh = b * p.Hq + h;
+    const float* nlb = p.nl + (int64_t)bh * NqP;
+    const float* ndb = p.nd + (int64_t)bh * NqP;
+    // -lse and -delta of the result rows (queries q0 + res_row(r, hf); padded rows give P = 0)
+    f32x16 s, dp;
 #pragma unroll
-        for (int kg = 0; kg < DS; kg += 8) {
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(nlb + q0 + 8 * q + 4 * hf);
+      const f32x4 c = *reinterpret_cast<const f32x4*>(ndb + q0 + 8 * q + 4 * hf);
 #pragma unroll
-          for (int kk = kg; kk < kg + 8; ++kk)
-            dp = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(dt + dO.row_at(kk))), vreg[kk], dp);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const bool ok = kvis && (!p.causal || kj <= q0 + res_row(r, hf));
-          const float pv = ok ? __builtin_amdgcn_exp2f(s[r]) : 0.f;
-          s[r] = pv;
-          dp[r] = pv * dp[r];
-        }
-#pragma unroll
-        for (int g2 = 0; g2 < 2; ++g2) {
-          const vec8 ap = as_vec8<vec8>(pack8w<T>(s, g2)), ads = as_vec8<vec8>(pack8w<T>(dp, g2));
-#pragma unroll
-          for (int db = 0; db < DBC; ++db) {
-            const int nb = ec * DBC + db;
-            dva[db] = T::mfma32(ap, as_vec8<vec8>(lds_tr8(dt, dO.lo_at(nb) + 16 * g2 * DV, dO.hi_at(nb) + 16 * g2 * DV)),
-                                dva[db]);
-          }
-#pragma unroll
-          for (int eb = 0; eb < EBC; ++eb) {
-            const int nb = ec * EBC + eb;
-            dka[eb] = T::mfma32(ads, as_vec8<vec8>(lds_tr8(qt, qo.lo_at(nb) + 16 * g2 * EP, qo.hi_at(nb) + 16 * g2 * EP)),
-                                dka[eb]);
-          }
-        }
-        __syncthreads();   // every tile read is done before the next tiles are staged
+      for (int x = 0; x < 4; ++x) {
+        s[4 * q + x] = a[x];
+        dp[4 * q + x] = c[x];
       }
     }
+    // S = Q_hat K_hat^T - lse and dP = dO V^T - delta (rows = queries, lane = key)
+#pragma unroll
+    for (int kg = 0; kg < KS; kg += 8) {
+#pragma unroll
+      for (int kk = kg; kk < kg + 8; ++kk)
+        s = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(qt[buf] + qo.row_at(kk))), kreg[kk], s);
+      __builtin_amdgcn_sched_barrier(0);   // eight operand reads in flight, not all of them
+    }
+#pragma unroll
+    for (int kg = 0; kg < DS; kg += 8) {
+#pragma unroll
+      for (int kk = kg; kk < kg + 8; ++kk)
+        dp = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(dt[buf] + dO.row_at(kk))), vreg[kk], dp);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const bool ok = kvis && (!p.causal || kj <= q0 + res_row(r, hf));
+      const float pv = ok ? __builtin_amdgcn_exp2f(s[r]) : 0.f;
+      s[r] = pv;
+      dp[r] = pv * dp[r];
+    }
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) {
+      const vec8 ap = as_vec8<vec8>(pack8w<T>(s, g2)), ads = as_vec8<vec8>(pack8w<T>(dp, g2));
+#pragma unroll
+      for (int db = 0; db < DBC; ++db) {
+        const int nb = ec * DBC + db;
+        dva[db] = T::mfma32(
+            ap, as_vec8<vec8>(lds_tr8(dt[buf], dO.lo_at(nb) + 16 * g2 * DV, dO.hi_at(nb) + 16 * g2 * DV)), dva[db]);
+      }
+#pragma unroll
+      for (int eb = 0; eb < EBC; ++eb) {
+        const int nb = ec * EBC + eb;
+        dka[eb] = T::mfma32(
+            ads, as_vec8<vec8>(lds_tr8(qt[buf], qo.lo_at(nb) + 16 * g2 * EP, qo.hi_at(nb) + 16 * g2 * EP)), dka[eb]);
+      }
+    }
+    if (st + 1 < nsteps) store_tile(buf ^ 1);   // the other buffer's last reads were before the last barrier
+    __syncthreads();
   }
   // dV (lane = d column, registers = keys); the raw dK_hat chunk, times ln 2 (Q_hat carries log2 e)
   uint16_t* dvb = p.dv + (int64_t)b * p.dv_s[0] + (int64_t)hk * p.dv_s[1];
@@ -350,16 +367,20 @@ __global__ __launch_bounds__(64) void wide_kv_kernel(FlashBwdParams p, float* wk
 }
 
 // ---- backward: dQ_hat -------------------------------------------------------------------
+// One workgroup per (32 queries, batch * head), wave w = column chunk w of the accumulator; the
+// K_hat and V tiles of each 32-key step go through LDS once for the four waves, double buffered.
 template <typename T, int EP, int DV>
-__global__ __launch_bounds__(64) void wide_q_kernel(FlashBwdParams p, float* wq) {
+__global__ __launch_bounds__(256) void wide_q_kernel(FlashBwdParams p, float* wq) {
   constexpr int KS = EP / 16, DS = DV / 16, EBC = EP / 32 / kChunks;
+  constexpr int KU = EP / 8, VU = DV / 8, KN = 32 * KU / 256, VN = 32 * VU / 256;
   typedef typename T::vec8 vec8;
-  __shared__ __attribute__((aligned(16))) uint16_t kt[32 * EP];
+  __shared__ __attribute__((aligned(16))) uint16_t kt[2][32 * EP];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[2][32 * DV];
 
-  const int lane = threadIdx.x, lr = lane & 31, hf = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int nqb = p.NqP / 32;
-  const int ec = blockIdx.x % kChunks, rest = blockIdx.x / kChunks;
-  const int q0 = 32 * (nqb - 1 - rest % nqb), bh = rest / nqb;   // heaviest causal blocks first
+  const int ec = tid >> 6;   // the wave's column chunk
+  const int q0 = 32 * (nqb - 1 - (int)blockIdx.x % nqb), bh = (int)blockIdx.x / nqb;   // heaviest causal blocks first
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const int Nk = p.Nk, Nq = p.Nq, D = p.D;
   if (q0 >= Nq) return;
@@ -383,28 +404,61 @@ __global__ __launch_bounds__(64) void wide_q_kernel(FlashBwdParams p, float* wq)
   for (int x = 0; x < EBC; ++x) dqa[x] = splat16(0.f);
   int nkeys = min(((ci32*)p.kend)[b], Nk);
   if (p.causal) nkeys = min(nkeys, q0 + 32);
-  const uint16_t* khb = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;
+  const uint16_t* khb = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;   // rows padded to NkP
   const uint16_t* vb = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
   cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
-  const TileOffsets<EP / 8> ko(lane);
-  for (int j0 = 0; j0 < nkeys; j0 += 32) {
-    stage32<EP>(kt, khb, EP, j0, p.NkP - 1, EP);
-    __syncthreads();   // the tile's stores are complete
-    // S^T = K_hat Q_hat^T - lse and dP^T = V dO^T - delta (rows = keys, lane = query)
-    const uint16_t* vr = vb + (int64_t)min(j0 + lr, Nk - 1) * p.v_s[2] + 8 * hf;
-    u32x4 va[DS];
+  const TileOffsets<KU> ko(lane);
+  const TileOffsets<VU> vo(lane);
+  u32x4 kst[KN], vst[VN];
+  auto load_tile = [&](int j0) {
 #pragma unroll
-    for (int kk = 0; kk < DS; ++kk) va[kk] = 16 * kk + 8 * hf < D ? ld16(vr + 16 * kk) : zero4();
+    for (int i = 0; i < KN; ++i) {
+      const int c = tid + 256 * i;
+      kst[i] = ld16(khb + (int64_t)(j0 + c / KU) * EP + 8 * (c % KU));
+    }
+#pragma unroll
+    for (int i = 0; i < VN; ++i) {
+      const int c = tid + 256 * i, d0 = 8 * (c % VU);
+      vst[i] = d0 < D ? ld16(vb + (int64_t)min(j0 + c / VU, Nk - 1) * p.v_s[2] + d0) : zero4();
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KN; ++i) {
+      const int c = tid + 256 * i, r = c / KU, u = c % KU;
+      *reinterpret_cast<u32x4*>(kt[buf] + r * EP + 8 * (u ^ tile_swz(KU, r))) = kst[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VN; ++i) {
+      const int c = tid + 256 * i, r = c / VU, u = c % VU;
+      *reinterpret_cast<u32x4*>(vt[buf] + r * DV + 8 * (u ^ tile_swz(VU, r))) = vst[i];
+    }
+  };
+  const int nt = (nkeys + 31) / 32;
+  if (nt > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < nt; ++t) {
+    const int buf = t & 1, j0 = 32 * t;
+    if (t + 1 < nt) load_tile(j0 + 32);
+    // S^T = K_hat Q_hat^T - lse and dP^T = V dO^T - delta (rows = keys, lane = query)
     f32x16 s = splat16(nls), dp = splat16(nds);
 #pragma unroll
     for (int kg = 0; kg < KS; kg += 8) {
 #pragma unroll
       for (int kk = kg; kk < kg + 8; ++kk)
-        s = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt + ko.row_at(kk))), qreg[kk], s);
+        s = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(kt[buf] + ko.row_at(kk))), qreg[kk], s);
       __builtin_amdgcn_sched_barrier(0);   // eight operand reads in flight, not all of them
     }
 #pragma unroll
-    for (int kk = 0; kk < DS; ++kk) dp = T::mfma32(as_vec8<vec8>(va[kk]), doreg[kk], dp);
+    for (int kg = 0; kg < DS; kg += 8) {
+#pragma unroll
+      for (int kk = kg; kk < kg + 8; ++kk)
+        dp = T::mfma32(as_vec8<vec8>(*reinterpret_cast<const u32x4*>(vt[buf] + vo.row_at(kk))), doreg[kk], dp);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     const uint32_t wv = (uint32_t)(mw[j0 >> 6] >> (j0 & 32));
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -418,10 +472,11 @@ __global__ __launch_bounds__(64) void wide_q_kernel(FlashBwdParams p, float* wq)
 #pragma unroll
       for (int eb = 0; eb < EBC; ++eb)
         dqa[eb] = T::mfma32(
-            as_vec8<vec8>(lds_tr8(kt, ko.lo_at(ec * EBC + eb) + 16 * g2 * EP, ko.hi_at(ec * EBC + eb) + 16 * g2 * EP)),
+            as_vec8<vec8>(lds_tr8(kt[buf], ko.lo_at(ec * EBC + eb) + 16 * g2 * EP, ko.hi_at(ec * EBC + eb) + 16 * g2 * EP)),
             bds, dqa[eb]);
     }
-    __syncthreads();   // every tile read is done before the next tile is staged
+    if (t + 1 < nt) store_tile(buf ^ 1);   // the other buffer's last reads were before the last barrier
+    __syncthreads();
   }
   // the raw dQ_hat chunk (rows = e, lane = query), times softmax_scale
   float* wqb = wq + ((int64_t)bh * p.NqP + qi) * EP;
@@ -526,11 +581,10 @@ hipError_t fwd_t(const FlashFwdParams& p, hipStream_t s) {
 
 template <typename T, int EP, int DV>
 hipError_t bwd_t(const FlashBwdParams& p, float* wk, float* wq, hipStream_t s) {
-  hipError_t e = launch_named("flash_wide_kv", wide_kv_kernel<T, EP, DV>, dim3((p.NkP / 32) * p.B * p.Hk * kChunks),
-                              dim3(64), s, p, wk);
+  hipError_t e = launch_named("flash_wide_kv", wide_kv_kernel<T, EP, DV>, dim3((p.NkP / 32) * p.B * p.Hk), dim3(256),
+                              s, p, wk);
   if (e != hipSuccess) return e;
-  e = launch_named("flash_wide_q", wide_q_kernel<T, EP, DV>, dim3((p.NqP / 32) * p.B * p.Hq * kChunks), dim3(64), s,
-                   p, wq);
+  e = launch_named("flash_wide_q", wide_q_kernel<T, EP, DV>, dim3((p.NqP / 32) * p.B * p.Hq), dim3(256), s, p, wq);
   if (e != hipSuccess) return e;
   const int nk = (p.NkP / 32) * p.B * p.Hk, nq = (p.NqP / 32) * p.B * p.Hq;
   return launch_named("flash_wide_chain", wide_chain_kernel<T>, dim3(nk + nq), dim3(256), s, p,
