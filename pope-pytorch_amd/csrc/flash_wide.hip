@@ -33,7 +33,6 @@ namespace pope {
 
 namespace {
 
-constexpr int kChunks = 4;   // column chunks of the backward's accumulators, one per wave of a workgroup
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
@@ -200,27 +199,29 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(FlashFwdParams p) {
 }
 
 // ---- backward: dK_hat / dV --------------------------------------------------------------
-// One workgroup per (32 keys, batch * kv head), wave w = column chunk w of the accumulators; the
-// Q_hat and dO tiles of each 32-query step go through LDS once for the four waves, double
-// buffered (the next step's loads in flight in registers during the current step).
-template <typename T, int EP, int DV>
+// One workgroup per (4 / CH blocks of 32 keys, batch * kv head); wave w takes key block w / CH and
+// column chunk w % CH of the accumulators (CH chunks recompute the scores CH times; fewer where the
+// registers allow).  The Q_hat and dO tiles of each 32-query step go through LDS once for the four
+// waves, double buffered (the next step's loads in flight in registers during the current step).
+template <typename T, int EP, int DV, int CH>
 __global__ __launch_bounds__(256) void wide_kv_kernel(FlashBwdParams p, float* wk) {
-  constexpr int KS = EP / 16, DS = DV / 16, EBC = EP / 32 / kChunks, DBC = DV / 32 / kChunks;
+  constexpr int KS = EP / 16, DS = DV / 16, EBC = EP / 32 / CH, DBC = DV / 32 / CH, RB = 4 / CH;
   constexpr int QU = EP / 8, OU = DV / 8, QN = 32 * QU / 256, ON = 32 * OU / 256;
   typedef typename T::vec8 vec8;
   __shared__ __attribute__((aligned(16))) uint16_t qt[2][32 * EP];
   __shared__ __attribute__((aligned(16))) uint16_t dt[2][32 * DV];
 
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
-  const int nkb = p.NkP / 32;
-  const int ec = tid >> 6;   // the wave's column chunk
-  const int k0 = 32 * ((int)blockIdx.x % nkb), bhk = (int)blockIdx.x / nkb;   // key block 0 (the heaviest causal one) first
+  const int nkb = p.NkP / (32 * RB);
+  const int ec = (tid >> 6) % CH;   // the wave's column chunk
+  const int kb0 = 32 * RB * ((int)blockIdx.x % nkb), bhk = (int)blockIdx.x / nkb;   // key block 0 (the heaviest causal one) first
+  const int k0 = kb0 + 32 * ((tid >> 6) / CH);   // the wave's keys
   const int b = bhk / p.Hk, hk = bhk % p.Hk;
   const int Nk = p.Nk, Nq = p.Nq, D = p.D, NqP = p.NqP;
-  if (k0 >= Nk) return;
+  if (kb0 >= Nk) return;
   const int kj = k0 + lr;
   cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
-  const bool kvis = (mw[kj >> 6] >> (kj & 63)) & 1ull;
+  const bool kvis = kj < Nk && ((mw[kj >> 6] >> (kj & 63)) & 1ull);
 
   vec8 kreg[KS], vreg[DS];
   {
@@ -244,9 +245,9 @@ __global__ __launch_bounds__(256) void wide_kv_kernel(FlashBwdParams p, float* w
 
   // the steps: (query head g of the kv head's group, 32-query block q0), flattened
   const int groups = p.Hq / p.Hk;
-  const int qstart = p.causal ? k0 : 0;
+  const int qstart = p.causal ? kb0 : 0;   // the workgroup's first key block
   const int nsq = Nq > qstart ? (Nq - qstart + 31) / 32 : 0;
-  const int nsteps = __any(kvis) ? groups * nsq : 0;   // uniform over the workgroup (same keys)
+  const int nsteps = __syncthreads_or(kvis) ? groups * nsq : 0;   // uniform over the workgroup
   u32x4 qst[QN], ost[ON];
   auto step_at = [&](int st, int& h, int& q0) {
     h = (st / nsq) * p.Hk + hk;
@@ -367,23 +368,25 @@ __global__ __launch_bounds__(256) void wide_kv_kernel(FlashBwdParams p, float* w
 }
 
 // ---- backward: dQ_hat -------------------------------------------------------------------
-// One workgroup per (32 queries, batch * head), wave w = column chunk w of the accumulator; the
-// K_hat and V tiles of each 32-key step go through LDS once for the four waves, double buffered.
-template <typename T, int EP, int DV>
+// One workgroup per (4 / CH blocks of 32 queries, batch * head); wave w takes query block w / CH
+// and column chunk w % CH of the accumulator.  The K_hat and V tiles of each 32-key step go
+// through LDS once for the four waves, double buffered.
+template <typename T, int EP, int DV, int CH>
 __global__ __launch_bounds__(256) void wide_q_kernel(FlashBwdParams p, float* wq) {
-  constexpr int KS = EP / 16, DS = DV / 16, EBC = EP / 32 / kChunks;
+  constexpr int KS = EP / 16, DS = DV / 16, EBC = EP / 32 / CH, RB = 4 / CH;
   constexpr int KU = EP / 8, VU = DV / 8, KN = 32 * KU / 256, VN = 32 * VU / 256;
   typedef typename T::vec8 vec8;
   __shared__ __attribute__((aligned(16))) uint16_t kt[2][32 * EP];
   __shared__ __attribute__((aligned(16))) uint16_t vt[2][32 * DV];
 
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
-  const int nqb = p.NqP / 32;
-  const int ec = tid >> 6;   // the wave's column chunk
-  const int q0 = 32 * (nqb - 1 - (int)blockIdx.x % nqb), bh = (int)blockIdx.x / nqb;   // heaviest causal blocks first
+  const int nqb = p.NqP / (32 * RB);
+  const int ec = (tid >> 6) % CH;   // the wave's column chunk
+  const int qb0 = 32 * RB * (nqb - 1 - (int)blockIdx.x % nqb), bh = (int)blockIdx.x / nqb;   // heaviest causal blocks first
+  const int q0 = qb0 + 32 * ((tid >> 6) / CH);   // the wave's queries
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const int Nk = p.Nk, Nq = p.Nq, D = p.D;
-  if (q0 >= Nq) return;
+  if (qb0 >= Nq) return;
   const int qi = q0 + lr;
 
   vec8 qreg[KS], doreg[DS];
@@ -403,7 +406,7 @@ __global__ __launch_bounds__(256) void wide_q_kernel(FlashBwdParams p, float* wq
 #pragma unroll
   for (int x = 0; x < EBC; ++x) dqa[x] = splat16(0.f);
   int nkeys = min(((ci32*)p.kend)[b], Nk);
-  if (p.causal) nkeys = min(nkeys, q0 + 32);
+  if (p.causal) nkeys = min(nkeys, qb0 + 32 * RB);   // the workgroup's last query block
   const uint16_t* khb = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;   // rows padded to NkP
   const uint16_t* vb = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
   cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
@@ -579,12 +582,20 @@ hipError_t fwd_t(const FlashFwdParams& p, hipStream_t s) {
   return launch_named("flash_wide_fwd", wide_fwd_kernel<T, EP, DV>, dim3((p.NqP / 128) * p.B * p.Hq), dim3(256), s, p);
 }
 
+// Column chunks per row block: as few as the registers allow (each chunk recomputes the scores).
+template <int EP>
+constexpr int kv_chunks() { return EP <= 256 ? 2 : 4; }
+template <int EP>
+constexpr int q_chunks() { return EP <= 256 ? 1 : EP <= 384 ? 2 : 4; }
+
 template <typename T, int EP, int DV>
 hipError_t bwd_t(const FlashBwdParams& p, float* wk, float* wq, hipStream_t s) {
-  hipError_t e = launch_named("flash_wide_kv", wide_kv_kernel<T, EP, DV>, dim3((p.NkP / 32) * p.B * p.Hk), dim3(256),
-                              s, p, wk);
+  constexpr int CK = kv_chunks<EP>(), CQ = q_chunks<EP>();
+  hipError_t e = launch_named("flash_wide_kv", wide_kv_kernel<T, EP, DV, CK>, dim3((p.NkP / (128 / CK)) * p.B * p.Hk),
+                              dim3(256), s, p, wk);
   if (e != hipSuccess) return e;
-  e = launch_named("flash_wide_q", wide_q_kernel<T, EP, DV>, dim3((p.NqP / 32) * p.B * p.Hq), dim3(256), s, p, wq);
+  e = launch_named("flash_wide_q", wide_q_kernel<T, EP, DV, CQ>, dim3((p.NqP / (128 / CQ)) * p.B * p.Hq), dim3(256), s,
+                   p, wq);
   if (e != hipSuccess) return e;
   const int nk = (p.NkP / 32) * p.B * p.Hk, nq = (p.NqP / 32) * p.B * p.Hq;
   return launch_named("flash_wide_chain", wide_chain_kernel<T>, dim3(nk + nq), dim3(256), s, p,
