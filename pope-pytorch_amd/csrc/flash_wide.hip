@@ -8,20 +8,21 @@
 // The rows of these heads do not fit the register tiling of flash_fwd.hip / flash_bwd.hip (the
 // backward's dK_hat accumulator alone is 256 registers per lane at E = 512), so the wide path
 // trades speed for a plain structure: four waves per workgroup (one per SIMD, up to 512
-// registers), 32 rows per wave in the forward, the backward's accumulators split over the four
-// waves as column chunks (each chunk recomputes the scores), tiles shared by the four waves through
-// LDS, and the polar transform's chain rule in a separate pass.  Memory stays linear in the
+// registers), 32 rows per wave, the backward's accumulators split into as few column chunks as the
+// registers allow (each chunk recomputes the scores; the other waves take neighbouring row blocks),
+// tiles shared by the four waves through LDS, and the polar transform's chain rule in a separate
+// pass.  Memory stays linear in the
 // sequence length: no score matrix is stored.  Same workspace preparation as the narrow path
 // (flash_prep.hip: K_hat, Q_hat pre-scaled by softmax_scale * log2 e, key visibility words,
 // phase tables), with EP = E rounded up to 128 and DV = 256.
 //   wide_fwd   one workgroup per (128 queries, batch * head): S^T = K_hat Q_hat^T, online softmax
 //              in log2 units, O^T += V^T P^T with V read transposed (ds_read_b64_tr_b16); the
 //              K_hat and V tiles of 32 keys double-buffered in LDS.
-//   wide_kv    one workgroup per (32 keys, batch * kv head), wave = column chunk: S = Q_hat K_hat^T
+//   wide_kv    one workgroup per (key blocks, batch * kv head), wave = (32 keys, column chunk): S = Q_hat K_hat^T
 //              - lse, dP = dO V^T - delta (Q_hat and dO tiles double-buffered in LDS), P = exp2 S,
 //              dS = P dP; dV (the wave's chunk of D columns) += P^T dO and dK_hat (its chunk of E
 //              columns) += dS^T Q_hat; writes dV and the raw dK_hat chunk (fp32 workspace).
-//   wide_q     one workgroup per (32 queries, batch * head), wave = column chunk: S^T, dP^T with
+//   wide_q     one workgroup per (query blocks, batch * head), wave = (32 queries, column chunk): S^T, dP^T with
 //              the K_hat and V tiles in LDS, dQ_hat^T (its chunk) += K_hat^T dS^T; writes the raw
 //              dQ_hat chunk.
 //   wide_chain the chain rule of the polar transform from the raw rows: dk, dq, dfreqs, dbias
