@@ -220,8 +220,8 @@ __device__ __forceinline__ void tile_frag(const uint16_t* t, int r, int u, int l
 // stream with two steps in flight (LDS buffer (s & 1) holds step s, register set (s + 1) & 1 step
 // s + 1, the other set receives step s + 2, clamped to the last step), so a tile's first loads
 // overlap the previous tile's products and its S stores.
-__global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p, SimSplit sp, int nib, int njb,
-                                                                    int tpw) {
+template <int tpw>
+__global__ __launch_bounds__(kThreads, 2) void sim_split_fwd_kernel(SimParams p, SimSplit sp, int nib, int njb) {
   __shared__ __attribute__((aligned(16))) uint16_t ts[2][2][kTile];   // [buffer][Q_hat, K_hat]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
@@ -596,9 +596,11 @@ hipError_t launch_sim_split_fwd(const SimParams& p, const SimSplit& sp, hipStrea
   const int nib = (p.Nq + 127) / 128, njb = (p.Nk + 127) / 128;
   // tiles per workgroup: 4 while that still leaves 1,024 workgroups (two rounds at two per CU), else 2
   const int64_t rows = (int64_t)nib * p.B * p.Hq;
-  const int tpw = rows * ((njb + 3) / 4) >= 1024 ? 4 : 2;
-  return launch_named("sim_split_fwd", sim_split_fwd_kernel, dim3((unsigned)(rows * ((njb + tpw - 1) / tpw))),
-                      dim3(kThreads), s, p, sp, nib, njb, tpw);
+  if (rows * ((njb + 3) / 4) >= 1024)
+    return launch_named("sim_split_fwd", sim_split_fwd_kernel<4>, dim3((unsigned)(rows * ((njb + 3) / 4))),
+                        dim3(kThreads), s, p, sp, nib, njb);
+  return launch_named("sim_split_fwd", sim_split_fwd_kernel<2>, dim3((unsigned)(rows * ((njb + 1) / 2))),
+                      dim3(kThreads), s, p, sp, nib, njb);
 }
 
 hipError_t launch_sim_split_bwd(const SimParams& p, const SimSplit& sp, float* U, float* W, hipStream_t s) {
