@@ -296,3 +296,33 @@ def test_registered_op_checks_on_the_decode_path(cuda):
     o, lse, ws = flash_fwd_op(*args)
     assert ws.numel() == 0
     torch.library.opcheck(flash_fwd_op, args, test_utils=("test_schema", "test_faketensor"))
+
+
+def test_workspace_reuse_off_gives_the_same_gradients(cuda):
+    """set_flash_workspace_reuse(False): the forward's workspace is not kept, the backward repeats
+    the preparation, and o, dq, dk, dv are bitwise those of the default path (dfreqs / dbias add
+    fp32 atomics in an arbitrary order, so they agree to rounding)."""
+    import pope_amd
+    from pope_amd import hip_pope_flash_attn as fa
+    inp = make_pope_inputs(41, 2, 4, 2, 300, 300, 64, 32, torch.bfloat16, mask_kind="prefix")
+
+    def run():
+        t = [inp[n].detach().clone().cuda().requires_grad_(True) for n in ("q", "k", "v", "freqs", "bias")]
+        mask = inp["mask"].cuda() if inp["mask"] is not None else None
+        o = pope_amd.flash_attn_with_pope(t[0], t[1], t[2], pos_emb=(t[3], t[4]), mask=mask, causal=True)
+        o.backward(inp["do"].cuda())
+        torch.cuda.synchronize()
+        return [o.detach()] + [x.grad for x in t], fa._LAST_BWD_PREPARED
+
+    ref, prepared = run()
+    assert prepared
+    fa.set_flash_workspace_reuse(False)
+    try:
+        got, prepared = run()
+    finally:
+        fa.set_flash_workspace_reuse(True)
+    assert not prepared
+    for a, b in zip(got[:4], ref[:4]):
+        assert torch.equal(a, b)
+    for a, b in zip(got[4:], ref[4:]):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5 * b.abs().max().item())
