@@ -168,8 +168,9 @@ int pope_flash_bwd(const pope_desc* desc, const void* dout, const void* q, const
  * cache (decode): split-K over the keys plus an LSE merge.  Same contract as
  * pope_flash_fwd; returns
  * POPE_ERR_UNSUPPORTED (callers then use pope_flash_fwd) for: Nq != 1; causal; head
- * dim above 128; per-head freqs tables (f_s[1] != 0); query heads x head dim above
- * 4096 (the query weights are staged in LDS); freqs rows that are not 16-byte
+ * dim above 128; per-head freqs tables (f_s[1] != 0); no power-of-two group of the
+ * query heads (dividing Hq) with at most 4096 query-weight words (group heads x head
+ * dim: the weights are staged in LDS, one group per workgroup); freqs rows that are not 16-byte
  * aligned (pointer, f_s[0] or f_s[2] not a multiple of 4 floats); K / V row offsets
  * within a (batch, head) beyond 32 bits.  Replaces flash_attn_forward at
  * seqlen_q = 1 (triton_pope_flash_attn.py:222-271 with grid (1, B*H)).

@@ -8,10 +8,11 @@
 //
 // The path is bound by HBM: every valid key costs 2 * D * 2 bytes of K and V
 // and a handful of flops.  Work decomposition (two launches):
-//   decode_split : one workgroup (4 waves) per (batch, split of S keys), covering
-//                  every query head of the batch; wave w takes heads w, w + 4, ...
+//   decode_split : one workgroup (4 waves) per (batch, split of S keys, group of query
+//                  heads: all of them unless their query weights exceed the LDS array);
+//                  wave w takes the group's heads w, w + 4, ...
 //                  A split whose keys are all masked exits after reading its mask
-//                  bytes.  The workgroup computes the batch's query weights (below)
+//                  bytes.  The workgroup computes its heads' query weights (below)
 //                  into LDS, and the cos / sin of its rows of F (fp16 pairs, from the
 //                  fp32 rows of the caller's freqs, which every batch's splits read
 //                  out of L2), staged in LDS once and shared by all heads.  A wave load reads
@@ -83,8 +84,9 @@ __device__ __forceinline__ uint32_t query_weight(const DecodeParams& p, int b, i
   return __builtin_bit_cast(uint32_t, qv * p.scale_log2);
 }
 
-// Split kernel.  A workgroup (4 waves) owns one (batch, split of S keys) for every query head;
-// wave w takes heads w, w + 4, ...  Lane = row r * LPK + chunk c: a load instruction of a wave
+// Split kernel.  A workgroup (4 waves) owns one (batch, split of S keys) for one group of query
+// heads (hgroups groups of Hq / hgroups heads: one group unless the heads' query weights exceed
+// kQwMax words); wave w takes the group's heads w, w + 4, ...  Lane = row r * LPK + chunk c: a load instruction of a wave
 // reads RPI = 64 / LPK consecutive key rows of one head (LPK lanes x 16 bytes per row), so a
 // wave streams contiguous memory, and load u of a head covers keys u * RPI + r.  A head's
 // kLoads K rows and kLoads V rows are all in flight before its scores are computed (the V
@@ -131,8 +133,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane / LPK, c = lane % LPK;
-  const int split = blockIdx.x % p.splits;
-  const int b = blockIdx.x / p.splits;
+  const int hg = blockIdx.x % p.hgroups, rest = blockIdx.x / p.hgroups;
+  const int split = rest % p.splits, b = rest / p.splits;
+  const int HG = p.Hq / p.hgroups, h_lo = hg * HG, h_hi = h_lo + HG;   // the workgroup's query heads
   const int D = p.D, R = p.R, Nk = p.Nk;
   const int d0 = 8 * c;
   const bool cact = d0 < D;
@@ -149,8 +152,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
     vis_any |= v;
   }
   if (!__syncthreads_or(vis_any)) {
-    for (int i = tid; i < p.Hq * (D + 2); i += kThreads) {
-      const int h = i / (D + 2), e = i % (D + 2);
+    for (int i = tid; i < HG * (D + 2); i += kThreads) {
+      const int h = h_lo + i / (D + 2), e = i % (D + 2);
       const int64_t row = ((int64_t)b * p.Hq + h) * p.splits + split;
       if (e < D) p.part_o[row * D + e] = 0.f;
       else p.part_ml[row * 2 + (e - D)] = e == D ? -INFINITY : 0.f;
@@ -178,7 +181,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
   // The query weight words of a head: two 16-byte LDS reads at the clamped chunk.
   u32x4 qwc[2];
   auto qwload = [&](int h) {
-    const uint32_t a = lds_addr(qw_s + h * D + dcl);
+    const uint32_t a = lds_addr(qw_s + (h - h_lo) * D + dcl);
     qwc[0] = lds_read16_at(a);
     qwc[1] = lds_read16_at(a + 16);
   };
@@ -193,7 +196,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
 
   // ---- the split's phase rows F[j] (rows past Nk repeat the last row), then the first head's
   // K and V rows, all issued before the rows' (cos, sin) are computed and stored to LDS as fp16
-  // pairs: the K / V loads do not wait for that round trip.  Waves past Hq load a valid head and
+  // pairs: the K / V loads do not wait for that round trip.  Waves past the group's heads load a valid head and
   // never use it.  The rows of the freqs table are read by every batch's splits (L2 hits after
   // the first): no table is built beforehand.
   constexpr int C4 = RMAX / 4;                        // 16-byte chunks per staged row
@@ -210,7 +213,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  const int h0 = min(wave, p.Hq - 1);
+  const int h0 = min(h_lo + wave, h_hi - 1);
   load(kb, kptr(h0), ks2);
   __builtin_amdgcn_sched_barrier(0);
   load(vb, vptr(h0), vs2);
@@ -232,8 +235,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
       }
     }
   }
-  // query weights of every head of the batch (after the rows: their registers are free again)
-  for (int i = tid; i < p.Hq * D; i += kThreads) qw_s[i] = query_weight<T>(p, b, i / D, i % D);
+  // query weights of the workgroup's heads (after the rows: their registers are free again)
+  for (int i = tid; i < HG * D; i += kThreads) qw_s[i] = query_weight<T>(p, b, h_lo + i / D, i % D);
   if constexpr (T::kCode == 2) {
     for (int i = tid; i < kSpN; i += kThreads) {
       const float t = __builtin_bit_cast(float, (uint32_t)(i + kSpLo) << 16);
@@ -331,10 +334,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
       p.part_ml[row * 2 + 1] = l;
     }
   };
-  if (wave < p.Hq) {
-    qwload(wave);
-    int h = wave;
-    for (; h + kWaves < p.Hq; h += kWaves) head(h, std::true_type{});
+  if (h_lo + wave < h_hi) {
+    int h = h_lo + wave;
+    qwload(h);
+    for (; h + kWaves < h_hi; h += kWaves) head(h, std::true_type{});
     head(h, std::false_type{});
   }
 }
@@ -414,9 +417,11 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
 }
 
 template <typename T, int LPK, int RMAX>
-hipError_t launch_t(const DecodeParams& p, hipStream_t s) {
-  hipError_t e = launch_named("flash_decode_split", decode_split_kernel<T, LPK, RMAX>, dim3(p.B * p.splits),
-                              dim3(kThreads), s, p);
+hipError_t launch_t(const DecodeParams& p0, hipStream_t s) {
+  DecodeParams p = p0;
+  p.hgroups = decode_head_groups(p.Hq, p.D);
+  hipError_t e = launch_named("flash_decode_split", decode_split_kernel<T, LPK, RMAX>,
+                              dim3(p.B * p.splits * p.hgroups), dim3(kThreads), s, p);
   if (e != hipSuccess) return e;
   return launch_named("flash_decode_combine", decode_combine_kernel<T>, dim3(p.B * p.Hq), dim3(256), s, p);
 }
@@ -468,11 +473,16 @@ int decode_split_keys(int D) {
   return chunks <= 4 ? split_rows<4>() : chunks <= 8 ? split_rows<8>() : split_rows<16>();
 }
 
-int decode_max_query_words() { return kQwMax; }
+int decode_head_groups(int Hq, int D) {
+  for (int g = 1; g <= Hq; g *= 2)
+    if (Hq % g == 0 && (Hq / g) * D <= kQwMax) return g;
+  return 0;
+}
 
 hipError_t launch_flash_decode(const DecodeParams& p, int dtype, hipStream_t s) {
   // per-head phase tables would need a table chunk per head: the general forward covers them
-  if (p.Nq != 1 || p.causal || p.D > 128 || p.t_sh != 0 || p.Hq * p.D > kQwMax) return hipErrorInvalidValue;
+  if (p.Nq != 1 || p.causal || p.D > 128 || p.t_sh != 0 || decode_head_groups(p.Hq, p.D) == 0)
+    return hipErrorInvalidValue;
   return dtype == 2 ? dispatch<BF16>(p, s) : dispatch<F16>(p, s);
 }
 

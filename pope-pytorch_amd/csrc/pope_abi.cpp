@@ -593,9 +593,9 @@ int pope_flash_decode(const pope_desc* d, const void* q, const void* k, const vo
                                       "(got %d rows, causal %d, head dim %d)", d->Nq, d->causal, d->D);
   if (d->R > 0 && d->f_s[1] != 0)
     return fail(POPE_ERR_UNSUPPORTED, "decode kernel: per-head freqs tables are not covered");
-  if ((int64_t)d->Hq * d->D > pope::decode_max_query_words())
-    return fail(POPE_ERR_UNSUPPORTED, "decode kernel: query heads x head dim = %lld exceeds %d",
-                (long long)d->Hq * d->D, pope::decode_max_query_words());
+  if (pope::decode_head_groups(d->Hq, d->D) == 0)
+    return fail(POPE_ERR_UNSUPPORTED, "decode kernel: no power-of-two group of the %d query heads has at most "
+                "4096 query-weight words (head dim %d)", d->Hq, d->D);
   // the split kernel reads freqs rows as 16-byte vectors
   if (d->R > 0 && ((reinterpret_cast<uintptr_t>(freqs) & 15u) || d->f_s[0] % 4 || d->f_s[2] % 4))
     return fail(POPE_ERR_UNSUPPORTED, "decode kernel: freqs rows must be 16-byte aligned");

@@ -181,15 +181,18 @@ struct DecodeParams {
   uint16_t* o; float* lse;
   float* part_o; float* part_ml;   // split-K partials (B*Hq*Nq, splits, D) and (.., splits, 2)
   int B, Hq, Hk, Nq, Nk, D, R, causal, has_mask, splits, keys_per_split;
+  int hgroups;                     // query-head groups per split (set by launch_flash_decode)
   float scale_log2;
   int64_t q_s[3], k_s[3], v_s[3], o_s[3], f_s[3];
   int64_t bias_sh, mask_sb, t_sb, t_sh;
 };
 // Keys per split of the decode kernel at head dim D.  launch_flash_decode returns
 // hipErrorInvalidValue for shapes the kernel does not cover (Nq != 1, causal, D > 128, per-head
-// freqs, more than decode_max_query_words() query heads x head dim).
+// freqs, decode_head_groups(Hq, D) == 0).
 int decode_split_keys(int D);
-int decode_max_query_words();
+// Query-head groups per split workgroup: the fewest (a power of two dividing Hq) whose heads'
+// query weights fit the kernel's 4096-word LDS array, or 0 when none does.
+int decode_head_groups(int Hq, int D);
 // The decode's scratch array on the current device (its device address, looked up once per
 // device): kDecodeScratchBytes, for the entry point that allocates nothing.
 constexpr size_t kDecodeScratchBytes = (size_t)16 << 20;

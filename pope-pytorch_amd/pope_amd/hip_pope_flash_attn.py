@@ -171,7 +171,18 @@ def _check_fp16_range(*ts):
 
 
 _INT32_MAX = 2 ** 31 - 1
-_DECODE_QUERY_WORDS = 4096   # decode_max_query_words() of the library
+_DECODE_QUERY_WORDS = 4096   # query-weight words a decode workgroup stages in LDS
+
+
+def _decode_head_groups(Hq: int, D: int) -> int:
+    """decode_head_groups() of the library: the fewest power-of-two groups of the query heads
+    whose query weights fit the decode workgroup's LDS array, or 0 when none does."""
+    g = 1
+    while g <= Hq:
+        if Hq % g == 0 and (Hq // g) * D <= _DECODE_QUERY_WORDS:
+            return g
+        g *= 2
+    return 0
 
 
 def _decode_eligible(q, k, v, freqs, causal) -> bool:
@@ -184,8 +195,8 @@ def _decode_eligible(q, k, v, freqs, causal) -> bool:
     R = freqs.shape[-1] if exists(freqs) else 0
     if Nq != 1 or causal or Nk < 1024 or D > 128:
         return False
-    if Hq * D > _DECODE_QUERY_WORDS:
-        return False   # the kernel stages Hq * D query weights in LDS
+    if _decode_head_groups(Hq, D) == 0:
+        return False   # a workgroup stages its group's query weights in LDS
     if R and (_freqs_strides(freqs)[1] != 0 or any(st % 4 for st in _freqs_strides(freqs))):
         return False   # per-head tables, or rows that are not whole 16-byte vectors
     return (Nk - 1) * max(k.stride(2), v.stride(2)) + D < _INT32_MAX

@@ -164,11 +164,20 @@ def test_fp32_flash_rejects_values_beyond_fp16(cuda):
         pope_amd.flash_attn_with_pope(q, inp["k"], inp["v"], pos_emb=(inp["freqs"], inp["bias"]))
 
 
-def test_decode_shape_beyond_the_split_kernel(cuda):
-    """Nq = 1 with query heads x head dim = 8192, above what the split kernel stages in LDS (4096):
-    the call takes the general forward and must still match the oracle."""
+def test_decode_head_groups(cuda):
+    """Nq = 1 with query heads x head dim = 8192, above what one split workgroup stages in LDS
+    (4096 query-weight words): the split kernel runs with two groups of 32 heads per split, and
+    must match the oracle."""
+    from pope_amd import _lib
     inp = _decode_inputs(71, 2, 64, 16, 2048, 128, 64, torch.bfloat16)
-    res = _run(inp)
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    try:
+        res = _run(inp)
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    assert "flash_decode_split" in _lib.profile_read()
     ref = oracle_attention(inp, False, grads=False)
     err = max_abs(res["o"], ref["o"])
     print(f"o={err:.2e}")
