@@ -46,10 +46,6 @@ namespace {
 constexpr int kThreads = 256;
 
 
-__device__ __forceinline__ float2 half2f(uint32_t w) {
-  const f16x2 v = __builtin_bit_cast(f16x2, w);
-  return make_float2((float)v[0], (float)v[1]);
-}
 
 // Sum over aligned groups of LPK lanes (LPK = 4, 8 or 16) with DPP lane moves (VALU, no LDS
 // round trip): xor 1 and xor 2 by quad permutes, then the half-row mirror (lane i <-> 7 - i in
