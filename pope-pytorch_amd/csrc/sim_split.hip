@@ -23,14 +23,14 @@
 
 #include "pope_common.hpp"
 #include "pope_kernels.hpp"
-#include "sim_phase.hpp"
 
 namespace pope {
 
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int64_t kSimMinJobs = 512;   // U / W workgroups below which each job's reduction is split
+constexpr int64_t kSimMinJobs = 512;
+constexpr int kPrepItems = 2;          // plane preparation items per thread   // U / W workgroups below which each job's reduction is split
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
@@ -51,132 +51,152 @@ __device__ __forceinline__ f32x16 mfma3(u32x4 ah, u32x4 al, u32x4 bh, u32x4 bl, 
   return BF16::mfma32(as_vec8<v8>(ah), as_vec8<v8>(bh), c);
 }
 
-// Expanded 8 columns [e0, e0 + 8) of one row (zeros past the row count or past E); the same
-// transform as the fp32 path (sim.hip).  cs8: the (cos, sin) pairs of the rotated dims the
-// columns belong to (dims e0 .. e0 + 7 for cos columns, e0 - R .. for sin columns).
-__device__ __forceinline__ void expand_row8(const float* x, const float2* cs8, int e0, int R, int E, bool valid,
-                                            float* out) {
-  if (!valid || e0 >= E) {
-#pragma unroll
-    for (int s = 0; s < 8; ++s) out[s] = 0.f;
-    return;
-  }
-  const bool is_cos = e0 < R, is_sin = !is_cos && e0 < 2 * R;
-  const int d0 = is_cos ? e0 : e0 - R;
-  const float4 x0 = *reinterpret_cast<const float4*>(x + d0);
-  const float4 x1 = *reinterpret_cast<const float4*>(x + d0 + 4);
-  const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-  if (is_cos || is_sin) {
-#pragma unroll
-    for (int s = 0; s < 8; ++s) out[s] = softplus_f(xv[s]) * (is_cos ? cs8[s].x : cs8[s].y);
-  } else {
-#pragma unroll
-    for (int s = 0; s < 8; ++s) out[s] = xv[s];
-  }
-}
-
 // Work items per row of the split planes: R / 8 rotated dim groups (each a cos and a sin chunk of
 // 8 columns, one phase evaluation for both), then one item per other 8-column chunk (pass-through
 // dims, zero padding up to EP).
 __host__ __device__ __forceinline__ int prep_items(int EP, int R) { return EP / 8 - R / 8; }
 
-// One thread per (row, item); blocks [0, nb0) take side 0 (query rows of (b, h), phase row
-// q_off + i, no bias), the rest side 1 (key rows of (b, hk), phase fl(F_j + bias)).  The phases
-// come from the tables when present, else are computed in place (sim_phase).
+// The split kernels never get phase tables (those are built for the fp32 kernels only): the
+// phases are computed in place, theta = F[b, h, n, d] for queries (n = Nk - Nq + i, no bias) and
+// fl(F[b, hk, n, d] + bias[hk, d]) for keys (pope.py:56, triton_pope.py:76: the sum rounded to
+// fp32 first), then sincos_rev.  Items: (row, 8-column chunk), the query rows of every (b, h)
+// first (side 0), then the key rows of every (b, hk) (side 1).  Each thread takes items i, i + T, i + 2T, ... (T threads in
+// the grid) with the next item's loads issued before the current item is expanded and stored,
+// so the loads, the arithmetic and the stores of the grid overlap instead of running as three
+// chip-wide phases.
 // transposed = 0: planes (heads, NP, EP); 1: planes (heads, EP, NP), rows fastest over threads so
 // that each 2-byte store of a wave covers 64 consecutive rows.
-__global__ __launch_bounds__(kThreads) void sim_split_prep_kernel(SimParams p, SimSplit sp, int nb0, int transposed) {
-  const int side = (int)blockIdx.x < nb0 ? 0 : 1;
-  const int heads = side == 0 ? p.B * p.Hq : p.B * p.Hk;
-  const int N = side == 0 ? p.Nq : p.Nk, NP = side == 0 ? sp.NqP : sp.NkP;
-  const int R = p.R, nch = prep_items(p.EP, R);
-  const int64_t total = (int64_t)heads * NP * nch;
-  const int64_t idx = (int64_t)(side == 0 ? blockIdx.x : blockIdx.x - nb0) * kThreads + threadIdx.x;
-  if (idx >= total) return;
-  int bh, n, ch;
-  if (total < INT32_MAX) {   // the usual case: 32-bit index decomposition
-    const int i = (int)idx;
-    if (transposed) {
-      n = i % NP;
-      const int r = i / NP;
-      ch = r % nch;
-      bh = r / nch;
-    } else {
-      ch = i % nch;
-      const int r = i / nch;
-      n = r % NP;
-      bh = r / NP;
-    }
-  } else if (transposed) {
-    n = (int)(idx % NP);
-    const int64_t r = idx / NP;
-    ch = (int)(r % nch);
-    bh = (int)(r / nch);
-  } else {
-    ch = (int)(idx % nch);
-    const int64_t r = idx / nch;
-    n = (int)(r % NP);
-    bh = (int)(r / NP);
-  }
+struct PrepItem {
+  int side, bh, n, ch;
+};
+struct PrepIn {
+  float4 x0, x1;   // the row's input values at dims [8 ch, 8 ch + 8) (clamped)
+  float f[8];      // F at the phase row, rotated dims [8 ch, 8 ch + 8) (clamped)
+  float bb[8];     // the key side's bias at those dims
+};
+
+__global__ __launch_bounds__(kThreads) void sim_split_prep_kernel(SimParams p, SimSplit sp, int transposed) {
+  const int R = p.R, D = p.D, nch = prep_items(p.EP, R);
+  const int64_t total0 = (int64_t)p.B * p.Hq * sp.NqP * nch;
+  const int64_t total = total0 + (int64_t)p.B * p.Hk * sp.NkP * nch;
+  const int64_t T = (int64_t)gridDim.x * kThreads;
+  int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= total) return;
   const int q_off = p.Nk - p.Nq;
-  const int nn = min(n, N - 1);
-  const int hh = side == 0 ? bh % p.Hq : bh % p.Hk, b = side == 0 ? bh / p.Hq : bh / p.Hk;
-  const float* x = side == 0 ? p.q + (int64_t)b * p.q_s[0] + (int64_t)hh * p.q_s[1] + (int64_t)nn * p.q_s[2]
-                             : p.k + (int64_t)b * p.k_s[0] + (int64_t)hh * p.k_s[1] + (int64_t)nn * p.k_s[2];
-  uint16_t* ph = side == 0 ? sp.qh : sp.kh;
-  uint16_t* pl = side == 0 ? sp.ql : sp.kl;
-  auto store = [&](int e0, const float* v) {   // split 8 columns [e0, e0 + 8) of the row
-    u32x4 hi, lo;
-    split8(v, hi, lo);
-    if (!transposed) {
-      const int64_t o = ((int64_t)bh * NP + n) * p.EP + e0;
-      *reinterpret_cast<u32x4*>(ph + o) = hi;
-      *reinterpret_cast<u32x4*>(pl + o) = lo;
+
+  auto item = [&](int64_t g) {
+    PrepItem it;
+    it.side = g < total0 ? 0 : 1;
+    const int64_t x = it.side == 0 ? g : g - total0;
+    const int NP = it.side == 0 ? sp.NqP : sp.NkP;
+    if (total < INT32_MAX) {   // the usual case: 32-bit index decomposition
+      const int xi = (int)x;
+      if (transposed) {
+        it.n = xi % NP;
+        const int r = xi / NP;
+        it.ch = r % nch;
+        it.bh = r / nch;
+      } else {
+        it.ch = xi % nch;
+        const int r = xi / nch;
+        it.n = r % NP;
+        it.bh = r / NP;
+      }
+    } else if (transposed) {
+      it.n = (int)(x % NP);
+      const int64_t r = x / NP;
+      it.ch = (int)(r % nch);
+      it.bh = (int)(r / nch);
     } else {
-      const int64_t o = ((int64_t)bh * p.EP + e0) * NP + n;
+      it.ch = (int)(x % nch);
+      const int64_t r = x / nch;
+      it.n = (int)(r % NP);
+      it.bh = (int)(r / NP);
+    }
+    return it;
+  };
+  // Branch-free loads at clamped rows and dims: an item past the rows or past D stores zeros.
+  auto load = [&](const PrepItem& it) {
+    PrepIn in;
+    const int heads_h = it.side == 0 ? p.Hq : p.Hk;
+    const int N = it.side == 0 ? p.Nq : p.Nk;
+    const int hh = it.bh % heads_h, b = it.bh / heads_h;
+    const int nn = min(it.n, N - 1);
+    const float* x = it.side == 0 ? p.q + (int64_t)b * p.q_s[0] + (int64_t)hh * p.q_s[1] + (int64_t)nn * p.q_s[2]
+                                  : p.k + (int64_t)b * p.k_s[0] + (int64_t)hh * p.k_s[1] + (int64_t)nn * p.k_s[2];
+    const int dx = min(8 * it.ch, D - 8);
+    in.x0 = *reinterpret_cast<const float4*>(x + dx);
+    in.x1 = *reinterpret_cast<const float4*>(x + dx + 4);
+    if (R > 0) {
+      const int d0 = min(8 * it.ch, R - 8);
+      const int prow = it.side == 0 ? q_off + nn : nn;
+      const float* f = p.freqs + (int64_t)b * p.f_s[0] + (int64_t)hh * p.f_s[1] + (int64_t)prow * p.f_s[2] + d0;
+      // the query side reads bias row 0 (always present) and never uses it
+      const float* bp = p.bias + (int64_t)(it.side == 1 ? hh : 0) * p.bias_sh + d0;
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        ph[o + (int64_t)s * NP] = (uint16_t)((s & 1) ? hi[s >> 1] >> 16 : hi[s >> 1] & 0xffffu);
-        pl[o + (int64_t)s * NP] = (uint16_t)((s & 1) ? lo[s >> 1] >> 16 : lo[s >> 1] & 0xffffu);
+        in.f[s] = f[s];
+        in.bb[s] = bp[s];
       }
+    }
+    return in;
+  };
+  auto emit = [&](const PrepItem& it, const PrepIn& in) {
+    const int NP = it.side == 0 ? sp.NqP : sp.NkP;
+    const int N = it.side == 0 ? p.Nq : p.Nk;
+    uint16_t* ph = it.side == 0 ? sp.qh : sp.kh;
+    uint16_t* pl = it.side == 0 ? sp.ql : sp.kl;
+    auto store = [&](int e0, const float* v) {   // split 8 columns [e0, e0 + 8) of the row
+      u32x4 hi, lo;
+      split8(v, hi, lo);
+      if (!transposed) {
+        const int64_t o = ((int64_t)it.bh * NP + it.n) * p.EP + e0;
+        *reinterpret_cast<u32x4*>(ph + o) = hi;
+        *reinterpret_cast<u32x4*>(pl + o) = lo;
+      } else {
+        const int64_t o = ((int64_t)it.bh * p.EP + e0) * NP + it.n;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          ph[o + (int64_t)s * NP] = (uint16_t)((s & 1) ? hi[s >> 1] >> 16 : hi[s >> 1] & 0xffffu);
+          pl[o + (int64_t)s * NP] = (uint16_t)((s & 1) ? lo[s >> 1] >> 16 : lo[s >> 1] & 0xffffu);
+        }
+      }
+    };
+    const bool live = it.n < N;
+    const float xv[8] = {in.x0.x, in.x0.y, in.x0.z, in.x0.w, in.x1.x, in.x1.y, in.x1.z, in.x1.w};
+    if (8 * it.ch < R) {   // rotated dims d0 .. d0 + 7: cos chunk at column d0, sin chunk at R + d0
+      float vc[8], vs[8];
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const float th = it.side == 1 ? in.f[s] + in.bb[s] : in.f[s];
+        float sn, cs;
+        sincos_rev(th, &sn, &cs);
+        const float a = live ? softplus_f(xv[s]) : 0.f;
+        vc[s] = a * cs;
+        vs[s] = a * sn;
+      }
+      store(8 * it.ch, vc);
+      store(R + 8 * it.ch, vs);
+    } else {               // pass-through dims (columns < E) or zero padding
+      const bool on = live && 8 * it.ch < D;
+      float v[8];
+#pragma unroll
+      for (int s = 0; s < 8; ++s) v[s] = on ? xv[s] : 0.f;
+      store(8 * it.ch + R, v);
     }
   };
-  if (8 * ch < R) {   // rotated dims d0 .. d0 + 7: cos chunk at column d0, sin chunk at R + d0
-    const int d0 = 8 * ch;
-    float vc[8], vs[8];
-    if (n < N) {
-      const int prow = side == 0 ? q_off + nn : nn;
-      float2 cs8[8];
-      const float2* tab = side == 0 ? p.qtab : p.ktab;
-      if (tab) {
-        const float2* t = tab + (int64_t)b * (side == 0 ? p.qt_sb : p.kt_sb) +
-                          (int64_t)hh * (side == 0 ? p.qt_sh : p.kt_sh) + (int64_t)prow * R + d0;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) cs8[s] = t[s];
-      } else {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) cs8[s] = sim_phase(p, side, b, hh, prow, d0 + s);
-      }
-      const float4 x0 = *reinterpret_cast<const float4*>(x + d0);
-      const float4 x1 = *reinterpret_cast<const float4*>(x + d0 + 4);
-      const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const float a = softplus_f(xv[s]);
-        vc[s] = a * cs8[s].x;
-        vs[s] = a * cs8[s].y;
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < 8; ++s) vc[s] = vs[s] = 0.f;
-    }
-    store(d0, vc);
-    store(R + d0, vs);
-  } else {            // pass-through dims (columns < E) or zero padding
-    const int e0 = 8 * ch + R;
-    float v[8];
-    expand_row8(x, nullptr, e0, R, p.E, n < N, v);
-    store(e0, v);
+
+  PrepItem cur = item(i);
+  PrepIn in = load(cur);
+  for (;;) {
+    const int64_t nx = i + T;
+    const PrepItem nxt = item(min(nx, total - 1));
+    const PrepIn nin = load(nxt);   // issued before this item's arithmetic and stores
+    emit(cur, in);
+    if (nx >= total) break;
+    i = nx;
+    cur = nxt;
+    in = nin;
   }
 }
 
@@ -580,14 +600,11 @@ __global__ __launch_bounds__(kThreads, 2) void sim_split_uw_kernel(SimParams p, 
 }  // namespace
 
 hipError_t launch_sim_split_prep(const SimParams& p, const SimSplit& sp, int transposed, hipStream_t s) {
-  int64_t blocks[2];
-  for (int side = 0; side < 2; ++side) {
-    const int heads = side == 0 ? p.B * p.Hq : p.B * p.Hk;
-    const int64_t total = (int64_t)heads * (side == 0 ? sp.NqP : sp.NkP) * prep_items(p.EP, p.R);
-    blocks[side] = (total + kThreads - 1) / kThreads;
-  }
-  return launch_named("sim_split_prep", sim_split_prep_kernel, dim3((unsigned)(blocks[0] + blocks[1])), dim3(kThreads),
-                      s, p, sp, (int)blocks[0], transposed);
+  const int64_t total = ((int64_t)p.B * p.Hq * sp.NqP + (int64_t)p.B * p.Hk * sp.NkP) * prep_items(p.EP, p.R);
+  // kPrepItems items per thread, so that each thread has a next item's loads in flight
+  const int64_t blocks = (total + kThreads * kPrepItems - 1) / (kThreads * kPrepItems);
+  return launch_named("sim_split_prep", sim_split_prep_kernel, dim3((unsigned)blocks), dim3(kThreads), s, p, sp,
+                      transposed);
 }
 
 hipError_t launch_sim_split_fwd(const SimParams& p, const SimSplit& sp, hipStream_t s) {

@@ -163,3 +163,13 @@ def test_reference_named_similarity_function(cuda):
         S = fn(t[0], t[1], t[2], t[3], 32, False)
         S.backward(G.cuda())
         _compare(S, [x.grad for x in t], S_ref, g_ref)
+
+
+def test_similarity_registered_op_checks(cuda):
+    """torch.library.opcheck on pope_amd::sim_fwd: schema, autograd registration and the fake
+    implementation."""
+    from pope_amd.hip_pope import sim_fwd_op
+    q, k, freqs, bias, G = _case(103, 1, 2, 2, 128, 128, 64, 32)
+    args = [x.cuda().requires_grad_(True) for x in (q, k, freqs, bias)]
+    torch.library.opcheck(sim_fwd_op, (*args, True),
+                          test_utils=("test_schema", "test_autograd_registration", "test_faketensor"))
