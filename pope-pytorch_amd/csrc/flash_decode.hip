@@ -338,78 +338,76 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
   }
 }
 
-// One workgroup per (batch, head): merge the splits by log-sum-exp.
+// One workgroup per (batch, head): merge the splits by log-sum-exp.  Thread = (split group g,
+// 4-dim quad q); group g takes every G-th split, eight splits' (m, l, o) loads in flight at a
+// time, and keeps a running (m, l, o) of its splits (one pass over the partials, no wait for a
+// global maximum first); the groups' states then merge through LDS.
 template <typename T>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
-  __shared__ float w_s[1024];
-  __shared__ float red[4];
-  __shared__ float4 red4[256];
-  const int bh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ float4 o_s[256];
+  __shared__ float2 ml_s[256];
+  const int bh = blockIdx.x, tid = threadIdx.x;
   const int b = bh / p.Hq, h = bh % p.Hq;
   const int D = p.D, S = p.splits;
-  const float* pml = p.part_ml + (int64_t)bh * S * 2;
+  const float2* pml = reinterpret_cast<const float2*>(p.part_ml) + (int64_t)bh * S;
   const float* po = p.part_o + (int64_t)bh * S * D;
-  float M = -INFINITY;
-  for (int s = tid; s < S; s += 256) M = fmaxf(M, pml[2 * s]);
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) M = fmaxf(M, __shfl_xor(M, m, 64));
-  if (lane == 0) red[wave] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float Mu = M == -INFINITY ? 0.f : M;
-  __syncthreads();
-  float L = 0.f;
-  for (int s = tid; s < S; s += 256) {
-    const float w = __builtin_amdgcn_exp2f(pml[2 * s] - Mu);
-    if (s < 1024) w_s[s] = w;
-    L += pml[2 * s + 1] * w;
-  }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) L += __shfl_xor(L, m, 64);
-  if (lane == 0) red[wave] = L;
-  __syncthreads();
-  L = red[0] + red[1] + red[2] + red[3];
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  // thread = (split group g, 4-dim quad q): the groups take every G-th split with 8 loads in
-  // flight, then sum through LDS
   const int qd = D / 4, G = 256 / qd;
   const int g = tid / qd, q = tid % qd;
+  float m = -INFINITY, l = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  // folds one split into the running state; a split without a visible key has m = -inf, l = 0,
+  // o = 0 and leaves the state as it is
+  auto fold = [&](float2 ml, float4 v) {
+    const float mn = fmaxf(m, ml.x);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float a = __builtin_amdgcn_exp2f(m - mu), w = __builtin_amdgcn_exp2f(ml.x - mu);
+    acc.x = fmaf(acc.x, a, v.x * w);
+    acc.y = fmaf(acc.y, a, v.y * w);
+    acc.z = fmaf(acc.z, a, v.z * w);
+    acc.w = fmaf(acc.w, a, v.w * w);
+    l = fmaf(l, a, ml.y * w);
+    m = mn;
+  };
   if (g < G) {
     const float4* po4 = reinterpret_cast<const float4*>(po) + q;
-    auto wt = [&](int s) { return s < 1024 ? w_s[s] : __builtin_amdgcn_exp2f(pml[2 * s] - Mu); };
     int s = g;
     for (; s + 7 * G < S; s += 8 * G) {
+      float2 ml[8];
       float4 v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = po4[(int64_t)(s + u * G) * qd];
-#pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const float w = wt(s + u * G);
-        acc.x += v[u].x * w; acc.y += v[u].y * w; acc.z += v[u].z * w; acc.w += v[u].w * w;
+        ml[u] = pml[s + u * G];
+        v[u] = po4[(int64_t)(s + u * G) * qd];
       }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) fold(ml[u], v[u]);
     }
-    for (; s < S; s += G) {
-      const float4 v = po4[(int64_t)s * qd];
-      const float w = wt(s);
-      acc.x += v.x * w; acc.y += v.y * w; acc.z += v.z * w; acc.w += v.w * w;
-    }
+    for (; s < S; s += G) fold(pml[s], po4[(int64_t)s * qd]);
   }
-  red4[tid] = acc;
+  o_s[tid] = acc;
+  ml_s[tid] = make_float2(m, l);
   __syncthreads();
   if (tid < qd) {
-    float4 o = red4[tid];
-    for (int g2 = 1; g2 < G; ++g2) {
-      const float4 v = red4[g2 * qd + tid];
-      o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
+    float M = -INFINITY;
+    for (int g2 = 0; g2 < G; ++g2) M = fmaxf(M, ml_s[g2 * qd + tid].x);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float L = 0.f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int g2 = 0; g2 < G; ++g2) {
+      const float2 st = ml_s[g2 * qd + tid];
+      const float w = __builtin_amdgcn_exp2f(st.x - Mu);
+      const float4 v = o_s[g2 * qd + tid];
+      o.x = fmaf(v.x, w, o.x); o.y = fmaf(v.y, w, o.y); o.z = fmaf(v.z, w, o.z); o.w = fmaf(v.w, w, o.w);
+      L = fmaf(st.y, w, L);
     }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
     uint16_t* orow = p.o + (int64_t)b * p.o_s[0] + (int64_t)h * p.o_s[1] + 4 * tid;
     orow[0] = T::bits(o.x * inv);
     orow[1] = T::bits(o.y * inv);
     orow[2] = T::bits(o.z * inv);
     orow[3] = T::bits(o.w * inv);
+    if (tid == 0) p.lse[bh] = L > 0.f ? (M + __builtin_amdgcn_logf(L)) * kLn2 : -INFINITY;
   }
-  if (tid == 0) p.lse[bh] = L > 0.f ? (M + __builtin_amdgcn_logf(L)) * kLn2 : -INFINITY;
 }
 
 template <typename T, int LPK, int RMAX>
