@@ -147,12 +147,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
     vis_s[j] = (uint8_t)v;
     vis_any |= v;
   }
-  if (!__syncthreads_or(vis_any)) {
-    for (int i = tid; i < HG * (D + 2); i += kThreads) {
-      const int h = h_lo + i / (D + 2), e = i % (D + 2);
-      const int64_t row = ((int64_t)b * p.Hq + h) * p.splits + split;
-      if (e < D) p.part_o[row * D + e] = 0.f;
-      else p.part_ml[row * 2 + (e - D)] = e == D ? -INFINITY : 0.f;
+  if (!__syncthreads_or(vis_any)) {   // (m, l) = (-inf, 0); the combine never reads o of such a split
+    for (int i = tid; i < HG; i += kThreads) {
+      const int64_t row = ((int64_t)b * p.Hq + h_lo + i) * p.splits + split;
+      *reinterpret_cast<float2*>(p.part_ml + row * 2) = make_float2(-INFINITY, 0.f);
     }
     return;
   }
@@ -355,9 +353,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
   const int g = tid / qd, q = tid % qd;
   float m = -INFINITY, l = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  // folds one split into the running state; a split without a visible key has m = -inf, l = 0,
-  // o = 0 and leaves the state as it is
+  // folds one split into the running state; a split without a visible key has m = -inf, l = 0
+  // and an o the split kernel never wrote, and leaves the state as it is
   auto fold = [&](float2 ml, float4 v) {
+    if (ml.x == -INFINITY) v = make_float4(0.f, 0.f, 0.f, 0.f);
     const float mn = fmaxf(m, ml.x);
     const float mu = mn == -INFINITY ? 0.f : mn;
     const float a = __builtin_amdgcn_exp2f(m - mu), w = __builtin_amdgcn_exp2f(ml.x - mu);

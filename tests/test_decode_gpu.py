@@ -187,8 +187,8 @@ def test_decode_head_groups(cuda):
 @pytest.mark.parametrize("lengths", [[0, 3000, 1], [1, 1, 1], [2048, 0, 2048], [5, 2048, 1000]],
                          ids=["dead-long-one", "ones", "dead-middle", "mixed"])
 def test_decode_deal_edge_lengths(cuda, lengths):
-    """The split workgroups' deal of the visible keys: batches with no visible key (o = 0 and
-    lse = -inf from the plan launch), one key, and very unequal lengths side by side."""
+    """Batches with no visible key (o = 0 and lse = -inf), one key, and very unequal lengths side
+    by side."""
     from pope_amd.hip_pope_flash_attn import flash_attn_forward
     B, H, Nk = len(lengths), 4, 3000
     inp = _decode_inputs(73, B, H, H, Nk, 64, 64, torch.bfloat16, lengths=lengths)
@@ -203,3 +203,45 @@ def test_decode_deal_edge_lengths(cuda, lengths):
     for b, L in enumerate(lengths):
         if L == 0:
             assert tr(o)[b].abs().max().item() == 0.0
+
+
+def test_decode_dead_splits_ignore_workspace_contents(cuda):
+    """A split whose keys are all masked writes only (m, l) = (-inf, 0); the combine must not read
+    the partial output rows it leaves unwritten.  The same call on a workspace filled with NaN
+    bytes and on a zeroed one gives the same o and lse bit for bit, and both meet the oracle.
+    The mask leaves dead splits at the start, in the middle and at the end of sequences, and one
+    sequence with no visible key."""
+    import ctypes
+    from pope_amd import _lib
+    from pope_amd.hip_pope_flash_attn import _desc
+    B, H, Nk = 3, 4, 6000
+    inp = _decode_inputs(77, B, H, H, Nk, 64, 64, torch.bfloat16, lengths=[Nk, Nk, 0])
+    mask = inp["mask"].cpu()
+    mask[0, 300:4000] = False      # dead splits between live ones
+    mask[1, :2500] = False         # dead splits before the first visible key
+    mask[1, 2600:] = False         # and after the last
+    inp["mask"] = mask.to("cuda")
+    q, k, v, freqs, bias, m = (inp[n] for n in ("q", "k", "v", "freqs", "bias", "mask"))
+    d = _desc(q, k, freqs, bias, False, q.shape[-1] ** -0.5)
+    outs = []
+    for fill in (0xFF, 0x00):
+        o = torch.empty_like(q)
+        lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
+        d.q_s[:], d.k_s[:], d.v_s[:], d.o_s[:] = (_lib.strides3(t) for t in (q, k, v, o))
+        d.mask_sb = m.stride(0)
+        n = _lib.workspace_bytes(_lib.OP_FLASH_DECODE, d)
+        ws = torch.full((n,), fill, dtype=torch.uint8, device=q.device)
+        st = _lib.lib().pope_flash_decode(ctypes.byref(d), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                          freqs.data_ptr(), bias.data_ptr(), m.data_ptr(), o.data_ptr(),
+                                          lse.data_ptr(), ws.data_ptr(), n, torch.cuda.current_stream().cuda_stream)
+        _lib.check(st, "decode")
+        torch.cuda.synchronize()
+        outs.append((o, lse))
+    (o1, l1), (o0, l0) = outs
+    assert torch.equal(o1, o0) and torch.equal(l1, l0)
+    assert torch.isfinite(o1).all()
+    ref = oracle_attention(inp, False, grads=False)
+    assert max_abs(o1, ref["o"]) <= TOL
+    finite = torch.isfinite(ref["lse"])
+    assert torch.equal(torch.isfinite(l1.cpu()), finite)
+    assert (l1.cpu()[finite] - ref["lse"][finite]).abs().max().item() <= TOL
