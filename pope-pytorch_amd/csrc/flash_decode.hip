@@ -66,18 +66,29 @@ __device__ __forceinline__ float group_sum(float x) {
 // Query weight word of (batch b, head h, dim d), scale * log2 e folded in: rotated dims the fp16
 // pair (a cos(F_q - b), a sin(F_q - b)) with a = softplus(q) and F_q = F[Nk - 1]; pass-through
 // dims the fp32 weight q.
+// Inputs of one query weight word: q, and for a rotated dim F_q and the bias.
+struct QwIn {
+  float qv, f, bb;
+};
 template <typename T>
-__device__ __forceinline__ uint32_t query_weight(const DecodeParams& p, int b, int h, int d) {
-  const float qv = T::to_float(p.q[(int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + d]);
+__device__ __forceinline__ QwIn query_weight_in(const DecodeParams& p, int b, int h, int d) {
+  QwIn in;
+  in.qv = T::to_float(p.q[(int64_t)b * p.q_s[0] + (int64_t)h * p.q_s[1] + d]);
+  in.f = in.bb = 0.f;
+  if (d < p.R) {
+    in.f = p.freqs[(int64_t)b * p.f_s[0] + (int64_t)(p.Nk - 1) * p.f_s[2] + d];
+    in.bb = p.bias[(int64_t)(h % p.Hk) * p.bias_sh + d];
+  }
+  return in;
+}
+__device__ __forceinline__ uint32_t query_weight_of(const DecodeParams& p, int d, QwIn in) {
   if (d < p.R) {
     float sn, cs;
-    sincos_acc(p.freqs[(int64_t)b * p.f_s[0] + (int64_t)(p.Nk - 1) * p.f_s[2] + d] -
-                   p.bias[(int64_t)(h % p.Hk) * p.bias_sh + d],
-               &sn, &cs);
-    const float a = softplus_f(qv) * p.scale_log2;
+    sincos_acc(in.f - in.bb, &sn, &cs);
+    const float a = softplus_f(in.qv) * p.scale_log2;
     return __builtin_bit_cast(uint32_t, f16x2{(_Float16)(a * cs), (_Float16)(a * sn)});
   }
-  return __builtin_bit_cast(uint32_t, qv * p.scale_log2);
+  return __builtin_bit_cast(uint32_t, in.qv * p.scale_log2);
 }
 
 // Split kernel.  A workgroup (4 waves) owns one (batch, split of S keys) for one group of query
@@ -196,6 +207,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
   constexpr int C4 = RMAX / 4;                        // 16-byte chunks per staged row
   constexpr int kTabIt = S * C4 / kThreads;           // chunks per thread
   static_assert(S * C4 % kThreads == 0, "whole table chunks per thread");
+  // the first kQwPre query-weight words of each thread: their inputs are loaded with the table
+  // rows, so their latency is not exposed after the rows' sine / cosine
+  constexpr int kQwPre = 4;
+  QwIn qin[kQwPre];
+#pragma unroll
+  for (int k = 0; k < kQwPre; ++k) {
+    const int i = tid + k * kThreads;
+    if (i < HG * D) qin[k] = query_weight_in<T>(p, b, h_lo + i / D, i % D);
+  }
   float4 tb[kTabIt];
   if (R) {
     const float* fsrc = p.freqs + (int64_t)b * p.f_s[0];
@@ -230,7 +250,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeParams 
     }
   }
   // query weights of the workgroup's heads (after the rows: their registers are free again)
-  for (int i = tid; i < HG * D; i += kThreads) qw_s[i] = query_weight<T>(p, b, h_lo + i / D, i % D);
+#pragma unroll
+  for (int k = 0; k < kQwPre; ++k) {
+    const int i = tid + k * kThreads;
+    if (i < HG * D) qw_s[i] = query_weight_of(p, i % D, qin[k]);
+  }
+  for (int i = tid + kQwPre * kThreads; i < HG * D; i += kThreads)
+    qw_s[i] = query_weight_of(p, i % D, query_weight_in<T>(p, b, h_lo + i / D, i % D));
   if constexpr (T::kCode == 2) {
     for (int i = tid; i < kSpN; i += kThreads) {
       const float t = __builtin_bit_cast(float, (uint32_t)(i + kSpLo) << 16);
