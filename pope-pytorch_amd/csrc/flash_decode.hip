@@ -63,10 +63,8 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
-// Query weight word of (batch b, head h, dim d), scale * log2 e folded in: rotated dims the fp16
-// pair (a cos(F_q - b), a sin(F_q - b)) with a = softplus(q) and F_q = F[Nk - 1]; pass-through
-// dims the fp32 weight q.
-// Inputs of one query weight word: q, and for a rotated dim F_q and the bias.
+// Inputs of the query weight word of (batch b, head h, dim d): q, and for a rotated dim F_q and
+// the bias.
 struct QwIn {
   float qv, f, bb;
 };
@@ -81,6 +79,9 @@ __device__ __forceinline__ QwIn query_weight_in(const DecodeParams& p, int b, in
   }
   return in;
 }
+// The query weight word, scale * log2 e folded in: rotated dims the fp16 pair
+// (a cos(F_q - b), a sin(F_q - b)) with a = softplus(q) and F_q = F[Nk - 1]; pass-through dims
+// the fp32 weight q.
 __device__ __forceinline__ uint32_t query_weight_of(const DecodeParams& p, int d, QwIn in) {
   if (d < p.R) {
     float sn, cs;
