@@ -484,8 +484,10 @@ __device__ __forceinline__ void w_job(const SimParams& p, const SimSplit& sp, fl
       if constexpr (VEC) {
         // 4-wide and branch-free (16-byte aligned rows, Nk a multiple of 8: a key quad lies wholly
         // inside or wholly past the row; one past it reads the last quad and is zeroed), so the wait
-        // before a step's stores covers only that step's loads
-        v = *reinterpret_cast<const float4*>(row + min(jq, Nk - 4));
+        // before a step's stores covers only that step's loads.  Non-temporal (at C2 the U / W launch
+        // and the finalize after it each ran about 1.5 us faster than with these loads cached; the
+        // U jobs' loads of G stay cached, which was slower non-temporal)
+        v = __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(row + min(jq, Nk - 4))));
         if (ii >= Nq || jq >= Nk) v = make_float4(0.f, 0.f, 0.f, 0.f);
       } else if (ii < Nq) {
         v.x = jq < Nk ? row[jq] : 0.f;
