@@ -394,6 +394,11 @@ __global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p,
   // thread = (4-dim quad dq4 of a 64-dim chunk, row group rg of 16); every load and store moves 16 bytes
   const int dq4 = tid & 15, rg = tid >> 4;
   auto ld4 = [](const float* a) { return *reinterpret_cast<const float4*>(a); };
+  // U / W rows are read once and dq / dk written once: non-temporal loads and stores (at C2 the
+  // step ran about 4 us faster: 248.8 -> 244.5 us)
+  auto ldnt = [](const float* a) {
+    return __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a)));
+  };
 
   for (int d0 = 0; d0 < D; d0 += 64) {
     const int d = d0 + 4 * dq4;
@@ -421,9 +426,9 @@ __global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p,
             }
           }
           const float4 xv = ld4(x + (int64_t)n * xs + d);
-          float4 uc = ld4(arow + d), us = ld4(arow + R + d);
+          float4 uc = ldnt(arow + d), us = ldnt(arow + R + d);
           if (arow2) {
-            const float4 uc2 = ld4(arow2 + d), us2 = ld4(arow2 + R + d);
+            const float4 uc2 = ldnt(arow2 + d), us2 = ldnt(arow2 + R + d);
             uc.x += uc2.x; uc.y += uc2.y; uc.z += uc2.z; uc.w += uc2.w;
             us.x += us2.x; us.y += us2.y; us.z += us2.z; us.w += us2.w;
           }
@@ -435,7 +440,7 @@ __global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p,
             g[t] = sigmoid_f(xa[t]) * (cs[t] * ca[t] + sn[t] * sa[t]);
             dph[t] = softplus_f(xa[t]) * (cs[t] * sa[t] - sn[t] * ca[t]);
           }
-          *reinterpret_cast<float4*>(orow) = make_float4(g[0], g[1], g[2], g[3]);
+          __builtin_nontemporal_store(f32x4{g[0], g[1], g[2], g[3]}, reinterpret_cast<f32x4*>(orow));
           if (part) {
             *reinterpret_cast<float4*>(part + ((int64_t)bh * rows + n) * R + d) = make_float4(dph[0], dph[1], dph[2], dph[3]);
           } else if (p.dfreqs) {
@@ -445,12 +450,12 @@ __global__ __launch_bounds__(kThreads) void sim_bwd_finalize_kernel(SimParams p,
           }
           dps.x += dph[0]; dps.y += dph[1]; dps.z += dph[2]; dps.w += dph[3];
         } else {
-          float4 v = ld4(arow + R + d);
+          float4 v = ldnt(arow + R + d);
           if (arow2) {
-            const float4 v2 = ld4(arow2 + R + d);
+            const float4 v2 = ldnt(arow2 + R + d);
             v.x += v2.x; v.y += v2.y; v.z += v2.z; v.w += v2.w;
           }
-          *reinterpret_cast<float4*>(orow) = v;
+          __builtin_nontemporal_store(f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4*>(orow));
         }
       }
     }
