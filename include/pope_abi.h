@@ -130,7 +130,8 @@ int pope_sim_fwd(const pope_desc* desc, const void* q, const void* k, const floa
 /*
  * Fused PoPE similarity backward.  dsim has the sim layout (sim_s).  dq, dk are
  * written (not accumulated).  dfreqs (fp32, df_s strides) and dbias (fp32, Hb
- * rows, bias_sh) are ACCUMULATED into and may be NULL; the caller zeroes them.
+ * rows, bias_sh) are ACCUMULATED into and may be NULL (caller zeroes), or
+ * overwritten with POPE_FLAG_ZERO_GRADS: dfreqs rows n < Nk, every dbias row.
  * Replaces PoPESimilarityFunction.backward (triton_pope.py:291-362; kernels
  * _bwd_kernel_dqk_df :85-194 and _bwd_kernel_dbias_optimized :196-256).
  */

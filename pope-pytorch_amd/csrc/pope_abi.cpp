@@ -365,11 +365,13 @@ int check_flash_common(const pope_desc* d, const void* q, const void* k, const v
 }
 
 
-int check_sim_common(const pope_desc* d, const void* q, const void* k, const float* freqs, const float* bias) {
+// op_flags: the flags one entry point accepts beyond SPLIT_BF16 and DETERMINISTIC.
+int check_sim_common(const pope_desc* d, const void* q, const void* k, const float* freqs, const float* bias,
+                     unsigned op_flags) {
   int rc = check_desc(d);
   if (rc) return rc;
   if (d->dtype != POPE_F32) return fail(POPE_ERR_UNSUPPORTED, "similarity kernels take fp32 (dtype %d)", d->dtype);
-  if (d->flags & ~(POPE_FLAG_SPLIT_BF16 | POPE_FLAG_DETERMINISTIC))
+  if (d->flags & ~(POPE_FLAG_SPLIT_BF16 | POPE_FLAG_DETERMINISTIC | op_flags))
     return fail(POPE_ERR_INVALID, "unknown flags 0x%x", (unsigned)d->flags);
   if (d->D > 512) return fail(POPE_ERR_UNSUPPORTED, "similarity covers head dim <= 512 (got %d)", d->D);
   if (!q || !k) return fail(POPE_ERR_INVALID, "q, k must be non-NULL");
@@ -660,7 +662,7 @@ int pope_flash_decode_noalloc(const pope_desc* d, const void* q, const void* k, 
 
 int pope_sim_fwd(const pope_desc* d, const void* q, const void* k, const float* freqs, const float* bias,
                  void* sim, void* workspace, size_t workspace_bytes, void* stream) {
-  int rc = check_sim_common(d, q, k, freqs, bias);
+  int rc = check_sim_common(d, q, k, freqs, bias, 0);
   if (rc) return rc;
   if (!sim) return fail(POPE_ERR_INVALID, "sim must be non-NULL");
   if (d->sim_s[0] < 0 || d->sim_s[1] < 0 || d->sim_s[2] < 0) return fail(POPE_ERR_INVALID, "negative sim stride");
@@ -681,7 +683,7 @@ int pope_sim_fwd(const pope_desc* d, const void* q, const void* k, const float* 
 int pope_sim_bwd(const pope_desc* d, const void* dsim, const void* q, const void* k, const float* freqs,
                  const float* bias, void* dq, void* dk, float* dfreqs, float* dbias, void* workspace,
                  size_t workspace_bytes, void* stream) {
-  int rc = check_sim_common(d, q, k, freqs, bias);
+  int rc = check_sim_common(d, q, k, freqs, bias, POPE_FLAG_ZERO_GRADS);
   if (rc) return rc;
   if (!dsim || !dq || !dk) return fail(POPE_ERR_INVALID, "dsim, dq, dk must be non-NULL");
   if (!aligned16(dq) || !aligned16(dk)) return fail(POPE_ERR_INVALID, "dq, dk must be 16-byte aligned");
@@ -714,12 +716,18 @@ int pope_sim_bwd(const pope_desc* d, const void* dsim, const void* q, const void
   const DetParts dp = det_parts(*d, ws + sim_ws(*d, POPE_OP_SIM_BWD) - det_bytes(*d), dfreqs, dbias);
   p.kpart = dp.kpart;
   p.qpart = dp.qpart;
+  const bool zero = (d->flags & POPE_FLAG_ZERO_GRADS) != 0;
+  // deterministic mode: the phase-gradient reduction overwrites dfreqs / dbias instead
+  p.zero_grads = zero && !dp.kpart && (dfreqs || dbias);
+  p.Bt = d->f_s[0] != 0 ? d->B : 1;
+  p.Ht = d->f_s[1] != 0 ? d->Hq : 1;   // per-head tables need Hq == Hk
+  p.Hb = d->bias_sh != 0 ? d->Hk : 1;
   if (d->flags & POPE_FLAG_SPLIT_BF16)
     e = pope::launch_sim_split_bwd(p, sim_split_planes(*d, ws, POPE_OP_SIM_BWD), U, W, s);
   else
     e = pope::launch_sim_bwd_ws(p, U, W, s);
   if (e != hipSuccess) return hip_fail(e, "similarity backward launch");
-  e = det_reduce(*d, dp, dfreqs, dbias, false, s);
+  e = det_reduce(*d, dp, dfreqs, dbias, zero, s);
   if (e != hipSuccess) return hip_fail(e, "phase gradient reduction launch");
   return POPE_OK;
 }

@@ -122,6 +122,8 @@ struct SimParams {
   int B, Hq, Hk, Nq, Nk, D, R, E, EP;
   int g_vec;                 // dsim rows are 16-byte aligned: 4-wide loads allowed
   float* kpart; float* qpart;   // deterministic mode: per-row phase derivatives (PhaseGradParams), else null
+  int zero_grads;            // backward: the first launch clears dfreqs (Bt, Ht, n < Nk) and dbias (Hb)
+  int Bt, Ht, Hb;            // extents of dfreqs / dbias (1 where freqs / bias broadcast)
   int64_t q_s[3], k_s[3], sim_s[3], dq_s[3], dk_s[3], f_s[3], df_s[3];
   int64_t bias_sh, kt_sb, kt_sh, qt_sb, qt_sh;
 };

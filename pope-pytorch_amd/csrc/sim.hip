@@ -152,6 +152,8 @@ constexpr int kKtRow = 128 + 1;   // fp32 row stride of the K_hat tile (keys x 1
 
 __global__ __launch_bounds__(kThreads, 2) void sim_bwd_u_kernel(SimParams p, float* U, int nib, int nec) {
   __shared__ float kt[kBJ * kKtRow];
+  if (p.zero_grads)   // the backward's first launch
+    sim_clear_grads(p, (int64_t)blockIdx.x * kThreads + threadIdx.x, (int64_t)gridDim.x * kThreads);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int ec = id % nec, ib = (id / nec) % nib, bh = id / (nec * nib);

@@ -20,4 +20,30 @@ __device__ __forceinline__ float2 sim_phase(const SimParams& p, int side, int b,
   return make_float2(c, s);
 }
 
+// Clears the phase gradients the finalize accumulates into, over what the backward addresses:
+// dfreqs rows n < Nk of every (bt, ht) and the Hb rows of dbias.  Called by every thread of the
+// backward's first launch with its flat index and the launch's thread count.
+__device__ __forceinline__ void sim_clear_grads(const SimParams& p, int64_t gid, int64_t nthreads) {
+  const int R = p.R;
+  if (p.dbias)
+    for (int64_t x = gid; x < (int64_t)p.Hb * R; x += nthreads) p.dbias[(x / R) * p.bias_sh + x % R] = 0.f;
+  if (!p.dfreqs) return;
+  const int64_t n = (int64_t)p.Bt * p.Ht * p.Nk * R;
+  // dense (bt, ht, n, d) layout (the usual one): one flat range
+  const bool dense = p.df_s[2] == R && (p.Ht == 1 || p.df_s[1] == (int64_t)p.Nk * R) &&
+                     (p.Bt == 1 || p.df_s[0] == (int64_t)p.Ht * p.Nk * R);
+  for (int64_t x = gid; x < n; x += nthreads) {
+    if (dense) {
+      p.dfreqs[x] = 0.f;
+    } else {
+      const int d = (int)(x % R);
+      int64_t rest = x / R;
+      const int row = (int)(rest % p.Nk);
+      rest /= p.Nk;
+      const int ht = (int)(rest % p.Ht), bt = (int)(rest / p.Ht);
+      p.dfreqs[(int64_t)bt * p.df_s[0] + (int64_t)ht * p.df_s[1] + (int64_t)row * p.df_s[2] + d] = 0.f;
+    }
+  }
+}
+
 }  // namespace pope

@@ -23,6 +23,7 @@
 
 #include "pope_common.hpp"
 #include "pope_kernels.hpp"
+#include "sim_phase.hpp"
 
 namespace pope {
 
@@ -81,6 +82,7 @@ __global__ __launch_bounds__(kThreads) void sim_split_prep_kernel(SimParams p, S
   const int64_t total = total0 + (int64_t)p.B * p.Hk * sp.NkP * nch;
   const int64_t T = (int64_t)gridDim.x * kThreads;
   int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (p.zero_grads) sim_clear_grads(p, i, T);   // the backward's first launch
   if (i >= total) return;
   const int q_off = p.Nk - p.Nq;
 

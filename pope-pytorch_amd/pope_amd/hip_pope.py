@@ -91,11 +91,15 @@ def sim_bwd_op(dsim: Tensor, q: Tensor, k: Tensor, freqs: Tensor, bias: Tensor, 
     q, k, dsim = _aligned(q), _aligned(k), _aligned(dsim.float())
     d = _desc(q, k, freqs, bias, split)
     d.flags |= _lib.deterministic_flag()   # torch.use_deterministic_algorithms(True): no fp32 atomics
+    # the library clears dfreqs / dbias before accumulating into them, over the positions n < Nk
+    # it addresses; rows of a longer freqs table get no gradient, so that gradient starts from zeros
+    d.flags |= _lib.FLAG_ZERO_GRADS
     d.sim_s[:] = _lib.strides3(dsim)
     dq, dk = torch.empty_like(q), torch.empty_like(k)
     d.dq_s[:], d.dk_s[:] = _lib.strides3(dq), _lib.strides3(dk)
-    dfreqs = torch.zeros(freqs.shape, device=q.device, dtype=torch.float32) if need_dfreqs else q.new_empty(0, dtype=torch.float32)
-    dbias = torch.zeros(bias.shape, device=q.device, dtype=torch.float32) if need_dbias else q.new_empty(0, dtype=torch.float32)
+    alloc_df = torch.zeros if freqs.shape[-2] > k.shape[2] else torch.empty
+    dfreqs = alloc_df(freqs.shape, device=q.device, dtype=torch.float32) if need_dfreqs else q.new_empty(0, dtype=torch.float32)
+    dbias = torch.empty(bias.shape, device=q.device, dtype=torch.float32) if need_dbias else q.new_empty(0, dtype=torch.float32)
     if need_dfreqs:
         d.df_s[:] = _freqs_strides(dfreqs)
     ws = _lib.workspace(_lib.OP_SIM_BWD, d, q.device)

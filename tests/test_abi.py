@@ -155,6 +155,15 @@ def test_sim_and_decode_validation():
     d.bias_sh = -1
     st = L.pope_sim_bwd(ctypes.byref(d), _A, _A, _A, _A, _A, _A, _A, None, None, _A, 1 << 16, None)
     assert st == 1 and "negative" in _lib.last_error()
+    # ZERO_GRADS is a backward flag: the similarity backward takes it (the check moves on to the
+    # bias stride), the forward refuses it
+    d.flags = _lib.FLAG_ZERO_GRADS
+    st = L.pope_sim_bwd(ctypes.byref(d), _A, _A, _A, _A, _A, _A, _A, None, None, _A, 1 << 16, None)
+    assert st == 1 and "negative" in _lib.last_error()
+    d = _desc(dtype=_lib.POPE_F32, D=64, R=64)
+    d.flags = _lib.FLAG_ZERO_GRADS
+    st = L.pope_sim_fwd(ctypes.byref(d), _A, _A, _A, _A, _A, _A, 1 << 16, None)
+    assert st == 1 and "flags" in _lib.last_error()
 
 
 def test_last_error_is_per_thread():

@@ -173,3 +173,55 @@ def test_similarity_registered_op_checks(cuda):
     args = [x.cuda().requires_grad_(True) for x in (q, k, freqs, bias)]
     torch.library.opcheck(sim_fwd_op, (*args, True),
                           test_utils=("test_schema", "test_autograd_registration", "test_faketensor"))
+
+
+@pytest.mark.parametrize("deterministic", [True, False], ids=["deterministic", "atomics"])
+@pytest.mark.parametrize("extra_rows", [0, 5], ids=["dense", "longer_table"])
+@pytest.mark.parametrize("split", [True, False], ids=["split_bf16", "fp32"])
+def test_similarity_zero_grads_flag(cuda, split, extra_rows, deterministic):
+    """POPE_FLAG_ZERO_GRADS through the C-ABI: the backward overwrites dfreqs rows n < Nk and
+    every dbias row whatever they held (NaN here), leaves the rows n >= Nk of a longer freqs
+    table untouched, and gives the gradients of a call that accumulates into zeros: bitwise in
+    deterministic mode, within fp32 atomic-order rounding otherwise.  A per-batch table with
+    extra rows takes the kernels' strided clearing, one without them the flat one."""
+    import ctypes
+    from pope_amd import _lib
+    from pope_amd.hip_pope import _desc
+    from pope_amd.hip_pope_flash_attn import _freqs_strides
+    B, Hq, Hk, Nq, Nk, D, R = 2, 4, 2, 40, 72, 64, 32
+    g = torch.Generator().manual_seed(211)
+    q = torch.randn(B, Hq, Nq, D, generator=g).cuda()
+    k = torch.randn(B, Hk, Nk, D, generator=g).cuda()
+    freqs = torch.randn(B, Nk + extra_rows, R, generator=g).cuda()
+    bias = torch.randn(Hk, R, generator=g).cuda()
+    dsim = torch.randn(B, Hq, Nq, Nk, generator=g).cuda()
+    L = _lib.lib()
+
+    def run(zero, fill):
+        d = _desc(q, k, freqs, bias, split)
+        d.flags |= (_lib.FLAG_ZERO_GRADS if zero else 0) | (_lib.FLAG_DETERMINISTIC if deterministic else 0)
+        d.sim_s[:] = _lib.strides3(dsim)
+        dq, dk = torch.empty_like(q), torch.empty_like(k)
+        d.dq_s[:], d.dk_s[:] = _lib.strides3(dq), _lib.strides3(dk)
+        dfreqs, dbias = torch.full_like(freqs, fill), torch.full_like(bias, fill)
+        d.df_s[:] = _freqs_strides(dfreqs)
+        ws = _lib.workspace(_lib.OP_SIM_BWD, d, q.device)
+        st = L.pope_sim_bwd(ctypes.byref(d), _lib.ptr(dsim), _lib.ptr(q), _lib.ptr(k), _lib.ptr(freqs),
+                            _lib.ptr(bias), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dfreqs), _lib.ptr(dbias),
+                            _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_ptr(q.device))
+        _lib.check(st, "similarity backward")
+        torch.cuda.synchronize()
+        return dq, dk, dfreqs, dbias
+
+    got = run(True, float("nan"))
+    want = run(False, 0.0)
+    if extra_rows:
+        assert torch.isnan(got[2][:, Nk:]).all(), "rows past Nk must keep their contents"
+        got = (*got[:2], got[2][:, :Nk], got[3])
+        want = (*want[:2], want[2][:, :Nk], want[3])
+    for name, a, b in zip(("dq", "dk", "dfreqs", "dbias"), got, want):
+        assert torch.isfinite(a).all(), name
+        if deterministic:
+            assert torch.equal(a, b), name
+        else:
+            assert _rel_inf(a, b) <= 1e-5, (name, _rel_inf(a, b))
