@@ -11,15 +11,18 @@
 // registers), 32 rows per wave, the backward's accumulators split into as few column chunks as the
 // registers allow (each chunk recomputes the scores; the other waves take neighbouring row blocks),
 // tiles shared by the four waves through LDS, and the polar transform's chain rule in a separate
-// pass.  Memory stays linear in the
-// sequence length: no score matrix is stored.  Same workspace preparation as the narrow path
+// pass.  The streamed tiles go straight from global memory into LDS (global_load_lds_dwordx4) in
+// three slots, two steps ahead of the step computed: a step's products take less time than the
+// tile's fetch, and tiles staged through registers would hold registers these kernels do not
+// have.  Memory stays linear in the sequence length: no score matrix is stored.  Same workspace preparation as the narrow path
 // (flash_prep.hip: K_hat, Q_hat pre-scaled by softmax_scale * log2 e, key visibility words,
 // phase tables), with EP = E rounded up to 128 and DV = 256.
 //   wide_fwd   one workgroup per (128 queries, batch * head): S^T = K_hat Q_hat^T, online softmax
 //              in log2 units, O^T += V^T P^T with V read transposed (ds_read_b64_tr_b16); the
-//              K_hat and V tiles of 32 keys double-buffered in LDS.
+//              K_hat and V tiles of 32 keys streamed through LDS.
 //   wide_kv    one workgroup per (key blocks, batch * kv head), wave = (32 keys, column chunk): S = Q_hat K_hat^T
-//              - lse, dP = dO V^T - delta (Q_hat and dO tiles double-buffered in LDS), P = exp2 S,
+//              - lse, dP = dO V^T - delta (Q_hat and dO tiles and the row terms streamed through
+//              LDS), P = exp2 S,
 //              dS = P dP; dV (the wave's chunk of D columns) += P^T dO and dK_hat (its chunk of E
 //              columns) += dS^T Q_hat; writes dV and the raw dK_hat chunk (fp32 workspace).
 //   wide_q     one workgroup per (query blocks, batch * head), wave = (32 queries, column chunk): S^T, dP^T with
@@ -60,20 +63,63 @@ __device__ __forceinline__ f32x16 splat16(float x) {
 // Row offset within a 32-row block of register r of a 32x32 MFMA result in lane half hf.
 __device__ __forceinline__ int res_row(int r, int hf) { return 8 * (r >> 2) + 4 * hf + (r & 3); }
 
+// LDS slots of the streamed tiles: tile t is computed from slot t % kSlots while tiles t + 1 and
+// t + 2 load, so each tile has two steps of compute to arrive in.
+constexpr int kSlots = 3;
+
+// Waits until at most N of this thread's vector memory loads are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Transpose-read offsets (lo, hi) of column block nb of a tile, nb known only at run time: the
+// entry of the swizzle period is picked by selects rather than by indexing the offset arrays,
+// which would place them in scratch memory (vector loads that would wait on the tile loads).
+template <int U>
+__device__ __forceinline__ int2 tr_offsets(const TileOffsets<U>& o, int nb) {
+  constexpr int TP = TileOffsets<U>::TP;
+  const int k = nb % TP;
+  int lo = o.lo[0], hi = o.hi[0];
+#pragma unroll
+  for (int i = 1; i < TP; ++i) {
+    lo = k == i ? o.lo[i] : lo;
+    hi = k == i ? o.hi[i] : hi;
+  }
+  return make_int2(lo + 32 * (nb - k), hi + 32 * (nb - k));
+}
+
+// Direct global -> LDS fill of one tile of 32 rows x U 16-byte units, stored unpadded with
+// tile_swz (unit u of row r at position u ^ tile_swz(U, r)).  Load i of the thread fills
+// position c = 256 i + tid (a wave's 64 lanes write 64 consecutive positions), in row c / U,
+// with unit (c % U) ^ tile_swz(U, c / U) of that row; src(r, u) is its global address.
+template <int U, typename Src>
+__device__ __forceinline__ void tile_fill(const uint16_t* tile, int tid, int wave, Src src) {
+  static_assert(32 * U % 256 == 0, "whole loads per thread");
+  const uint32_t base = lds_addr(tile) + 1024 * wave;
+#pragma unroll
+  for (int i = 0; i < 32 * U / 256; ++i) {
+    const int c = tid + 256 * i, r = c / U;
+    load_lds16(src(r, (c % U) ^ tile_swz(U, r)), base + 4096 * i);
+  }
+}
+
 // ---- forward ---------------------------------------------------------------------------
 // Four waves per workgroup, 128 query rows (wave w: rows q0 + 32 w ..); per 32-key tile the K_hat
-// rows and the V rows go through LDS once for the four waves (unpadded, XOR-swizzled), double
-// buffered: the next tile's loads are in flight in registers while the current tile is computed.
+// rows and the V rows go straight from global memory into LDS once for the four waves (unpadded,
+// XOR-swizzled), in three slots: the loads of the next two tiles are in flight while the current
+// tile is computed.
 template <typename T, int EP, int DV>
 __global__ __launch_bounds__(256) void wide_fwd_kernel(FlashFwdParams p) {
   constexpr int KS = EP / 16, NDB = DV / 32;
   constexpr int KU = EP / 8, VU = DV / 8;              // 16-byte units per K_hat / V row
-  constexpr int KN = 32 * KU / 256, VN = 32 * VU / 256;  // units per thread and tile
+  constexpr int NL = 32 * (KU + VU) / 256;             // loads per thread and tile
   typedef typename T::vec8 vec8;
-  __shared__ __attribute__((aligned(16))) uint16_t kt[2][32 * EP];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[2][32 * DV];
+  __shared__ __attribute__((aligned(16))) uint16_t kt[kSlots][32 * EP];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[kSlots][32 * DV];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
+  const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int BH = p.B * p.Hq, nqb = p.NqP / 128;
   const int bh = blockIdx.x % BH;
   const int q0 = 128 * (nqb - 1 - (int)(blockIdx.x / BH));   // heaviest causal blocks first
@@ -81,12 +127,6 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(FlashFwdParams p) {
   const int b = bh / p.Hq, h = bh % p.Hq, hk = h % p.Hk;
   const int Nk = p.Nk, D = p.D, qi = q0 + 32 * wave + lr;
 
-  vec8 qreg[KS];
-  {
-    const uint16_t* qrow = p.qh + ((int64_t)bh * p.NqP + qi) * EP + 8 * hf;
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) qreg[kk] = as_vec8<vec8>(ld16(qrow + 16 * kk));
-  }
   int nkeys = min(((ci32*)p.kend)[b], Nk);
   if (p.causal) nkeys = min(nkeys, q0 + 128);
   const uint16_t* khb = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;   // rows padded to NkP
@@ -95,48 +135,42 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(FlashFwdParams p) {
   const TileOffsets<KU> ko(lane);
   const TileOffsets<VU> vo(lane);
 
-  // tile staging: unit c = tid + 256 i of the tile's rows (row c / U, unit c % U); V rows past Nk
-  // repeat the last one, V columns at or past D are zero
-  u32x4 kst[KN], vst[VN];
-  auto load_tile = [&](int j0) {
-#pragma unroll
-    for (int i = 0; i < KN; ++i) {
-      const int c = tid + 256 * i;
-      kst[i] = ld16(khb + (int64_t)(j0 + c / KU) * EP + 8 * (c % KU));
-    }
-#pragma unroll
-    for (int i = 0; i < VN; ++i) {
-      const int c = tid + 256 * i, d0 = 8 * (c % VU);
-      vst[i] = d0 < D ? ld16(vb + (int64_t)min(j0 + c / VU, Nk - 1) * p.v_s[2] + d0) : u32x4{0u, 0u, 0u, 0u};
-    }
+  // tile t into slot t % kSlots: K_hat rows are padded to NkP (no clamp); V rows past Nk repeat
+  // the last one and V units at or past D repeat the row's last unit (they only reach the O rows
+  // at or past D, which are not stored)
+  auto issue = [&](int t) {
+    const int j0 = 32 * t, slot = t % kSlots;
+    const uint16_t* kp = khb + (int64_t)j0 * EP;
+    tile_fill<KU>(kt[slot], tid, wave, [&](int r, int u) { return kp + r * EP + 8 * u; });
+    tile_fill<VU>(vt[slot], tid, wave, [&](int r, int u) {
+      return vb + (int64_t)min(j0 + r, Nk - 1) * p.v_s[2] + min(8 * u, D - 8);
+    });
   };
-  auto store_tile = [&](int buf) {
+  const int nt = (nkeys + 31) / 32;
+  if (nt > 0) issue(0);
+  if (nt > 1) issue(1);
+
+  vec8 qreg[KS];
+  {
+    const uint16_t* qrow = p.qh + ((int64_t)bh * p.NqP + qi) * EP + 8 * hf;
 #pragma unroll
-    for (int i = 0; i < KN; ++i) {
-      const int c = tid + 256 * i, r = c / KU, u = c % KU;
-      *reinterpret_cast<u32x4*>(kt[buf] + r * EP + 8 * (u ^ tile_swz(KU, r))) = kst[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VN; ++i) {
-      const int c = tid + 256 * i, r = c / VU, u = c % VU;
-      *reinterpret_cast<u32x4*>(vt[buf] + r * DV + 8 * (u ^ tile_swz(VU, r))) = vst[i];
-    }
-  };
+    for (int kk = 0; kk < KS; ++kk) qreg[kk] = as_vec8<vec8>(ld16(qrow + 16 * kk));
+  }
+  // the Q_hat rows as loads the compiler sees complete: no use of them in the loop waits on the
+  // tile loads in flight there
+  settle_vector_loads();
 
   f32x16 oacc[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) oacc[db] = splat16(0.f);
   float m = -INFINITY, l = 0.f;
   const uint32_t ones = T::pack2(1.f, 1.f);
-  const int nt = (nkeys + 31) / 32;
-  if (nt > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
   for (int t = 0; t < nt; ++t) {
-    const int buf = t & 1, j0 = 32 * t;
-    if (t + 1 < nt) load_tile(j0 + 32);
+    const int buf = t % kSlots, j0 = 32 * t;
+    if (t + 1 < nt) wait_vmcnt<NL>();   // this thread's loads of tile t landed (t + 1 may be in flight)
+    else wait_vmcnt<0>();
+    __syncthreads();                    // ... everyone's; and slot (t + 2) % kSlots was last read in step t - 1
+    if (t + 2 < nt) issue(t + 2);
     // S^T (rows = keys, lane = query), log2 units
     f32x16 s = splat16(0.f);
 #pragma unroll
@@ -177,8 +211,6 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(FlashFwdParams p) {
         oacc[db] = T::mfma32(as_vec8<vec8>(lds_tr8(vt[buf], vo.lo_at(db) + 16 * g * DV, vo.hi_at(db) + 16 * g * DV)),
                              as_vec8<vec8>(pw[g]), oacc[db]);
     }
-    if (t + 1 < nt) store_tile(buf ^ 1);   // the other buffer's last reads were before the last barrier
-    __syncthreads();
   }
   if (qi >= p.Nq) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
@@ -202,17 +234,19 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(FlashFwdParams p) {
 // ---- backward: dK_hat / dV --------------------------------------------------------------
 // One workgroup per (4 / CH blocks of 32 keys, batch * kv head); wave w takes key block w / CH and
 // column chunk w % CH of the accumulators (CH chunks recompute the scores CH times; fewer where the
-// registers allow).  The Q_hat and dO tiles of each 32-query step go through LDS once for the four
-// waves, double buffered (the next step's loads in flight in registers during the current step).
+// registers allow).  The Q_hat and dO tiles of each 32-query step go straight from global memory
+// into LDS once for the four waves, in three slots (two steps ahead of the step computed), with
+// the step's -lse and -delta rows (one more load, wave 0).
 template <typename T, int EP, int DV, int CH>
 __global__ __launch_bounds__(256) void wide_kv_kernel(FlashBwdParams p, float* wk) {
   constexpr int KS = EP / 16, DS = DV / 16, EBC = EP / 32 / CH, DBC = DV / 32 / CH, RB = 4 / CH;
-  constexpr int QU = EP / 8, OU = DV / 8, QN = 32 * QU / 256, ON = 32 * OU / 256;
+  constexpr int QU = EP / 8, OU = DV / 8, NL = 32 * (QU + OU) / 256;
   typedef typename T::vec8 vec8;
-  __shared__ __attribute__((aligned(16))) uint16_t qt[2][32 * EP];
-  __shared__ __attribute__((aligned(16))) uint16_t dt[2][32 * DV];
+  __shared__ __attribute__((aligned(16))) uint16_t qt[kSlots][32 * EP];
+  __shared__ __attribute__((aligned(16))) uint16_t dt[kSlots][32 * DV];
+  __shared__ __attribute__((aligned(16))) float rt[kSlots][256];   // [0, 32) -lse, [32, 64) -delta
 
-  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
+  const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int nkb = p.NkP / (32 * RB);
   const int ec = (tid >> 6) % CH;   // the wave's column chunk
   const int kb0 = 32 * RB * ((int)blockIdx.x % nkb), bhk = (int)blockIdx.x / nkb;   // key block 0 (the heaviest causal one) first
@@ -223,6 +257,39 @@ __global__ __launch_bounds__(256) void wide_kv_kernel(FlashBwdParams p, float* w
   const int kj = k0 + lr;
   cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
   const bool kvis = kj < Nk && ((mw[kj >> 6] >> (kj & 63)) & 1ull);
+
+  // the steps: (query head g of the kv head's group, 32-query block q0), flattened
+  const int groups = p.Hq / p.Hk;
+  const int qstart = p.causal ? kb0 : 0;   // the workgroup's first key block
+  const int nsq = Nq > qstart ? (Nq - qstart + 31) / 32 : 0;
+  const int nsteps = __syncthreads_or(kvis) ? groups * nsq : 0;   // uniform over the workgroup
+  auto step_at = [&](int st, int& h, int& q0) {
+    h = (st / nsq) * p.Hk + hk;
+    q0 = qstart + 32 * (st % nsq);
+  };
+  // step st's tiles into slot st % kSlots: Q_hat rows padded to NqP (no clamp); dO rows past Nq
+  // repeat the last one and dO units at or past D repeat the row's last unit (they meet zero V
+  // columns in dP and reach only the dV columns at or past D, which are not stored)
+  auto issue = [&](int st) {
+    int h, q0;
+    step_at(st, h, q0);
+    const int slot = st % kSlots;
+    const uint16_t* qhb = p.qh + ((int64_t)(b * p.Hq + h) * NqP + q0) * EP;
+    const uint16_t* dob = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1];
+    tile_fill<QU>(qt[slot], tid, wave, [&](int r, int u) { return qhb + r * EP + 8 * u; });
+    tile_fill<OU>(dt[slot], tid, wave, [&](int r, int u) {
+      return dob + (int64_t)min(q0 + r, Nq - 1) * p.do_s[2] + min(8 * u, D - 8);
+    });
+    // the row terms of queries q0 .. q0 + 31: lane units 0-7 -lse, 8-15 -delta (lanes past 15
+    // repeat them past float 64, unread)
+    if (wave == 0) {
+      const int u = lane & 15;
+      const float* src = (u < 8 ? p.nl : p.nd) + (int64_t)(b * p.Hq + h) * NqP + q0 + 4 * (u & 7);
+      load_lds16(src, lds_addr(rt[slot]));
+    }
+  };
+  if (nsteps > 0) issue(0);
+  if (nsteps > 1) issue(1);
 
   vec8 kreg[KS], vreg[DS];
   {
@@ -236,71 +303,43 @@ __global__ __launch_bounds__(256) void wide_kv_kernel(FlashBwdParams p, float* w
       vreg[kk] = as_vec8<vec8>((kj < Nk && d0 < D) ? ld16(vr + d0) : zero4());
     }
   }
+  // the K_hat / V rows as loads the compiler sees complete: no use of them in the loop waits on
+  // the tile loads in flight there
+  settle_vector_loads();
   f32x16 dka[EBC], dva[DBC];
 #pragma unroll
   for (int x = 0; x < EBC; ++x) dka[x] = splat16(0.f);
 #pragma unroll
   for (int x = 0; x < DBC; ++x) dva[x] = splat16(0.f);
+  // the tiles' row-read offsets, and the wave's transpose-read offsets: its dV column blocks of
+  // the dO tile, its dK_hat column blocks of the Q_hat tile
   const TileOffsets<QU> qo(lane);
   const TileOffsets<OU> dO(lane);
+  int2 dof[DBC], qof[EBC];
+#pragma unroll
+  for (int db = 0; db < DBC; ++db) dof[db] = tr_offsets(dO, ec * DBC + db);
+#pragma unroll
+  for (int eb = 0; eb < EBC; ++eb) qof[eb] = tr_offsets(qo, ec * EBC + eb);
 
-  // the steps: (query head g of the kv head's group, 32-query block q0), flattened
-  const int groups = p.Hq / p.Hk;
-  const int qstart = p.causal ? kb0 : 0;   // the workgroup's first key block
-  const int nsq = Nq > qstart ? (Nq - qstart + 31) / 32 : 0;
-  const int nsteps = __syncthreads_or(kvis) ? groups * nsq : 0;   // uniform over the workgroup
-  u32x4 qst[QN], ost[ON];
-  auto step_at = [&](int st, int& h, int& q0) {
-    h = (st / nsq) * p.Hk + hk;
-    q0 = qstart + 32 * (st % nsq);
-  };
-  auto load_tile = [&](int st) {
-    int h, q0;
-    step_at(st, h, q0);
-    const uint16_t* qhb = p.qh + (int64_t)(b * p.Hq + h) * NqP * EP;   // rows padded to NqP
-    const uint16_t* dob = p.dout + (int64_t)b * p.do_s[0] + (int64_t)h * p.do_s[1];
-#pragma unroll
-    for (int i = 0; i < QN; ++i) {
-      const int c = tid + 256 * i;
-      qst[i] = ld16(qhb + (int64_t)(q0 + c / QU) * EP + 8 * (c % QU));
-    }
-#pragma unroll
-    for (int i = 0; i < ON; ++i) {
-      const int c = tid + 256 * i, d0 = 8 * (c % OU);
-      ost[i] = d0 < D ? ld16(dob + (int64_t)min(q0 + c / OU, Nq - 1) * p.do_s[2] + d0) : zero4();
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < QN; ++i) {
-      const int c = tid + 256 * i, r = c / QU, u = c % QU;
-      *reinterpret_cast<u32x4*>(qt[buf] + r * EP + 8 * (u ^ tile_swz(QU, r))) = qst[i];
-    }
-#pragma unroll
-    for (int i = 0; i < ON; ++i) {
-      const int c = tid + 256 * i, r = c / OU, u = c % OU;
-      *reinterpret_cast<u32x4*>(dt[buf] + r * DV + 8 * (u ^ tile_swz(OU, r))) = ost[i];
-    }
-  };
-  if (nsteps > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
   for (int st = 0; st < nsteps; ++st) {
-    const int buf = st & 1;
+    const int buf = st % kSlots;
     int h, q0;
     step_at(st, h, q0);
-    if (st + 1 < nsteps) load_tile(st + 1);
-    const int bh = b * p.Hq + h;
-    const float* nlb = p.nl + (int64_t)bh * NqP;
-    const float* ndb = p.nd + (int64_t)bh * NqP;
+    // this thread's loads of step st landed (st + 1 may be in flight; wave 0 has one more per step)
+    if (st + 1 < nsteps) {
+      if (wave == 0) wait_vmcnt<NL + 1>();
+      else wait_vmcnt<NL>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    __syncthreads();                         // ... everyone's; and slot (st + 2) % kSlots was last read in step st - 1
+    if (st + 2 < nsteps) issue(st + 2);
     // -lse and -delta of the result rows (queries q0 + res_row(r, hf); padded rows give P = 0)
     f32x16 s, dp;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(nlb + q0 + 8 * q + 4 * hf);
-      const f32x4 c = *reinterpret_cast<const f32x4*>(ndb + q0 + 8 * q + 4 * hf);
+      const f32x4 a = *reinterpret_cast<const f32x4*>(&rt[buf][8 * q + 4 * hf]);
+      const f32x4 c = *reinterpret_cast<const f32x4*>(&rt[buf][32 + 8 * q + 4 * hf]);
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
         s[4 * q + x] = a[x];
@@ -333,20 +372,14 @@ __global__ __launch_bounds__(256) void wide_kv_kernel(FlashBwdParams p, float* w
     for (int g2 = 0; g2 < 2; ++g2) {
       const vec8 ap = as_vec8<vec8>(pack8w<T>(s, g2)), ads = as_vec8<vec8>(pack8w<T>(dp, g2));
 #pragma unroll
-      for (int db = 0; db < DBC; ++db) {
-        const int nb = ec * DBC + db;
+      for (int db = 0; db < DBC; ++db)
         dva[db] = T::mfma32(
-            ap, as_vec8<vec8>(lds_tr8(dt[buf], dO.lo_at(nb) + 16 * g2 * DV, dO.hi_at(nb) + 16 * g2 * DV)), dva[db]);
-      }
+            ap, as_vec8<vec8>(lds_tr8(dt[buf], dof[db].x + 16 * g2 * DV, dof[db].y + 16 * g2 * DV)), dva[db]);
 #pragma unroll
-      for (int eb = 0; eb < EBC; ++eb) {
-        const int nb = ec * EBC + eb;
+      for (int eb = 0; eb < EBC; ++eb)
         dka[eb] = T::mfma32(
-            ads, as_vec8<vec8>(lds_tr8(qt[buf], qo.lo_at(nb) + 16 * g2 * EP, qo.hi_at(nb) + 16 * g2 * EP)), dka[eb]);
-      }
+            ads, as_vec8<vec8>(lds_tr8(qt[buf], qof[eb].x + 16 * g2 * EP, qof[eb].y + 16 * g2 * EP)), dka[eb]);
     }
-    if (st + 1 < nsteps) store_tile(buf ^ 1);   // the other buffer's last reads were before the last barrier
-    __syncthreads();
   }
   // dV (lane = d column, registers = keys); the raw dK_hat chunk, times ln 2 (Q_hat carries log2 e)
   uint16_t* dvb = p.dv + (int64_t)b * p.dv_s[0] + (int64_t)hk * p.dv_s[1];
@@ -371,16 +404,16 @@ __global__ __launch_bounds__(256) void wide_kv_kernel(FlashBwdParams p, float* w
 // ---- backward: dQ_hat -------------------------------------------------------------------
 // One workgroup per (4 / CH blocks of 32 queries, batch * head); wave w takes query block w / CH
 // and column chunk w % CH of the accumulator.  The K_hat and V tiles of each 32-key step go
-// through LDS once for the four waves, double buffered.
+// straight from global memory into LDS once for the four waves, in three slots (two steps ahead).
 template <typename T, int EP, int DV, int CH>
 __global__ __launch_bounds__(256) void wide_q_kernel(FlashBwdParams p, float* wq) {
   constexpr int KS = EP / 16, DS = DV / 16, EBC = EP / 32 / CH, RB = 4 / CH;
-  constexpr int KU = EP / 8, VU = DV / 8, KN = 32 * KU / 256, VN = 32 * VU / 256;
+  constexpr int KU = EP / 8, VU = DV / 8, NL = 32 * (KU + VU) / 256;
   typedef typename T::vec8 vec8;
-  __shared__ __attribute__((aligned(16))) uint16_t kt[2][32 * EP];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[2][32 * DV];
+  __shared__ __attribute__((aligned(16))) uint16_t kt[kSlots][32 * EP];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[kSlots][32 * DV];
 
-  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, hf = lane >> 5;
+  const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lr = lane & 31, hf = lane >> 5;
   const int nqb = p.NqP / (32 * RB);
   const int ec = (tid >> 6) % CH;   // the wave's column chunk
   const int qb0 = 32 * RB * (nqb - 1 - (int)blockIdx.x % nqb), bh = (int)blockIdx.x / nqb;   // heaviest causal blocks first
@@ -389,6 +422,23 @@ __global__ __launch_bounds__(256) void wide_q_kernel(FlashBwdParams p, float* wq
   const int Nk = p.Nk, Nq = p.Nq, D = p.D;
   if (qb0 >= Nq) return;
   const int qi = q0 + lr;
+  int nkeys = min(((ci32*)p.kend)[b], Nk);
+  if (p.causal) nkeys = min(nkeys, qb0 + 32 * RB);   // the workgroup's last query block
+  const uint16_t* khb = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;   // rows padded to NkP
+  const uint16_t* vb = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
+  // tile t into slot t % kSlots: K_hat rows padded to NkP (no clamp); V rows past Nk repeat the
+  // last one and V units at or past D repeat the row's last unit (they meet zero dO columns)
+  auto issue = [&](int t) {
+    const int j0 = 32 * t, slot = t % kSlots;
+    const uint16_t* kp = khb + (int64_t)j0 * EP;
+    tile_fill<KU>(kt[slot], tid, wave, [&](int r, int u) { return kp + r * EP + 8 * u; });
+    tile_fill<VU>(vt[slot], tid, wave, [&](int r, int u) {
+      return vb + (int64_t)min(j0 + r, Nk - 1) * p.v_s[2] + min(8 * u, D - 8);
+    });
+  };
+  const int nt = (nkeys + 31) / 32;
+  if (nt > 0) issue(0);
+  if (nt > 1) issue(1);
 
   vec8 qreg[KS], doreg[DS];
   {
@@ -403,50 +453,21 @@ __global__ __launch_bounds__(256) void wide_q_kernel(FlashBwdParams p, float* wq
     }
   }
   const float nls = p.nl[(int64_t)bh * p.NqP + qi], nds = p.nd[(int64_t)bh * p.NqP + qi];
+  // the row loads as loads the compiler sees complete: no use of them in the loop waits on the
+  // tile loads in flight there
+  settle_vector_loads();
   f32x16 dqa[EBC];
 #pragma unroll
   for (int x = 0; x < EBC; ++x) dqa[x] = splat16(0.f);
-  int nkeys = min(((ci32*)p.kend)[b], Nk);
-  if (p.causal) nkeys = min(nkeys, qb0 + 32 * RB);   // the workgroup's last query block
-  const uint16_t* khb = p.kh + (int64_t)(b * p.Hk + hk) * p.NkP * EP;   // rows padded to NkP
-  const uint16_t* vb = p.v + (int64_t)b * p.v_s[0] + (int64_t)hk * p.v_s[1];
   cu64* mw = (cu64*)p.mwords + (int64_t)b * p.NW;
   const TileOffsets<KU> ko(lane);
   const TileOffsets<VU> vo(lane);
-  u32x4 kst[KN], vst[VN];
-  auto load_tile = [&](int j0) {
-#pragma unroll
-    for (int i = 0; i < KN; ++i) {
-      const int c = tid + 256 * i;
-      kst[i] = ld16(khb + (int64_t)(j0 + c / KU) * EP + 8 * (c % KU));
-    }
-#pragma unroll
-    for (int i = 0; i < VN; ++i) {
-      const int c = tid + 256 * i, d0 = 8 * (c % VU);
-      vst[i] = d0 < D ? ld16(vb + (int64_t)min(j0 + c / VU, Nk - 1) * p.v_s[2] + d0) : zero4();
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < KN; ++i) {
-      const int c = tid + 256 * i, r = c / KU, u = c % KU;
-      *reinterpret_cast<u32x4*>(kt[buf] + r * EP + 8 * (u ^ tile_swz(KU, r))) = kst[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VN; ++i) {
-      const int c = tid + 256 * i, r = c / VU, u = c % VU;
-      *reinterpret_cast<u32x4*>(vt[buf] + r * DV + 8 * (u ^ tile_swz(VU, r))) = vst[i];
-    }
-  };
-  const int nt = (nkeys + 31) / 32;
-  if (nt > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
   for (int t = 0; t < nt; ++t) {
-    const int buf = t & 1, j0 = 32 * t;
-    if (t + 1 < nt) load_tile(j0 + 32);
+    const int buf = t % kSlots, j0 = 32 * t;
+    if (t + 1 < nt) wait_vmcnt<NL>();   // this thread's loads of tile t landed (t + 1 may be in flight)
+    else wait_vmcnt<0>();
+    __syncthreads();                    // ... everyone's; and slot (t + 2) % kSlots was last read in step t - 1
+    if (t + 2 < nt) issue(t + 2);
     // S^T = K_hat Q_hat^T - lse and dP^T = V dO^T - delta (rows = keys, lane = query)
     f32x16 s = splat16(nls), dp = splat16(nds);
 #pragma unroll
@@ -479,8 +500,6 @@ __global__ __launch_bounds__(256) void wide_q_kernel(FlashBwdParams p, float* wq
             as_vec8<vec8>(lds_tr8(kt[buf], ko.lo_at(ec * EBC + eb) + 16 * g2 * EP, ko.hi_at(ec * EBC + eb) + 16 * g2 * EP)),
             bds, dqa[eb]);
     }
-    if (t + 1 < nt) store_tile(buf ^ 1);   // the other buffer's last reads were before the last barrier
-    __syncthreads();
   }
   // the raw dQ_hat chunk (rows = e, lane = query), times softmax_scale
   float* wqb = wq + ((int64_t)bh * p.NqP + qi) * EP;
