@@ -90,28 +90,6 @@ __device__ __forceinline__ u32x4 pack8(const f32x16& x, int g) {
   return w;
 }
 
-// Waits until at most n of this thread's vector loads are outstanding (n a compile-time count).
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(n >= 0 && n <= 15, "wait count");
-  if (n == 0) POPE_WAIT_VMCNT(0);
-  else if (n == 1) POPE_WAIT_VMCNT(1);
-  else if (n == 2) POPE_WAIT_VMCNT(2);
-  else if (n == 3) POPE_WAIT_VMCNT(3);
-  else if (n == 4) POPE_WAIT_VMCNT(4);
-  else if (n == 5) POPE_WAIT_VMCNT(5);
-  else if (n == 6) POPE_WAIT_VMCNT(6);
-  else if (n == 7) POPE_WAIT_VMCNT(7);
-  else if (n == 8) POPE_WAIT_VMCNT(8);
-  else if (n == 9) POPE_WAIT_VMCNT(9);
-  else if (n == 10) POPE_WAIT_VMCNT(10);
-  else if (n == 11) POPE_WAIT_VMCNT(11);
-  else if (n == 12) POPE_WAIT_VMCNT(12);
-  else if (n == 13) POPE_WAIT_VMCNT(13);
-  else if (n == 14) POPE_WAIT_VMCNT(14);
-  else if (n == 15) POPE_WAIT_VMCNT(15);
-}
-
 // ---------------------------------------------------------------------------
 // delta: 8 lanes per (batch * query head, padded query row), one 8-element chunk of O and dO
 // each (_bwd_preprocess, triton_pope_flash_attn.py:119-130).  Writes -lse * log2 e and

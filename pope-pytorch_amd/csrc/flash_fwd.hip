@@ -14,8 +14,9 @@
 //   own online-softmax state; group 1 hands (m, l, O) to group 0 through LDS at the end.
 // Staging
 //   K_hat and V tiles go straight from global memory into LDS (global_load_lds_dwordx4, no
-//   registers), into a ring of three stage slots: while pair t is consumed, pair t + 1 is
-//   resident and pair t + 2 is in flight.  Tiles are unpadded and XOR-swizzled (tile_swz).
+//   registers), into a ring of stage slots: while pair t is consumed, pair t + 1 is resident
+//   and pair t + 2 (four slots, where they fit the LDS: also pair t + 3) is in flight.  Tiles
+//   are unpadded and XOR-swizzled (tile_swz).
 // Per wave and tile
 //   S^T = K_hat Q_hat^T on v_mfma_f32_32x32x16: A = K_hat rows from LDS (lane = key), B = the
 //   wave's Q_hat rows held in registers (lane = query), so every query's scores sit in one
@@ -48,7 +49,6 @@ namespace {
 
 constexpr int kBM = 128;        // query rows per workgroup
 constexpr int kThreads = 512;   // 8 waves
-constexpr int kStages = 3;
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
@@ -65,9 +65,14 @@ struct FwdCfg {
   static constexpr int UNITS = STAGE / 16;
   static constexpr int KUNITS = 2 * KTILE / 8;
   static constexpr int LPT = (UNITS + kThreads - 1) / kThreads;       // direct loads per thread
+  // loads per pair of the last wave (the fewest: the last load of a pair can be partial)
+  static constexpr int LMIN = (UNITS - (kThreads - 64) + kThreads - 1) / kThreads;
+  // stage slots: pair t's V and pair t + 1's K_hat in use, SLOTS - 2 pairs loading ahead (four
+  // where they fit the LDS, except for 128-wide V rows, whose registers the deeper ring spills)
+  static constexpr int SLOTS = 4 * STAGE <= 160 * 1024 && DV < 128 ? 4 : 3;
   static constexpr int MS = 3 + 16 * NDB;                             // floats per lane in the merge
   static constexpr int MERGE = 4 * 64 * MS * 4;
-  static constexpr int LDS = kStages * STAGE > MERGE ? kStages * STAGE : MERGE;
+  static constexpr int LDS = SLOTS * STAGE > MERGE ? SLOTS * STAGE : MERGE;
   static_assert(KUNITS % 64 == 0 && UNITS % 64 == 0, "loads must split at wave boundaries");
   static_assert(LDS <= 160 * 1024, "LDS budget");
 };
@@ -136,7 +141,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   }
   const int v_last = (Nk - 1) * vs2 + D - 8;   // start of the last chunk of the last row
   auto issue = [&](int pr) {
-    char* slot = smem + (pr % kStages) * C::STAGE;
+    char* slot = smem + (pr % C::SLOTS) * C::STAGE;
     const int j0 = pr * 2 * BN;
     const uint16_t* kp = khg + j0 * EP;   // K_hat rows are padded to NkP: no clamp
     const int vrow0 = j0 * vs2;
@@ -172,10 +177,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   bool m_set = false;
   f32x16 sacc[KB];
   auto kh_tile = [&](int pr) -> const uint16_t* {
-    return reinterpret_cast<const uint16_t*>(smem + (pr % kStages) * C::STAGE) + grp * C::KTILE;
+    return reinterpret_cast<const uint16_t*>(smem + (pr % C::SLOTS) * C::STAGE) + grp * C::KTILE;
   };
   auto v_tile = [&](int pr) -> const uint16_t* {
-    return reinterpret_cast<const uint16_t*>(smem + (pr % kStages) * C::STAGE) + 2 * C::KTILE + grp * C::VTILE;
+    return reinterpret_cast<const uint16_t*>(smem + (pr % C::SLOTS) * C::STAGE) + 2 * C::KTILE + grp * C::VTILE;
   };
   // Visibility of the group's tile of pair pr: true when every key is visible to every row of
   // the wave (no per-element mask needed).
@@ -364,17 +369,14 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
   // accumulators; then the score MFMAs of tile t + 1 interleaved with the exponentials of
   // tile t, and the P V MFMAs of tile t interleaved with the row maximum of tile t + 1.
   if (npair > 0) {
+    // pairs 0 .. SLOTS - 2 in flight; wait for pair 0 (every wave issues at least LMIN loads per
+    // pair, so allowing that many per later pair never lets one of pair 0's through)
     issue(0);
-    if (npair > 1) {
-      issue(1);
-      if (C::LPT == 3) POPE_WAIT_VMCNT(3);
-      else if (C::LPT == 4) POPE_WAIT_VMCNT(4);
-      else if (C::LPT == 5) POPE_WAIT_VMCNT(5);
-      else if (C::LPT == 6) POPE_WAIT_VMCNT(6);
-      else POPE_WAIT_VMCNT(0);
-    } else {
-      POPE_WAIT_VMCNT(0);
-    }
+    if (npair > 1) issue(1);
+    if (C::SLOTS > 3 && npair > 2) issue(2);
+    if (C::SLOTS > 3 && npair > 2) wait_vmcnt<2 * C::LMIN>();
+    else if (npair > 1) wait_vmcnt<C::LMIN>();
+    else wait_vmcnt<0>();
     __syncthreads();
     uint64_t mb0;
     const bool full0 = tile_full(0, mb0);
@@ -390,9 +392,11 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashFwdParams p
       u32x4 pw[2 * KB];
       uint64_t mb;
       const bool full = tile_full(t + 1, mb);
-      POPE_WAIT_VMCNT(0);   // this thread's loads of pair t + 1 landed
+      // this thread's loads of pair t + 1 landed (with four slots pair t + 2 may be in flight)
+      if (C::SLOTS > 3 && t + 2 < npair) wait_vmcnt<C::LMIN>();
+      else wait_vmcnt<0>();
       __syncthreads();      // ... everyone's; and pair t - 1's slot is free
-      if (t + 2 < npair) issue(t + 2);
+      if (t + C::SLOTS - 1 < npair) issue(t + C::SLOTS - 1);
       // keep the exponentials of tile t below the barrier, next to the MFMAs they overlap
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) asm volatile("" : "+v"(cur[kb]));

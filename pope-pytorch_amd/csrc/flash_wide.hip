@@ -67,13 +67,6 @@ __device__ __forceinline__ int res_row(int r, int hf) { return 8 * (r >> 2) + 4 
 // t + 2 load, so each tile has two steps of compute to arrive in.
 constexpr int kSlots = 3;
 
-// Waits until at most N of this thread's vector memory loads are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 // Transpose-read offsets (lo, hi) of column block nb of a tile, nb known only at run time: the
 // entry of the swizzle period is picked by selects rather than by indexing the offset arrays,
 // which would place them in scratch memory (vector loads that would wait on the tile loads).

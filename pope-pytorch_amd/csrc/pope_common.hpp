@@ -228,6 +228,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Waits until at most n of this thread's vector memory loads are outstanding.
 #define POPE_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
 
+// The same with the count as a template argument.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // Waits for every outstanding vector memory load, as an instruction the compiler's own wait
 // insertion accounts for: registers loaded before it count as ready afterwards, so no later
 // use of them (inside a loop that also has direct-to-LDS loads in flight) adds a vmcnt(0).
