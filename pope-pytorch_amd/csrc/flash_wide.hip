@@ -595,9 +595,11 @@ hipError_t fwd_t(const FlashFwdParams& p, hipStream_t s) {
   return launch_named("flash_wide_fwd", wide_fwd_kernel<T, EP, DV>, dim3((p.NqP / 128) * p.B * p.Hq), dim3(256), s, p);
 }
 
-// Column chunks per row block: as few as the registers allow (each chunk recomputes the scores).
+// Column chunks per row block: as few as the registers allow without spilling (each chunk
+// recomputes the scores); the direct LDS tile loads freed the registers for two dK/dV chunks at
+// 384 features.
 template <int EP>
-constexpr int kv_chunks() { return EP <= 256 ? 2 : 4; }
+constexpr int kv_chunks() { return EP <= 384 ? 2 : 4; }
 template <int EP>
 constexpr int q_chunks() { return EP <= 256 ? 1 : EP <= 384 ? 2 : 4; }
 
