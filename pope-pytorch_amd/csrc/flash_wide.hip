@@ -595,13 +595,13 @@ hipError_t fwd_t(const FlashFwdParams& p, hipStream_t s) {
   return launch_named("flash_wide_fwd", wide_fwd_kernel<T, EP, DV>, dim3((p.NqP / 128) * p.B * p.Hq), dim3(256), s, p);
 }
 
-// Column chunks per row block: as few as the registers allow without spilling (each chunk
-// recomputes the scores); the direct LDS tile loads freed the registers for two dK/dV chunks at
-// 384 features.
+// Column chunks per row block (each chunk recomputes the scores), as few as measured fastest: the
+// direct LDS tile loads freed the registers for two dK/dV chunks at 384 features and two dQ
+// chunks at 512 (the latter spills a few address registers, which still beats four chunks).
 template <int EP>
 constexpr int kv_chunks() { return EP <= 384 ? 2 : 4; }
 template <int EP>
-constexpr int q_chunks() { return EP <= 256 ? 1 : EP <= 384 ? 2 : 4; }
+constexpr int q_chunks() { return EP <= 256 ? 1 : 2; }
 
 template <typename T, int EP, int DV>
 hipError_t bwd_t(const FlashBwdParams& p, float* wk, float* wq, hipStream_t s) {
