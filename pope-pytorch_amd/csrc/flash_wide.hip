@@ -595,11 +595,12 @@ hipError_t fwd_t(const FlashFwdParams& p, hipStream_t s) {
   return launch_named("flash_wide_fwd", wide_fwd_kernel<T, EP, DV>, dim3((p.NqP / 128) * p.B * p.Hq), dim3(256), s, p);
 }
 
-// Column chunks per row block (each chunk recomputes the scores), as few as measured fastest: the
-// direct LDS tile loads freed the registers for two dK/dV chunks at 384 features and two dQ
-// chunks at 512 (the latter spills a few address registers, which still beats four chunks).
+// Column chunks per row block (each chunk recomputes the scores), as few as measured fastest: with
+// the tiles loaded straight into LDS, one dK/dV chunk at 256 features and two at 384 / 512, one
+// dQ chunk at 256 and two at 384 / 512 (some of these spill a few registers, which still beats
+// recomputing the scores more often).
 template <int EP>
-constexpr int kv_chunks() { return EP <= 384 ? 2 : 4; }
+constexpr int kv_chunks() { return EP <= 256 ? 1 : 2; }
 template <int EP>
 constexpr int q_chunks() { return EP <= 256 ? 1 : 2; }
 
