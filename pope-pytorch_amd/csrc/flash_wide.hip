@@ -509,7 +509,24 @@ __global__ __launch_bounds__(256) void wide_q_kernel(FlashBwdParams p, float* wq
 // F[q_off + i] - bias, the bias on the query side as in the preparation):
 //   dx = sigmoid(x) (cos U_c + sin U_s),  dphase = softplus(x) (cos U_s - sin U_c)
 // and pass-through dims dx = U.  Key phase derivatives also sum into dbias (per block in LDS,
-// then one atomic per dim).
+// then one atomic per dim).  A thread takes 4 consecutive dims per step (D and R are multiples of
+// 8; the rows of q, k, dq, dk are 16-byte aligned): 16-byte loads of U, 8-byte loads and stores
+// of the bf16 / fp16 rows.
+template <typename T>
+__device__ __forceinline__ void load4(const uint16_t* p, float* x) {
+  const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+  x[0] = T::to_float((uint16_t)(w[0] & 0xffffu));
+  x[1] = T::to_float((uint16_t)(w[0] >> 16));
+  x[2] = T::to_float((uint16_t)(w[1] & 0xffffu));
+  x[3] = T::to_float((uint16_t)(w[1] >> 16));
+}
+template <typename T>
+__device__ __forceinline__ void store4(uint16_t* p, const float* g) {
+  u32x2 w;
+  w[0] = T::pack2(g[0], g[1]);
+  w[1] = T::pack2(g[2], g[3]);
+  *reinterpret_cast<u32x2*>(p) = w;
+}
 template <typename T>
 __global__ __launch_bounds__(256) void wide_chain_kernel(FlashBwdParams p, const float* wk, const float* wq, int nk) {
   __shared__ float dsum[256];
@@ -528,27 +545,36 @@ __global__ __launch_bounds__(256) void wide_chain_kernel(FlashBwdParams p, const
     float* dfb = p.dfreqs ? p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)hk * p.df_s[1] : nullptr;
     float* kpb = p.kpart ? p.kpart + (int64_t)bhk * p.Nk * R : nullptr;
     const float* wrow = wk + (int64_t)bhk * p.NkP * EP;
-    for (int it = tid; it < 32 * D; it += 256) {
-      const int key = k0 + it / D, d = it % D;
+    const int D4 = D / 4;
+    for (int it = tid; it < 32 * D4; it += 256) {
+      const int key = k0 + it / D4, d = 4 * (it % D4);
       if (key >= p.Nk) continue;
       const float* u = wrow + (int64_t)key * EP;
-      float g;
-      if (d < R) {
-        const float x = T::to_float(kb[(int64_t)key * p.k_s[2] + d]);
-        const float2 cs = tb[(int64_t)key * R + d];
-        const float uc = u[d], us = u[R + d];
-        g = sigmoid_f(x) * (cs.x * uc + cs.y * us);
-        const float dpsi = softplus_f(x) * (cs.x * us - cs.y * uc);
-        if (kpb) {
-          kpb[(int64_t)key * R + d] = dpsi;
-        } else {
-          if (dfb) atomicAdd(dfb + (int64_t)key * p.df_s[2] + d, dpsi);
-          if (p.dbias) atomicAdd(&dsum[d], dpsi);
+      float g[4];
+      if (d < R) {   // R % 4 == 0: all four dims rotated
+        float x[4];
+        load4<T>(kb + (int64_t)key * p.k_s[2] + d, x);
+        const float4 c01 = *reinterpret_cast<const float4*>(tb + (int64_t)key * R + d);
+        const float4 c23 = *reinterpret_cast<const float4*>(tb + (int64_t)key * R + d + 2);
+        const float4 uc = *reinterpret_cast<const float4*>(u + d), us = *reinterpret_cast<const float4*>(u + R + d);
+        const float cs[4] = {c01.x, c01.z, c23.x, c23.z}, sn[4] = {c01.y, c01.w, c23.y, c23.w};
+        const float ucv[4] = {uc.x, uc.y, uc.z, uc.w}, usv[4] = {us.x, us.y, us.z, us.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          g[t] = sigmoid_f(x[t]) * (cs[t] * ucv[t] + sn[t] * usv[t]);
+          const float dpsi = softplus_f(x[t]) * (cs[t] * usv[t] - sn[t] * ucv[t]);
+          if (kpb) {
+            kpb[(int64_t)key * R + d + t] = dpsi;
+          } else {
+            if (dfb) atomicAdd(dfb + (int64_t)key * p.df_s[2] + d + t, dpsi);
+            if (p.dbias) atomicAdd(&dsum[d + t], dpsi);
+          }
         }
       } else {
-        g = u[R + d];
+        const float4 us = *reinterpret_cast<const float4*>(u + R + d);
+        g[0] = us.x; g[1] = us.y; g[2] = us.z; g[3] = us.w;
       }
-      dkb[(int64_t)key * p.dk_s[2] + d] = T::bits(g);
+      store4<T>(dkb + (int64_t)key * p.dk_s[2] + d, g);
     }
     if (p.dbias && !kpb) {
       __syncthreads();
@@ -568,25 +594,32 @@ __global__ __launch_bounds__(256) void wide_chain_kernel(FlashBwdParams p, const
   float* dfb = p.dfreqs ? p.dfreqs + (int64_t)b * p.df_s[0] + (int64_t)h * p.df_s[1] : nullptr;
   float* qpb = p.qpart && p.dfreqs ? p.qpart + (int64_t)bh * p.Nq * R : nullptr;
   const float* wrow = wq + (int64_t)bh * p.NqP * EP;
-  for (int it = tid; it < 32 * D; it += 256) {
-    const int i = q0 + it / D, d = it % D;
+  const int D4 = D / 4;
+  for (int it = tid; it < 32 * D4; it += 256) {
+    const int i = q0 + it / D4, d = 4 * (it % D4);
     if (i >= p.Nq) continue;
     const float* u = wrow + (int64_t)i * EP;
-    float g;
-    if (d < R) {
-      const float x = T::to_float(qb[(int64_t)i * p.q_s[2] + d]);
-      // cos / sin(F[q_off + i] - bias) from the tables of F and of the bias
-      const float2 tf = tq[(int64_t)(q_off + i) * R + d], tbv = bq[d];
-      const float cs = fmaf(tf.x, tbv.x, tf.y * tbv.y), sn = fmaf(tf.y, tbv.x, -tf.x * tbv.y);
-      const float uc = u[d], us = u[R + d];
-      g = sigmoid_f(x) * (cs * uc + sn * us);
-      const float dph = softplus_f(x) * (cs * us - sn * uc);
-      if (qpb) qpb[(int64_t)i * R + d] = dph;
-      else if (dfb) atomicAdd(dfb + (int64_t)(q_off + i) * p.df_s[2] + d, dph);
+    float g[4];
+    if (d < R) {   // R % 4 == 0: all four dims rotated
+      float x[4];
+      load4<T>(qb + (int64_t)i * p.q_s[2] + d, x);
+      const float4 uc = *reinterpret_cast<const float4*>(u + d), us = *reinterpret_cast<const float4*>(u + R + d);
+      const float ucv[4] = {uc.x, uc.y, uc.z, uc.w}, usv[4] = {us.x, us.y, us.z, us.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        // cos / sin(F[q_off + i] - bias) from the tables of F and of the bias
+        const float2 tf = tq[(int64_t)(q_off + i) * R + d + t], tbv = bq[d + t];
+        const float cs = fmaf(tf.x, tbv.x, tf.y * tbv.y), sn = fmaf(tf.y, tbv.x, -tf.x * tbv.y);
+        g[t] = sigmoid_f(x[t]) * (cs * ucv[t] + sn * usv[t]);
+        const float dph = softplus_f(x[t]) * (cs * usv[t] - sn * ucv[t]);
+        if (qpb) qpb[(int64_t)i * R + d + t] = dph;
+        else if (dfb) atomicAdd(dfb + (int64_t)(q_off + i) * p.df_s[2] + d + t, dph);
+      }
     } else {
-      g = u[R + d];
+      const float4 us = *reinterpret_cast<const float4*>(u + R + d);
+      g[0] = us.x; g[1] = us.y; g[2] = us.z; g[3] = us.w;
     }
-    dqb[(int64_t)i * p.dq_s[2] + d] = T::bits(g);
+    store4<T>(dqb + (int64_t)i * p.dq_s[2] + d, g);
   }
 }
 
