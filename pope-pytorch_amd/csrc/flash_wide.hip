@@ -63,6 +63,10 @@ __device__ __forceinline__ f32x16 splat16(float x) {
 // Row offset within a 32-row block of register r of a 32x32 MFMA result in lane half hf.
 __device__ __forceinline__ int res_row(int r, int hf) { return 8 * (r >> 2) + 4 * hf + (r & 3); }
 
+// Growth of a row's running max (log2 units) that the forward absorbs without rescaling its
+// accumulators: probabilities reach at most 2^kLazyMax.
+constexpr float kLazyMax = 8.f;
+
 // LDS slots of the streamed tiles: tile t is computed from slot t % kSlots while tiles t + 1 and
 // t + 2 load, so each tile has two steps of compute to arrive in.
 constexpr int kSlots = 3;
@@ -179,9 +183,28 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(FlashFwdParams p) {
       mt = fmaxf(mt, s[r]);
     }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float mn = fmaxf(m, mt);
-    const float mu = mn == -INFINITY ? 0.f : mn;
-    const float alpha = __builtin_amdgcn_exp2f(m - mu);
+    float alpha = 1.f;
+    if constexpr (EP < 512) {
+      // lazy rescale: a row's reference max m moves only when the tile's max exceeds it by more
+      // than kLazyMax (log2 units), so the probabilities stay below 2^kLazyMax and most steps skip
+      // rescaling the O accumulators (the branch is taken when any row of the wave moves).  At
+      // 512 features the branch costs more than it saves: the rescale stays in every step.
+      const bool grow = mt > m + kLazyMax;
+      if (__ballot(grow)) {
+        const float mn = grow ? mt : m;
+        alpha = __builtin_amdgcn_exp2f(m - (mn == -INFINITY ? 0.f : mn));
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+        m = mn;   // l takes alpha below
+      }
+    } else {
+      const float mn = fmaxf(m, mt);
+      alpha = __builtin_amdgcn_exp2f(m - (mn == -INFINITY ? 0.f : mn));
+      m = mn;
+    }
+    const float mu = m == -INFINITY ? 0.f : m;
     u32x4 pw[2];
     float ls = 0.f;
 #pragma unroll
@@ -194,11 +217,12 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(FlashFwdParams p) {
         ls = T::dot2(w, ones, ls);   // the row sum of the probabilities the products use
       }
     l = l * alpha + ls + __shfl_xor(ls, 32, 64);
-    m = mn;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
+      if constexpr (EP >= 512) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+      }
 #pragma unroll
       for (int g = 0; g < 2; ++g)
         oacc[db] = T::mfma32(as_vec8<vec8>(lds_tr8(vt[buf], vo.lo_at(db) + 16 * g * DV, vo.hi_at(db) + 16 * g * DV)),
